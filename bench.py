@@ -1,0 +1,284 @@
+#!/usr/bin/env python3
+"""Benchmark of the W4A16 decode GEMV on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 1000] [--warmup 50] [--configs all|c0,c3,...]
+
+Metric: HBM read GB/s and % of the measured read roof of the
+W4A16 GEMV at M=4096, K=4096, B=1, with p50 latency. One "step" is one GEMV
+launch over the resident packed weights, preceded (outside the timed events)
+by a 1 GiB read-only sweep that evicts L2 and the Infinity Cache, so every
+step reads its weights from HBM. `value` = algorithmic bytes / p50 step time.
+
+Also reported on the same line: the read roof, the empty-kernel event floor,
+every kernel variant at the headline shape, the other four configurations,
+a roofline object for the headline kernel, and the CPU baseline (the oracle's
+restatement of the reference's CPU path, timed on this host).
+
+Prints exactly one JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "decode-kernel_amd"))
+sys.path.insert(0, str(REPO))
+
+METRIC = "HBM read GB/s & % of measured read roof, W4A16 GEMV 4096x4096 B=1; p50 us"
+
+# name -> (M, K, batches, variants timed). The headline is c0 B=1 with the
+# default op (v5). Seeds follow the config index.
+CONFIGS = {
+    "c0": (4096, 4096, [1], ["v0", "v1", "v1_wpr2", "v1_wpr4", "v2", "v3", "v4", "v5", "reuse"]),
+    "c1": (11008, 4096, [1], ["v5", "v4", "reuse"]),
+    "c2": (4096, 11008, [1], ["v5", "v4", "reuse"]),
+    "c3": (4096, 4096, [1, 2, 4, 8, 16], ["reuse", "v5", "v4"]),
+    "c4a": (28672, 8192, [1], ["v5", "v4", "reuse"]),
+    "c4b": (8192, 28672, [1], ["v5", "v4", "reuse"]),
+}
+VARIANTS = {
+    "v0": dict(version=0), "v1": dict(version=1), "v1_wpr2": dict(version=1, warps_per_row=2),
+    "v1_wpr4": dict(version=1, warps_per_row=4), "v2": dict(version=2), "v3": dict(version=3),
+    "v4": dict(version=4, split_k=4), "v5": dict(version=5),
+    "reuse": dict(version=5, reuse_weights=True),
+}
+EXPECTED_STAMP = {"v0": 0, "v1": 1, "v1_wpr2": 12, "v1_wpr4": 14, "v2": 2, "v3": 3, "v4": 4,
+                  "v5": 5, "reuse": 15}
+PROFILE_TRAFFIC = REPO / "profiles" / "traffic_c0_v5.json"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--configs", default="all",
+                    help="comma list of c0,c1,c2,c3,c4a,c4b or 'all' (c0 is always run)")
+    ap.add_argument("--other-steps", type=int, default=200,
+                    help="timed steps per variant outside the headline")
+    ap.add_argument("--flush", choices=["read", "write", "none"], default="read")
+    ap.add_argument("--flush-bytes", type=int, default=1 << 30)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="budget of the CPU baseline sample")
+    ap.add_argument("--out", type=Path, default=None, help="also write the full JSON here")
+    return ap.parse_args()
+
+
+def make_inputs(m, k, batch, seed):
+    """Synthetic inputs: W ~ N(0, 0.02) fp32, x ~ N(0,1) fp16 (PCG64), quantized
+    on the CPU by the package's quantizer, then copied to HBM."""
+    import torch
+
+    from decode_kernel.quantize import quantize_and_pack
+    from oracle.oracle import make_case
+
+    w, x = make_case(m, k, batch, seed)
+    packed, scales = quantize_and_pack(torch.from_numpy(w))
+    del w
+    return (packed.cuda(), scales.cuda(), torch.from_numpy(x).cuda(), packed, scales, x)
+
+
+def bench_variant(ext, packed, scales, x, variant, warmup, iters, flush):
+    from decode_kernel import gemv
+    from dk_bench.common import bytes_moved_w4, flop_gemv, time_gpu
+
+    kw = VARIANTS[variant]
+
+    def fn():
+        gemv(packed, scales, x, **kw)
+
+    fn()
+    stamp = int(ext.last_kernel_stamp())
+    if stamp != EXPECTED_STAMP[variant]:
+        raise RuntimeError(f"{variant}: dispatch stamp {stamp}, expected {EXPECTED_STAMP[variant]}")
+    st = time_gpu(fn, warmup=warmup, iters=iters, flush=flush)
+    m, k, b = packed.shape[0], packed.shape[1] * 8, x.shape[0]
+    moved = bytes_moved_w4(m, k, b)
+    return {
+        "impl": variant, "stamp": stamp, "bytes_moved": moved,
+        "gbps": moved / (st["median_us"] * 1e3),
+        "gbps_mean": moved / (st["mean_us"] * 1e3),
+        "tflops": flop_gemv(m, k, b) / (st["median_us"] * 1e-6) / 1e12,
+        **st,
+    }
+
+
+def cpu_baseline(packed, scales, x, budget_s):
+    """The oracle's numpy restatement of reference.py:17-26 (unpack, fp32
+    dequant, fp32 GEMM) on this host, for a bounded number of calls."""
+    import numpy as np
+
+    from dk_bench.common import bytes_moved_w4
+    from oracle import oracle
+
+    p, s, xv = packed.numpy(), scales.numpy(), np.asarray(x)
+    oracle.linear_fp32(xv, p, s)  # warm BLAS and page in
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end and len(times) < 200:
+        t0 = time.perf_counter_ns()
+        oracle.linear_fp32(xv, p, s)
+        times.append((time.perf_counter_ns() - t0) / 1e3)
+    times.sort()
+    med = times[len(times) // 2]
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas_threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:
+        blas_threads = 1
+    m, k, b = p.shape[0], p.shape[1] * 8, xv.shape[0]
+    moved = bytes_moved_w4(m, k, b)
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": moved / (med * 1e3), "unit": "GB/s", "cores": int(blas_threads), "kind": "port",
+        "sample": (f"c0 M={m} K={k} B={b}: {len(times)} calls of oracle.linear_fp32 "
+                   f"(numpy unpack + fp32 dequant single-threaded, OpenBLAS sgemv with "
+                   f"{blas_threads} threads), median of ~{budget_s:.0f} s"),
+        "p50_us": med, "iqr_us": times[(3 * len(times)) // 4] - times[len(times) // 4],
+        "calls": len(times), "host_cpus": len(os.sched_getaffinity(0)), "cpu_model": cpu_model,
+    }
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE "
+              f"{world}). The W4A16 GEMV has no multi-GPU path in this build: rows would shard "
+              f"across GPUs with no communication beyond an optional all-gather of y.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    from decode_kernel import _cuda  # the HIP extension; no fallback exists
+    from dk_bench.ceilings import measure_event_floor, measure_read
+    from dk_bench.common import MI355X_HBM_PEAK_GBPS, Flush, meta_dict
+    from oracle import oracle
+
+    wanted = list(CONFIGS) if args.configs == "all" else ["c0"] + [
+        c for c in args.configs.split(",") if c and c != "c0"]
+    for c in wanted:
+        if c not in CONFIGS:
+            raise SystemExit(f"unknown config {c}")
+
+    log("[bench] read roof (1 GiB STREAM read)")
+    roof = measure_read(1 << 30)
+    floor = measure_event_floor()
+    flush = Flush(args.flush_bytes, args.flush)
+    log(f"[bench] read roof {roof['gbps']:.1f} GB/s, event floor p50 {floor['median_us']:.2f} us")
+
+    results = {}
+    headline = None
+    cpu = None
+    for ci, name in enumerate(CONFIGS):
+        if name not in wanted:
+            continue
+        m, k, batches, variants = CONFIGS[name]
+        for b in batches:
+            log(f"[bench] {name} M={m} K={k} B={b}")
+            pd, sd, xd, p_cpu, s_cpu, x_cpu = make_inputs(m, k, b, seed=1000 + ci)
+            if name == "c0":
+                y = _cuda.w4a16_gemv(pd, sd, xd)
+                err = oracle.max_abs_err(y.float().cpu().numpy(),
+                                         oracle.linear_f64(x_cpu, p_cpu.numpy(), s_cpu.numpy()))
+                if not err < 1e-2:
+                    raise RuntimeError(f"headline kernel fails the 1e-2 gate: {err}")
+            rows = []
+            for v in variants:
+                iters = args.steps if (name == "c0" and v == "v5") else args.other_steps
+                warm = args.warmup if (name == "c0" and v == "v5") else min(args.warmup, 20)
+                if v == "v0" and name != "c0":
+                    continue
+                r = bench_variant(_cuda, pd, sd, xd, v, warm, iters, flush)
+                r["pct_of_read_roof"] = 100.0 * r["gbps"] / roof["gbps"]
+                rows.append(r)
+                log(f"   {v:8s} p50 {r['median_us']:8.2f} us  {r['gbps']:8.1f} GB/s  "
+                    f"{r['pct_of_read_roof']:5.1f}% of read roof")
+            results[f"{name}_B{b}"] = {"M": m, "K": k, "batch": b, "kernels": rows}
+            if name == "c0":
+                headline = next(r for r in rows if r["impl"] == "v5")
+                if not args.no_cpu_baseline:
+                    log(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)")
+                    cpu = cpu_baseline(p_cpu, s_cpu, x_cpu, args.cpu_seconds)
+            del pd, sd, xd, p_cpu, s_cpu, x_cpu
+            torch.cuda.empty_cache()
+
+    traffic = None
+    if PROFILE_TRAFFIC.exists():
+        try:
+            traffic = json.loads(PROFILE_TRAFFIC.read_text()).get("hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+    achieved = headline["bytes_moved"] / (headline["mean_us"] * 1e3)
+    line = {
+        "metric": METRIC,
+        "value": headline["gbps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": headline["median_us"] / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "w4a16 (int4 weights, fp16 activations, fp32 accumulate)",
+        "data": "synthetic: W~N(0,0.02) fp32 quantized to int4 group 128, x~N(0,1) fp16, PCG64 seeds",
+        "config": {"workload": "c0: W4A16 GEMV M=4096 K=4096 B=1 group 128 (BASELINE configs[0])",
+                   "M": 4096, "K": 4096, "batch": 1, "group_size": 128, "kernel": "v5",
+                   "stamp": headline["stamp"], "parallelism": "single GPU"},
+        "p50_us": headline["median_us"],
+        "iqr_us": headline["iqr_us"],
+        "pct_of_read_roof": 100.0 * headline["gbps"] / roof["gbps"],
+        "read_roof_gbps": roof["gbps"],
+        "event_floor_p50_us": floor["median_us"],
+        "flush": flush.describe(),
+        "roofline": {
+            "bound": "hbm", "achieved": achieved, "peak": MI355X_HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": achieved / MI355X_HBM_PEAK_GBPS, "traffic": traffic,
+            "kernel": "dk::gemv_v5<4,2,1,false>", "mean_us": headline["mean_us"],
+            "algorithmic_bytes": headline["bytes_moved"],
+        },
+        "cpu_baseline": cpu,
+        "configs": {
+            key: {"M": r["M"], "K": r["K"], "batch": r["batch"],
+                  "kernels": {row["impl"]: {"p50_us": round(row["median_us"], 3),
+                                            "iqr_us": round(row["iqr_us"], 3),
+                                            "gbps": round(row["gbps"], 1),
+                                            "pct_read_roof": round(row["pct_of_read_roof"], 2)}
+                              for row in r["kernels"]}}
+            for key, r in results.items()
+        },
+    }
+    if args.out:
+        full = {"line": line, "meta": meta_dict(), "read_roof": roof, "event_floor": floor,
+                "results": results}
+        args.out.parent.mkdir(parents=True, exist_ok=True)
+        args.out.write_text(json.dumps(full, indent=2) + "\n")
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

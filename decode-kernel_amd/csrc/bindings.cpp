@@ -1,0 +1,177 @@
+// PyTorch-ROCm extension `decode_kernel._cuda` over the C ABI in
+// include/decode_kernel/dk_gemv.h.
+//
+// Same Python surface, argument names, defaults and validation messages as
+// the reference binding (csrc/bindings.cpp:10-129). Differences:
+//   * every C-ABI status is checked and raised as RuntimeError (the reference
+//     printed launch errors and returned garbage, csrc/gemv_w4a16.cu:9-16);
+//   * work is issued on the current HIP stream of the tensors' device under a
+//     device guard (the reference assumed the current device);
+//   * the split-K workspace comes from torch's caching allocator without a
+//     memset (the reference used torch::zeros, csrc/bindings.cpp:65-68).
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/extension.h>
+
+#include <cstdint>
+
+#include "decode_kernel/dk_gemv.h"
+
+namespace {
+
+constexpr int64_t kGroupSize = DK_GROUP_SIZE;
+constexpr int64_t kNibblesPerWord = DK_NIBBLES_PER_WORD;
+
+hipStream_t current_stream(const torch::Tensor& t) {
+  return c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+void check_status(int rc, const char* what) {
+  TORCH_CHECK(rc == DK_OK, what, " failed (status ", rc, "): ", dk_last_error());
+}
+
+// Reference: csrc/bindings.cpp:10-33.
+void check_gemv_inputs(const torch::Tensor& packed, const torch::Tensor& scales,
+                       const torch::Tensor& x) {
+  TORCH_CHECK(packed.is_cuda() && scales.is_cuda() && x.is_cuda(),
+              "packed, scales, and x must be CUDA tensors");
+  TORCH_CHECK(packed.device() == x.device() && scales.device() == x.device(),
+              "packed, scales, and x must be on the same device");
+  TORCH_CHECK(packed.scalar_type() == torch::kInt32, "packed must be int32 (uint32 bit pattern)");
+  TORCH_CHECK(scales.scalar_type() == torch::kFloat16, "scales must be fp16");
+  TORCH_CHECK(x.scalar_type() == torch::kFloat16, "x must be fp16");
+  TORCH_CHECK(packed.dim() == 2 && scales.dim() == 2 && x.dim() == 2,
+              "packed [M,K/8], scales [M,K/128], x [B,K]");
+  TORCH_CHECK(packed.is_contiguous() && scales.is_contiguous() && x.is_contiguous(),
+              "packed, scales, and x must be contiguous");
+  const int64_t M = packed.size(0);
+  const int64_t K = packed.size(1) * kNibblesPerWord;
+  TORCH_CHECK(K % kGroupSize == 0, "K must be divisible by group size 128");
+  TORCH_CHECK(scales.size(0) == M && scales.size(1) == K / kGroupSize,
+              "scales shape must be [M, K/128]");
+  TORCH_CHECK(x.size(1) == K, "x.shape[1] must equal K");
+  TORCH_CHECK(M <= INT32_MAX && K <= INT32_MAX && x.size(0) <= INT32_MAX,
+              "M, K and B must fit in int32");
+}
+
+}  // namespace
+
+// Reference: csrc/bindings.cpp:37-78.
+torch::Tensor w4a16_gemv(torch::Tensor packed, torch::Tensor scales, torch::Tensor x, int version,
+                         int split_k, bool reuse_weights, int warps_per_row) {
+  check_gemv_inputs(packed, scales, x);
+  TORCH_CHECK(version >= 0 && version <= 5, "version must be 0..5");
+  TORCH_CHECK(split_k >= 1 && split_k <= 32, "split_k must be in [1, 32]");
+  TORCH_CHECK(warps_per_row >= 1 && warps_per_row <= 8, "warps_per_row must be in [1, 8]");
+  if (warps_per_row > 1) {
+    TORCH_CHECK(version == 1 && !reuse_weights,
+                "warps_per_row > 1 is implemented for streaming v1 only");
+  }
+
+  const int M = static_cast<int>(packed.size(0));
+  const int K = static_cast<int>(packed.size(1) * kNibblesPerWord);
+  const int B = static_cast<int>(x.size(0));
+
+  c10::DeviceGuard guard(x.device());
+  auto y = torch::empty({B, M}, x.options());
+  if (K == 0) return y.zero_();  // empty sums (the reference returned uninitialised y)
+
+  dk_gemv_config cfg;
+  cfg.version = version;
+  cfg.split_k = split_k;
+  cfg.reuse_weights = reuse_weights ? 1 : 0;
+  cfg.warps_per_row = warps_per_row;
+
+  const size_t ws_bytes = dk_gemv_workspace_bytes(M, K, B, &cfg);
+  torch::Tensor workspace;
+  void* ws_ptr = nullptr;
+  if (ws_bytes > 0) {
+    workspace = torch::empty({static_cast<int64_t>((ws_bytes + 3) / 4)},
+                             x.options().dtype(torch::kFloat32));
+    ws_ptr = workspace.data_ptr();
+  }
+
+  const int rc = dk_w4a16_gemv(reinterpret_cast<const uint32_t*>(packed.data_ptr<int32_t>()),
+                               reinterpret_cast<const uint16_t*>(scales.data_ptr<at::Half>()),
+                               reinterpret_cast<const uint16_t*>(x.data_ptr<at::Half>()),
+                               reinterpret_cast<uint16_t*>(y.data_ptr<at::Half>()), M, K, B, &cfg,
+                               ws_ptr, ws_bytes, current_stream(x));
+  check_status(rc, "w4a16_gemv");
+  return y;
+}
+
+// Reference: csrc/bindings.cpp:80-86.
+void d2d_copy(torch::Tensor src, torch::Tensor dst) {
+  TORCH_CHECK(src.is_cuda() && dst.is_cuda(), "src and dst must be CUDA");
+  TORCH_CHECK(src.nbytes() == dst.nbytes(), "src/dst size mismatch");
+  TORCH_CHECK(src.nbytes() % 16 == 0, "copy size must be a multiple of 16");
+  TORCH_CHECK(src.is_contiguous() && dst.is_contiguous(), "src and dst must be contiguous");
+  c10::DeviceGuard guard(src.device());
+  check_status(dk_d2d_copy(src.data_ptr(), dst.data_ptr(), src.nbytes(), current_stream(src)),
+               "d2d_copy");
+}
+
+// Reference: csrc/bindings.cpp:88-98.
+void stream_read(torch::Tensor src, torch::Tensor partials) {
+  TORCH_CHECK(src.is_cuda() && partials.is_cuda(), "src and partials must be CUDA");
+  TORCH_CHECK(src.nbytes() % 16 == 0, "buffer size must be a multiple of 16");
+  TORCH_CHECK(src.is_contiguous(), "src must be contiguous");
+  TORCH_CHECK(partials.scalar_type() == torch::kFloat32, "partials must be fp32");
+  TORCH_CHECK(partials.is_contiguous(), "partials must be contiguous");
+  const int64_t blocks = partials.numel();
+  TORCH_CHECK(blocks >= 1 && blocks <= INT32_MAX, "partials must have one float per block");
+  c10::DeviceGuard guard(src.device());
+  check_status(dk_stream_read(src.data_ptr(), partials.data_ptr<float>(), src.nbytes(),
+                              static_cast<int>(blocks), current_stream(src)),
+               "stream_read");
+}
+
+// Reference: csrc/bindings.cpp:100-106.
+void stream_write(torch::Tensor dst) {
+  TORCH_CHECK(dst.is_cuda(), "dst must be CUDA");
+  TORCH_CHECK(dst.nbytes() % 16 == 0, "buffer size must be a multiple of 16");
+  TORCH_CHECK(dst.is_contiguous(), "dst must be contiguous");
+  c10::DeviceGuard guard(dst.device());
+  const int blocks = dk_stream_recommended_blocks();
+  TORCH_CHECK(blocks > 0, "stream_recommended_blocks failed: ", dk_last_error());
+  check_status(dk_stream_write(dst.data_ptr(), dst.nbytes(), blocks, current_stream(dst)),
+               "stream_write");
+}
+
+int stream_recommended_blocks() {
+  const int blocks = dk_stream_recommended_blocks();
+  TORCH_CHECK(blocks > 0, "stream_recommended_blocks failed: ", dk_last_error());
+  return blocks;
+}
+
+int last_kernel_stamp() { return dk_last_kernel_stamp(); }
+
+void empty_kernel() {
+  check_status(dk_empty_kernel(c10::hip::getCurrentHIPStream().stream()), "empty_kernel");
+}
+
+int64_t workspace_bytes(int64_t M, int64_t K, int64_t B, int version, int split_k,
+                        bool reuse_weights, int warps_per_row) {
+  dk_gemv_config cfg{version, split_k, reuse_weights ? 1 : 0, warps_per_row};
+  return static_cast<int64_t>(
+      dk_gemv_workspace_bytes(static_cast<int>(M), static_cast<int>(K), static_cast<int>(B), &cfg));
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("w4a16_gemv", &w4a16_gemv, "W4A16 GEMV", py::arg("packed"), py::arg("scales"),
+        py::arg("x"), py::arg("version") = 5, py::arg("split_k") = 4,
+        py::arg("reuse_weights") = false, py::arg("warps_per_row") = 1);
+  m.def("d2d_copy", &d2d_copy, "Aligned device-to-device copy", py::arg("src"), py::arg("dst"));
+  m.def("stream_read", &stream_read, "Read-only STREAM sum-reduction (one float partial per block)",
+        py::arg("src"), py::arg("partials"));
+  m.def("stream_write", &stream_write, "Write-only STREAM fill", py::arg("dst"));
+  m.def("stream_recommended_blocks", &stream_recommended_blocks,
+        "Block count used by STREAM probes");
+  m.def("last_kernel_stamp", &last_kernel_stamp,
+        "Stage stamp written by the GEMV that actually launched");
+  m.def("empty_kernel", &empty_kernel, "Empty kernel on the current stream (event-timer floor)");
+  m.def("workspace_bytes", &workspace_bytes, "Device workspace bytes a GEMV call needs",
+        py::arg("M"), py::arg("K"), py::arg("B"), py::arg("version") = 5, py::arg("split_k") = 4,
+        py::arg("reuse_weights") = false, py::arg("warps_per_row") = 1);
+  m.attr("ABI_VERSION") = dk_abi_version();
+}

@@ -1,0 +1,84 @@
+"""Symmetric grouped int4 weight format (group 128), the layout the kernels read.
+
+Format (identical to python/decode_kernel/quantize.py:1-15 of the reference):
+
+* every 128 consecutive weights of a row share one fp16 scale
+  ``scale = max(|w|)/7`` (computed in fp32, clamped below at 1e-8, then
+  rounded to fp16);
+* ``q = clamp(round_half_even(w / scale_fp32), -7, 7)``, using the fp32 scale
+  before its fp16 rounding;
+* eight consecutive q are packed into one int32, weight ``k = 8*word + n`` in
+  bits ``4n .. 4n+3`` as a two's-complement nibble (low nibble first).
+  -8 (nibble 0x8) is a valid encoding the kernels decode, but this quantizer
+  never produces it.
+
+These functions run on whatever device the input tensor lives on; they are
+the format producer, not the GEMV (which only exists as a HIP kernel).
+"""
+
+from __future__ import annotations
+
+import torch
+
+GROUP_SIZE = 128
+NIBBLES_PER_WORD = 8
+QMIN, QMAX = -7, 7
+SCALE_FLOOR = 1e-8
+
+_NIBBLE_SHIFTS = tuple(range(0, 32, 4))
+
+
+def quantize_and_pack(
+    weight: torch.Tensor, group_size: int = GROUP_SIZE
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """W[M, K] -> (packed int32 [M, K/8], scales fp16 [M, K/group]).
+
+    Reference: python/decode_kernel/quantize.py:26-51.
+    """
+    if weight.dim() != 2:
+        raise ValueError("weight must be [M, K]")
+    m, k = weight.shape
+    if k % group_size != 0:
+        raise ValueError(f"K={k} is not divisible by group_size={group_size}")
+    if k % NIBBLES_PER_WORD != 0:
+        raise ValueError(f"K={k} is not divisible by {NIBBLES_PER_WORD}")
+
+    groups = weight.float().reshape(m, k // group_size, group_size)
+    scale = (groups.abs().amax(dim=-1) / float(QMAX)).clamp_min(SCALE_FLOOR)
+    q = torch.round(groups / scale[..., None]).clamp_(QMIN, QMAX).to(torch.int32)
+
+    # Nibble fields are disjoint, so an int32 sum of the shifted fields is
+    # their bitwise OR (the top field wraps to the sign bit, as intended).
+    fields = (q.reshape(m, k // NIBBLES_PER_WORD, NIBBLES_PER_WORD) & 0xF) << torch.tensor(
+        _NIBBLE_SHIFTS, dtype=torch.int32, device=q.device
+    )
+    packed = fields.sum(dim=-1, dtype=torch.int32)
+    return packed.contiguous(), scale.half().contiguous()
+
+
+def unpack_to_int(packed: torch.Tensor) -> torch.Tensor:
+    """int32 words [M, K/8] -> signed q [M, K] in [-8, 7] (int32).
+
+    Reference: python/decode_kernel/quantize.py:54-63.
+    """
+    m, words = packed.shape
+    shifts = torch.tensor(_NIBBLE_SHIFTS, dtype=torch.int32, device=packed.device)
+    nib = (packed.to(torch.int32)[..., None] >> shifts) & 0xF  # [M, words, 8]
+    q = nib - ((nib & 0x8) << 1)  # two's complement of the 4-bit field
+    return q.reshape(m, words * NIBBLES_PER_WORD).to(torch.int32)
+
+
+def dequantize(
+    packed: torch.Tensor,
+    scales: torch.Tensor,
+    group_size: int = GROUP_SIZE,
+    dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """Materialise W = q * scale [M, K] (for checks; the kernels never do this).
+
+    Reference: python/decode_kernel/quantize.py:66-78.
+    """
+    q = unpack_to_int(packed).to(dtype)
+    m, k = q.shape
+    s = scales.to(dtype).reshape(m, k // group_size, 1)
+    return (q.reshape(m, k // group_size, group_size) * s).reshape(m, k)

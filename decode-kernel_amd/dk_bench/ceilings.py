@@ -1,0 +1,119 @@
+"""Hardware ceilings for one MI355X, measured before the GEMV is judged.
+
+    python -m dk_bench.ceilings [--bytes N] [--out PATH]   (from decode-kernel_amd/)
+
+STREAM probes over a buffer of at least 1 GiB (past the 256 MB Infinity
+Cache and the 8 x 4 MB L2s), as bench/ceilings.py:1-13 of the reference did
+with 512 MB on NVIDIA parts:
+  * read:  grid-stride sum, read-only, bytes counted once  <- GEMV denominator
+  * copy:  read + write, bytes counted twice
+  * write: fill, bytes counted once
+plus the empty-kernel event floor (what two HIP events around a launch cost
+with nothing in between) and an fp16 GEMM for the ridge point.
+"""
+
+from __future__ import annotations
+
+import argparse
+from pathlib import Path
+
+import torch
+
+from .common import meta_dict, save_json, time_gpu
+
+DEFAULT_STREAM_BYTES = 1 << 30
+
+
+def _measure(fn, nbytes: int, factor: float, warmup: int, iters: int) -> dict:
+    stats = time_gpu(fn, warmup=warmup, iters=iters, flush=None)
+    return {"nbytes": nbytes, "bytes_factor": factor,
+            "gbps": factor * nbytes / (stats["median_us"] * 1e3), **stats}
+
+
+def measure_read(nbytes: int = DEFAULT_STREAM_BYTES, warmup: int = 10, iters: int = 50) -> dict:
+    from decode_kernel import _cuda
+
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    blocks = int(_cuda.stream_recommended_blocks())
+    partials = torch.empty(blocks, dtype=torch.float32, device="cuda")
+    out = _measure(lambda: _cuda.stream_read(src, partials), nbytes, 1.0, warmup, iters)
+    out["kind"] = "stream_read_sum"
+    out["blocks"] = blocks
+    # The sum must equal the element count (buffer of ones): the loads happened.
+    out["checksum_ok"] = float(partials.double().sum()) == float(nbytes // 4)
+    return out
+
+
+def measure_copy(nbytes: int = DEFAULT_STREAM_BYTES, warmup: int = 10, iters: int = 50) -> dict:
+    from decode_kernel import _cuda
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    out = _measure(lambda: _cuda.d2d_copy(src, dst), nbytes, 2.0, warmup, iters)
+    out["kind"] = "d2d_copy"
+    return out
+
+
+def measure_write(nbytes: int = DEFAULT_STREAM_BYTES, warmup: int = 10, iters: int = 50) -> dict:
+    from decode_kernel import _cuda
+
+    dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    out = _measure(lambda: _cuda.stream_write(dst), nbytes, 1.0, warmup, iters)
+    out["kind"] = "stream_write_fill"
+    return out
+
+
+def measure_event_floor(warmup: int = 50, iters: int = 500) -> dict:
+    from decode_kernel import _cuda
+
+    return time_gpu(_cuda.empty_kernel, warmup=warmup, iters=iters, flush=None)
+
+
+def measure_gemm_fp16(n: int = 8192, warmup: int = 10, iters: int = 30) -> dict:
+    a = torch.randn(n, n, device="cuda", dtype=torch.float16)
+    b = torch.randn(n, n, device="cuda", dtype=torch.float16)
+    stats = time_gpu(lambda: torch.mm(a, b), warmup=warmup, iters=iters, flush=None)
+    return {"n": n, "tflops": 2.0 * n ** 3 / (stats["median_us"] * 1e-6) / 1e12, **stats}
+
+
+def measure_all(nbytes: int = DEFAULT_STREAM_BYTES, gemm: bool = True) -> dict:
+    read = measure_read(nbytes)
+    out = {
+        "hbm_read": read,
+        "hbm_copy": measure_copy(nbytes),
+        "hbm_write": measure_write(nbytes),
+        "event_floor": measure_event_floor(),
+        "hbm_denominator": "read",
+    }
+    if gemm:
+        g = measure_gemm_fp16()
+        out["gemm_fp16"] = g
+        out["ridge_flop_per_byte"] = g["tflops"] * 1e12 / (read["gbps"] * 1e9)
+    return out
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--bytes", type=int, default=DEFAULT_STREAM_BYTES)
+    ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--out", type=Path, default=None)
+    args = ap.parse_args()
+    if not torch.cuda.is_available():
+        raise SystemExit("a GPU is required")
+    if args.bytes % 16 or args.bytes < (1 << 30):
+        raise SystemExit("--bytes must be a multiple of 16 and at least 1 GiB")
+    payload = {"meta": meta_dict(), **measure_all(args.bytes, gemm=not args.no_gemm)}
+    if args.out:
+        save_json(args.out, payload)
+    r, c, w = payload["hbm_read"], payload["hbm_copy"], payload["hbm_write"]
+    print(f"STREAM buffer {args.bytes / 2**30:.2f} GiB")
+    print(f"read  {r['gbps']:.1f} GB/s  (denominator, checksum_ok={r['checksum_ok']})")
+    print(f"copy  {c['gbps']:.1f} GB/s   write {w['gbps']:.1f} GB/s")
+    print(f"event floor p50 {payload['event_floor']['median_us']:.2f} us")
+    if "gemm_fp16" in payload:
+        print(f"fp16 GEMM {payload['gemm_fp16']['tflops']:.1f} TFLOP/s, "
+              f"ridge {payload['ridge_flop_per_byte']:.0f} FLOP/B")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,180 @@
+"""Shared benchmark helpers: HIP-event timer, cache flush, bytes and roofs.
+
+Restates bench/common.py of the reference for MI355X:
+  * time_gpu: events around exactly one call per iteration on the stream the
+    kernel runs on, a flush before each iteration outside the events, median
+    and IQR (bench/common.py:64-108); also the mean, which the roofline uses;
+  * the flush defaults to a read-only sweep of 1 GiB (the reference wrote
+    64 MB, bench/common.py:54-61): larger than the 256 MB Infinity Cache and
+    the 8 x 4 MB L2s, and read-only so the timed kernel never competes with
+    the write-back of a dirty flush buffer;
+  * bytes_moved_w4 / flop_gemv: bench/common.py:111-125.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+import platform
+import statistics
+import subprocess
+from dataclasses import asdict, dataclass
+from datetime import datetime, timezone
+from typing import Callable, Optional
+
+import torch
+
+GROUP_SIZE = 128
+FLUSH_BYTES_DEFAULT = 1 << 30
+MI355X_HBM_PEAK_GBPS = 8000.0
+
+
+def bytes_moved_w4(m: int, k: int, batch: int) -> int:
+    """Algorithmic HBM bytes if W is read once: packed W + scales + x + y."""
+    return m * (k // 2) + m * (k // GROUP_SIZE) * 2 + batch * k * 2 + batch * m * 2
+
+
+def bytes_moved_fp16(m: int, k: int, batch: int) -> int:
+    return m * k * 2 + batch * k * 2 + batch * m * 2
+
+
+def flop_gemv(m: int, k: int, batch: int) -> int:
+    return 2 * m * k * batch
+
+
+class Flush:
+    """Evicts L2 and the Infinity Cache between timed iterations."""
+
+    def __init__(self, nbytes: int = FLUSH_BYTES_DEFAULT, kind: str = "read"):
+        from decode_kernel import _cuda
+
+        if kind not in ("read", "write", "none"):
+            raise ValueError(kind)
+        self.kind = kind
+        self.nbytes = nbytes if kind != "none" else 0
+        self._cuda = _cuda
+        if kind == "none":
+            return
+        self.buf = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+        self.partials = torch.empty(_cuda.stream_recommended_blocks(), dtype=torch.float32,
+                                    device="cuda")
+
+    def __call__(self) -> None:
+        if self.kind == "read":
+            self._cuda.stream_read(self.buf, self.partials)
+        elif self.kind == "write":
+            self._cuda.stream_write(self.buf)
+
+    def describe(self) -> dict:
+        return {"kind": self.kind, "bytes": self.nbytes}
+
+
+def time_gpu(fn: Callable[[], object], warmup: int, iters: int,
+             flush: Optional[Flush] = None) -> dict:
+    """Median / IQR / mean of one `fn()` call between two HIP events."""
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    for _ in range(warmup):
+        if flush is not None:
+            flush()
+        fn()
+    torch.cuda.synchronize()
+    import time
+
+    t0 = time.perf_counter()
+    for i in range(iters):
+        if flush is not None:
+            flush()
+        starts[i].record(stream)
+        fn()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    us = sorted(s.elapsed_time(e) * 1000.0 for s, e in zip(starts, ends))
+    n = len(us)
+    return {
+        "median_us": us[n // 2],
+        "q1_us": us[n // 4],
+        "q3_us": us[(3 * n) // 4],
+        "iqr_us": us[(3 * n) // 4] - us[n // 4],
+        "mean_us": statistics.fmean(us),
+        "stdev_us": statistics.pstdev(us) if n > 1 else 0.0,
+        "min_us": us[0],
+        "max_us": us[-1],
+        "warmup": warmup,
+        "iters": iters,
+        "wall_s_timed_loop": wall_s,
+        "flush": flush.describe() if flush is not None else None,
+    }
+
+
+def gpu_info() -> dict:
+    if not torch.cuda.is_available():
+        return {"name": "none"}
+    p = torch.cuda.get_device_properties(0)
+    info = {
+        "name": torch.cuda.get_device_name(0),
+        "gcn_arch": getattr(p, "gcnArchName", None),
+        "total_memory_bytes": int(p.total_memory),
+        "multi_processor_count": int(p.multi_processor_count),
+        "l2_cache_bytes": int(getattr(p, "L2_cache_size", 0)),
+    }
+    info["amd_smi"] = _smi()
+    return info
+
+
+def _smi() -> dict:
+    for cmd in (["amd-smi", "static", "--asic", "--clock", "--json"],
+                ["rocm-smi", "--showclocks", "--json"]):
+        try:
+            out = subprocess.run(cmd, capture_output=True, text=True, timeout=20)
+            if out.returncode == 0 and out.stdout.strip():
+                return {"cmd": " ".join(cmd), "raw": out.stdout.strip()[:4000]}
+        except Exception as exc:  # tool missing on this host
+            last = str(exc)
+            continue
+    return {"error": locals().get("last", "no smi tool")}
+
+
+@dataclass
+class RunMeta:
+    gpu: dict
+    host: str
+    platform: str
+    torch: str
+    hip: Optional[str]
+    timestamp: str
+    git: Optional[str]
+    host_cpus: int
+
+
+def collect_meta() -> RunMeta:
+    git = None
+    try:
+        git = subprocess.check_output(["git", "rev-parse", "--short", "HEAD"], text=True,
+                                      timeout=5, stderr=subprocess.DEVNULL).strip()
+    except Exception:
+        pass
+    return RunMeta(
+        gpu=gpu_info(),
+        host=platform.node(),
+        platform=platform.platform(),
+        torch=torch.__version__,
+        hip=getattr(torch.version, "hip", None),
+        timestamp=datetime.now(timezone.utc).isoformat(),
+        git=git,
+        host_cpus=len(os.sched_getaffinity(0)),
+    )
+
+
+def meta_dict() -> dict:
+    return asdict(collect_meta())
+
+
+def save_json(path, payload: dict) -> None:
+    from pathlib import Path
+
+    p = Path(path)
+    p.parent.mkdir(parents=True, exist_ok=True)
+    p.write_text(json.dumps(payload, indent=2) + "\n")

@@ -1,0 +1,129 @@
+/*
+ * decode_kernel C ABI for MI355X (gfx950): W4A16 decode GEMV and HBM probes.
+ *
+ * Plain C, plain pointers and sizes, no torch types. Every entry point
+ * validates its arguments on the host before touching the device and returns
+ * a dk_status; dk_last_error() gives the message for the calling thread.
+ *
+ * Weight format (unchanged from the reference, python/decode_kernel/quantize.py:1-15):
+ *   packed  uint32 [M, K/8]   8 signed two's-complement nibbles per word,
+ *                             nibble n of word w is weight k = 8*w + n (low first)
+ *   scales  fp16   [M, K/128] one symmetric scale per 128-wide K group
+ *   x       fp16   [B, K]
+ *   y       fp16   [B, M]     y[b,m] = sum_k fp32(scale[m,k/128]) * q[m,k] * fp32(x[b,k])
+ * fp16 values travel as their uint16 bit patterns.
+ */
+#ifndef DECODE_KERNEL_DK_GEMV_H_
+#define DECODE_KERNEL_DK_GEMV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h> /* hipStream_t */
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Format constants. Reference: include/decode_kernel/gemv_w4a16.h:9-11. */
+#define DK_GROUP_SIZE 128
+#define DK_NIBBLES_PER_WORD 8
+#define DK_WEIGHTS_PER_CHUNK 32 /* one 16-byte load of packed weights */
+
+/* Kernel variants. Reference: include/decode_kernel/gemv_w4a16.h:13-20.
+ * Each variant is a distinct gfx950 kernel and writes its own dispatch stamp:
+ * v0..v5 -> 0..5, waves-per-row w (2..8) -> 10+w, weight-reuse -> 15. */
+typedef enum dk_kernel_version {
+  DK_V0 = 0, /* one thread per row (naive baseline) */
+  DK_V1 = 1, /* one wave64 per row, 4-byte coalesced word loads */
+  DK_V2 = 2, /* one wave64 per row, 16-byte coalesced loads */
+  DK_V3 = 3, /* v2 with the row's group scales staged in LDS */
+  DK_V4 = 4, /* split-K over grid.y, deterministic single-launch reduction */
+  DK_V5 = 5  /* tuned: several rows per wave, x reused from registers */
+} dk_kernel_version;
+
+#define DK_STAMP_REUSE 15
+#define DK_STAMP_MULTIWAVE_BASE 10
+
+/* Launch configuration. Reference: include/decode_kernel/gemv_w4a16.h:22-27
+ * (GemvLaunchConfig); defaults are the same (v5, split_k 4, no reuse, 1). */
+typedef struct dk_gemv_config {
+  int version;       /* dk_kernel_version, 0..5 */
+  int split_k;       /* v4 only, 1..32; ignored otherwise */
+  int reuse_weights; /* nonzero: weight-reuse path (MFMA), ignores version */
+  int warps_per_row; /* v1 only, 1..8: wave64s sharing one row's K */
+} dk_gemv_config;
+
+typedef enum dk_status {
+  DK_OK = 0,
+  DK_ERR_INVALID_ARGUMENT = 1, /* rejected on the host; nothing was launched */
+  DK_ERR_HIP = 2,              /* the HIP runtime reported an error */
+  DK_ERR_UNSUPPORTED = 3       /* valid request beyond a compiled limit */
+} dk_status;
+
+/* Fill *cfg with the reference defaults (v5, split_k 4, reuse 0, 1 wave/row). */
+void dk_gemv_config_default(dk_gemv_config* cfg);
+
+/* Bytes of device workspace dk_w4a16_gemv needs for this call (0 for every
+ * variant except split-K v4, which keeps fp32 partials [split_k, B, M]). No
+ * counterpart in the reference, whose v4 took an fp32 [B, M] buffer
+ * (include/decode_kernel/gemv_w4a16.h:33). Returns 0 for invalid arguments. */
+size_t dk_gemv_workspace_bytes(int M, int K, int B, const dk_gemv_config* cfg);
+
+/* Host-side argument check of dk_w4a16_gemv without launching anything
+ * (shape rules of csrc/bindings.cpp:10-48). Returns DK_OK or
+ * DK_ERR_INVALID_ARGUMENT. */
+int dk_gemv_validate(int M, int K, int B, const dk_gemv_config* cfg);
+
+/* y[B, M] = dequant(packed, scales)[M, K] @ x[B, K]^T, asynchronously on
+ * `stream`. Replaces decode_kernel::w4a16_gemv
+ * (include/decode_kernel/gemv_w4a16.h:34-36, csrc/gemv_w4a16.cu:568-591).
+ * M, K or B <= 0 is a no-op returning DK_OK (csrc/gemv_w4a16.cu:571).
+ * `workspace` must hold dk_gemv_workspace_bytes() bytes (may be NULL if 0).
+ * Differences from the reference: launch errors are returned (the reference
+ * printed and continued, csrc/gemv_w4a16.cu:9-16), and split-K is one
+ * launch with a deterministic reduction instead of memset+atomics+convert.
+ * Concurrent split-K calls on one device must not overlap in time: they
+ * share the device's completion tickets. */
+int dk_w4a16_gemv(const uint32_t* packed, const uint16_t* scales,
+                  const uint16_t* x, uint16_t* y, int M, int K, int B,
+                  const dk_gemv_config* cfg, void* workspace,
+                  size_t workspace_bytes, hipStream_t stream);
+
+/* STREAM probes. Reference: include/decode_kernel/gemv_w4a16.h:38-43,
+ * csrc/gemv_w4a16.cu:593-626. `bytes` must be a multiple of 16.
+ * dk_stream_read writes one fp32 partial sum per block into `partials`
+ * (blocks entries); blocks < 1 selects dk_stream_recommended_blocks(). */
+int dk_d2d_copy(const void* src, void* dst, size_t bytes, hipStream_t stream);
+int dk_stream_read(const void* src, float* partials, size_t bytes, int blocks,
+                   hipStream_t stream);
+int dk_stream_write(void* dst, size_t bytes, int blocks, hipStream_t stream);
+
+/* Block count for the probes on the current device: CUs*32 clamped to
+ * [1024, 8192] (csrc/gemv_w4a16.cu:602-609 queried device 0 instead).
+ * Returns a negative dk_status on error. */
+int dk_stream_recommended_blocks(void);
+
+/* Stamp written by the last GEMV kernel that ran on the current device, or -1
+ * if none ran since the previous read. Synchronises the device, reads the
+ * stamp and clears it to -1 (the reference cleared it with an extra host-to-
+ * device copy before every launch, csrc/gemv_w4a16.cu:553-564,573).
+ * Returns -1 on error as well; see dk_last_error(). */
+int dk_last_kernel_stamp(void);
+
+/* An empty kernel on `stream`: the event-timer floor for the benchmark.
+ * No counterpart in the reference. */
+int dk_empty_kernel(hipStream_t stream);
+
+/* Message for the last non-DK_OK status returned on the calling thread. */
+const char* dk_last_error(void);
+
+/* ABI version of this header, (major << 16) | minor. */
+int dk_abi_version(void);
+#define DK_ABI_VERSION ((1 << 16) | 0)
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* DECODE_KERNEL_DK_GEMV_H_ */

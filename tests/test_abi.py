@@ -1,0 +1,144 @@
+"""CPU checks of the drop-in boundary: the C-ABI library loads, exports every
+entry point include/decode_kernel/*.h declares, and rejects bad arguments on
+the host (no compute call needs a GPU here). Also checks the torch extension
+exposes the reference's pybind surface (csrc/bindings.cpp:114-129).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from decode_kernel import _abi
+
+REPO = Path(__file__).resolve().parents[1]
+HEADERS = sorted((REPO / "include").rglob("*.h"))
+
+
+def _declared_functions() -> set[str]:
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"^\s*[A-Za-z_][\w\s\*]*?\b(dk_\w+)\s*\(", text, flags=re.M):
+            names.add(m.group(1))
+    return names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _abi.LIB_PATH.exists():
+        pytest.fail(f"{_abi.LIB_PATH} is not built (python decode-kernel_amd/build_ext.py)")
+    return _abi.load()
+
+
+def test_header_declarations_found():
+    names = _declared_functions()
+    assert "dk_w4a16_gemv" in names and "dk_stream_read" in names
+    assert names == set(_abi.EXPORTS), names ^ set(_abi.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version(lib):
+    assert lib.dk_abi_version() == (1 << 16) | 0
+
+
+def test_default_config_matches_reference(lib):
+    # include/decode_kernel/gemv_w4a16.h:22-27: V5, split_k 4, no reuse, 1 warp/row.
+    cfg = _abi.default_config(lib)
+    assert (cfg.version, cfg.split_k, cfg.reuse_weights, cfg.warps_per_row) == (5, 4, 0, 1)
+
+
+@pytest.mark.parametrize(
+    "overrides,msg",
+    [
+        ({"version": 6}, "version must be 0..5"),
+        ({"version": -1}, "version must be 0..5"),
+        ({"split_k": 0}, "split_k must be in [1, 32]"),
+        ({"split_k": 33}, "split_k must be in [1, 32]"),
+        ({"warps_per_row": 9}, "warps_per_row must be in [1, 8]"),
+        ({"warps_per_row": 2, "version": 5}, "streaming v1 only"),
+        ({"warps_per_row": 2, "version": 1, "reuse_weights": 1}, "streaming v1 only"),
+    ],
+)
+def test_validate_rejects_reference_ranges(lib, overrides, msg):
+    cfg = _abi.default_config(lib, **overrides)
+    rc = lib.dk_gemv_validate(64, 256, 1, ctypes.byref(cfg))
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT
+    assert msg in lib.dk_last_error().decode()
+
+
+def test_validate_k_multiple_of_group(lib):
+    cfg = _abi.default_config(lib)
+    assert lib.dk_gemv_validate(4, 200, 1, ctypes.byref(cfg)) == _abi.DK_ERR_INVALID_ARGUMENT
+    assert "divisible by group size 128" in lib.dk_last_error().decode()
+    assert lib.dk_gemv_validate(4, 256, 1, ctypes.byref(cfg)) == _abi.DK_OK
+
+
+def test_empty_problem_is_a_noop(lib):
+    # csrc/gemv_w4a16.cu:571: M, K or B <= 0 returns before any launch; no
+    # pointers are touched, so this is safe without a GPU.
+    cfg = _abi.default_config(lib)
+    for m, k, b in [(0, 128, 1), (4, 0, 1), (4, 128, 0), (-1, 128, 1)]:
+        rc = lib.dk_w4a16_gemv(None, None, None, None, m, k, b, ctypes.byref(cfg), None, 0, None)
+        assert rc == _abi.DK_OK
+
+
+def test_null_and_misaligned_pointers_rejected(lib):
+    cfg = _abi.default_config(lib)
+    rc = lib.dk_w4a16_gemv(None, None, None, None, 4, 128, 1, ctypes.byref(cfg), None, 0, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "NULL" in lib.dk_last_error().decode()
+    fake = 0x10000
+    rc = lib.dk_w4a16_gemv(fake + 4, fake, fake, fake, 4, 128, 1, ctypes.byref(cfg), None, 0, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "16-byte aligned" in lib.dk_last_error().decode()
+
+
+def test_split_k_workspace_contract(lib):
+    cfg = _abi.default_config(lib, version=4, split_k=4)
+    # [split_k, B, M] fp32 partials; split is capped at the group count.
+    assert lib.dk_gemv_workspace_bytes(4096, 4096, 2, ctypes.byref(cfg)) == 4 * 2 * 4096 * 4
+    assert lib.dk_gemv_workspace_bytes(64, 256, 1, ctypes.byref(cfg)) == 2 * 1 * 64 * 4
+    for v in (0, 1, 2, 3, 5):
+        c = _abi.default_config(lib, version=v)
+        assert lib.dk_gemv_workspace_bytes(4096, 4096, 1, ctypes.byref(c)) == 0
+    fake = 0x10000
+    rc = lib.dk_w4a16_gemv(fake, fake, fake, fake, 64, 256, 1, ctypes.byref(cfg), None, 0, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "workspace" in lib.dk_last_error().decode()
+
+
+def test_probe_argument_checks(lib):
+    assert lib.dk_stream_read(None, None, 16, 1, None) == _abi.DK_ERR_INVALID_ARGUMENT
+    assert lib.dk_stream_read(0x10000, 0x10000, 15, 1, None) == _abi.DK_ERR_INVALID_ARGUMENT
+    assert lib.dk_stream_write(None, 16, 1, None) == _abi.DK_ERR_INVALID_ARGUMENT
+    assert lib.dk_d2d_copy(0x10000, 0x10000, 17, None) == _abi.DK_ERR_INVALID_ARGUMENT
+    assert lib.dk_d2d_copy(0x10000, 0x10008, 16, None) == _abi.DK_ERR_INVALID_ARGUMENT
+
+
+def test_torch_extension_surface():
+    from decode_kernel import _cuda
+
+    for name in ("w4a16_gemv", "d2d_copy", "stream_read", "stream_write",
+                 "stream_recommended_blocks", "last_kernel_stamp"):
+        assert hasattr(_cuda, name), name
+    doc = _cuda.w4a16_gemv.__doc__
+    for pat in (r"version: [\w.]*Int = 5", r"split_k: [\w.]*Int = 4",
+                r"reuse_weights: bool = False", r"warps_per_row: [\w.]*Int = 1"):
+        assert re.search(pat, doc), (pat, doc)
+    assert _cuda.ABI_VERSION == (1 << 16) | 0
+
+
+def test_extension_rejects_cpu_tensors():
+    import torch
+    from decode_kernel import gemv
+
+    packed = torch.zeros(4, 16, dtype=torch.int32)
+    scales = torch.zeros(4, 1, dtype=torch.float16)
+    x = torch.zeros(1, 128, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="must be CUDA tensors"):
+        gemv(packed, scales, x)
