@@ -56,9 +56,17 @@ void check_gemv_inputs(const torch::Tensor& packed, const torch::Tensor& scales,
 
 }  // namespace
 
+torch::Tensor gemv_common(torch::Tensor packed, torch::Tensor scales, torch::Tensor x, int version,
+                          int split_k, bool reuse_weights, int warps_per_row);
+
 // Reference: csrc/bindings.cpp:37-78.
 torch::Tensor w4a16_gemv(torch::Tensor packed, torch::Tensor scales, torch::Tensor x, int version,
                          int split_k, bool reuse_weights, int warps_per_row) {
+  return gemv_common(packed, scales, x, version, split_k, reuse_weights, warps_per_row);
+}
+
+torch::Tensor gemv_common(torch::Tensor packed, torch::Tensor scales, torch::Tensor x, int version,
+                          int split_k, bool reuse_weights, int warps_per_row) {
   check_gemv_inputs(packed, scales, x);
   TORCH_CHECK(version >= 0 && version <= 5, "version must be 0..5");
   TORCH_CHECK(split_k >= 1 && split_k <= 32, "split_k must be in [1, 32]");
@@ -169,7 +177,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Block count used by STREAM probes");
   m.def("last_kernel_stamp", &last_kernel_stamp,
         "Stage stamp written by the GEMV that actually launched");
-  m.def("empty_kernel", &empty_kernel, "Empty kernel on the current stream (event-timer floor)");
+  m.def("empty_kernel", &empty_kernel, "Empty kernel on the current stream (launch floor)");
   m.def("workspace_bytes", &workspace_bytes, "Device workspace bytes a GEMV call needs",
         py::arg("M"), py::arg("K"), py::arg("B"), py::arg("version") = 5, py::arg("split_k") = 4,
         py::arg("reuse_weights") = false, py::arg("warps_per_row") = 1);

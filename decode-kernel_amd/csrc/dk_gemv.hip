@@ -7,11 +7,7 @@
 // decode with packed fp16 math, v_dot2_f32_f16 or MFMA products with fp32
 // accumulation, DPP wave reductions and a single-launch split-K.
 //
-// Layout in HBM (the reference format, no repacking):
-//   packed uint32 [M, K/8]: row m is K/2 bytes; 16-byte chunk c of a row holds
-//                           weights k = 32c .. 32c+31 (4 words, low nibble first)
-//   scales fp16  [M, K/128]: chunk c of row m uses scales[m, c/4]
-//   x      fp16  [B, K], y fp16 [B, M]
+// The kernels themselves are in dk_kernels.hpp.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -19,486 +15,9 @@
 #include <cstdio>
 #include <string>
 
-#include "dk_device.hpp"
 #include "dk_host.hpp"
+#include "dk_kernels.hpp"
 #include "decode_kernel/dk_gemv.h"
-
-namespace dk {
-
-// ---------------------------------------------------------------------------
-// Dispatch stamp: written by block (0,0) thread 0 of whichever GEMV kernel
-// ran. Host reads and clears it in dk_last_kernel_stamp().
-// Reference: csrc/gemv_w4a16.cu:18-25.
-// ---------------------------------------------------------------------------
-__device__ int g_stamp = -1;
-
-__device__ __forceinline__ void write_stamp(int s) {
-  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) g_stamp = s;
-}
-
-// Split-K completion tickets, one per row tile. Zero at load; the last
-// workgroup of a tile resets its ticket, so they are zero between launches.
-constexpr int kMaxTickets = 1 << 16;
-__device__ unsigned int g_tickets[kMaxTickets];
-
-// ---------------------------------------------------------------------------
-// v0: one thread per row, scalar decode (the uncoalesced baseline stage).
-// Reference: csrc/gemv_w4a16.cu:70-94.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void gemv_v0(const uint32_t* __restrict__ packed,
-                                               const uint16_t* __restrict__ scales,
-                                               const uint16_t* __restrict__ x,
-                                               uint16_t* __restrict__ y, int M, int K, int B) {
-  write_stamp(0);
-  const int row = blockIdx.x * blockDim.x + threadIdx.x;
-  if (row >= M) return;
-  const int words = K >> 3;
-  const int G = K >> 7;
-  const uint32_t* rw = packed + (size_t)row * words;
-  const uint16_t* rs = scales + (size_t)row * G;
-  for (int b = 0; b < B; ++b) {
-    const uint16_t* xb = x + (size_t)b * K;
-    float acc = 0.f;
-    for (int i = 0; i < words; ++i) {
-      const uint32_t w = rw[i];
-      const float s = h2f(rs[i >> 4]);
-#pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        const int q = (int)(w << (28 - 4 * n)) >> 28;
-        acc += s * (float)q * h2f(xb[8 * i + n]);
-      }
-    }
-    y[(size_t)b * M + row] = f2h(acc);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// v1: one wave64 per row; lane l reads words l, l+64, ... (256 contiguous
-// bytes per wave instruction); one 16-byte x load per word.
-// Reference: csrc/gemv_w4a16.cu:99-128.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void gemv_v1(const uint32_t* __restrict__ packed,
-                                               const uint16_t* __restrict__ scales,
-                                               const uint4* __restrict__ x4,
-                                               uint16_t* __restrict__ y, int M, int K, int B) {
-  write_stamp(1);
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (row >= M) return;
-  const int words = K >> 3;
-  const int G = K >> 7;
-  const uint32_t* rw = packed + (size_t)row * words;
-  const uint16_t* rs = scales + (size_t)row * G;
-  for (int b = 0; b < B; ++b) {
-    const uint4* xb = x4 + (size_t)b * words;
-    float acc = 0.f;
-    for (int i = lane; i < words; i += kWave) {
-      h2_t xp[4];
-      pair_x(xb[i], xp);
-      acc += h2f(rs[i >> 4]) * dot_word(rw[i], xp, 0.f);
-    }
-    acc = wave_sum(acc);
-    if (lane == 63) y[(size_t)b * M + row] = f2h(acc);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// v1 with K split over `wpr` waves of one workgroup per row, LDS reduction in
-// wave order. Stamp 10 + wpr. Reference: csrc/gemv_w4a16.cu:134-172.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(512) void gemv_v1_multiwave(const uint32_t* __restrict__ packed,
-                                                         const uint16_t* __restrict__ scales,
-                                                         const uint4* __restrict__ x4,
-                                                         uint16_t* __restrict__ y, int M, int K,
-                                                         int B) {
-  const int wpr = blockDim.x >> 6;
-  write_stamp(10 + wpr);
-  __shared__ float red[8];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int row = blockIdx.x;  // grid is exactly M
-  const int words = K >> 3;
-  const int G = K >> 7;
-  const uint32_t* rw = packed + (size_t)row * words;
-  const uint16_t* rs = scales + (size_t)row * G;
-  for (int b = 0; b < B; ++b) {
-    const uint4* xb = x4 + (size_t)b * words;
-    float acc = 0.f;
-    for (int i = wave * kWave + lane; i < words; i += wpr * kWave) {
-      h2_t xp[4];
-      pair_x(xb[i], xp);
-      acc += h2f(rs[i >> 4]) * dot_word(rw[i], xp, 0.f);
-    }
-    acc = wave_sum(acc);
-    if (lane == 63) red[wave] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float t = 0.f;
-      for (int w = 0; w < wpr; ++w) t += red[w];
-      y[(size_t)b * M + row] = f2h(t);
-    }
-    __syncthreads();
-  }
-}
-
-// ---------------------------------------------------------------------------
-// v2 / v3: one wave64 per row with 16-byte loads (32 weights per lane per
-// load, 1 KiB per wave instruction). v3 stages the row's group scales in LDS.
-// Reference: csrc/gemv_w4a16.cu:183-257.
-// ---------------------------------------------------------------------------
-template <bool kScalesInLds>
-__global__ __launch_bounds__(256) void gemv_v23(const uint4* __restrict__ packed,
-                                                const uint16_t* __restrict__ scales,
-                                                const uint4* __restrict__ x4,
-                                                uint16_t* __restrict__ y, int M, int K, int B) {
-  write_stamp(kScalesInLds ? 3 : 2);
-  extern __shared__ uint16_t lds_scales[];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int row_raw = blockIdx.x * (blockDim.x >> 6) + wave;
-  const int row = row_raw < M ? row_raw : M - 1;  // clamp: keep waves alive for the barrier
-  const int nck = K >> 5;
-  const int G = K >> 7;
-  const uint4* rw = packed + (size_t)row * nck;
-  const uint16_t* rs = scales + (size_t)row * G;
-  const uint16_t* sc = rs;
-  if (kScalesInLds) {
-    uint16_t* mine = lds_scales + wave * G;
-    for (int g = lane; g < G; g += kWave) mine[g] = rs[g];
-    __syncthreads();
-    sc = mine;
-  }
-  for (int b = 0; b < B; ++b) {
-    const uint4* xb = x4 + (size_t)b * (K >> 3);
-    float acc = 0.f;
-    for (int c = lane; c < nck; c += kWave) {
-      const uint4 w = rw[c];
-      float part = 0.f;
-      h2_t xp[4];
-      pair_x(xb[4 * c + 0], xp);
-      part = dot_word(w.x, xp, part);
-      pair_x(xb[4 * c + 1], xp);
-      part = dot_word(w.y, xp, part);
-      pair_x(xb[4 * c + 2], xp);
-      part = dot_word(w.z, xp, part);
-      pair_x(xb[4 * c + 3], xp);
-      part = dot_word(w.w, xp, part);
-      acc += h2f(sc[c >> 2]) * part;
-    }
-    acc = wave_sum(acc);
-    if (lane == 63 && row_raw < M) y[(size_t)b * M + row] = f2h(acc);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// v5: the tuned streaming kernel. Each wave owns R consecutive rows; lane l
-// owns 16-byte chunks l, l+64, ... of every one of them. All loads of a stage
-// (U chunks x R rows of weights, their scales, and the U x NB activation
-// chunks) are issued before any math, activations are paired once per stage
-// and reused for all R rows, and with kPipe the next stage's loads are in
-// flight while the current one is decoded. NB batch rows per launch tile
-// (grid.y covers B). Reference: csrc/gemv_w4a16.cu:318-357.
-// ---------------------------------------------------------------------------
-template <int R, int U, int NB>
-struct V5Stage {
-  uint4 w[U][R];
-  float s[U][R];
-  uint4 xv[U][NB][4];
-};
-
-template <int R, int U, int NB>
-__device__ __forceinline__ void v5_load(V5Stage<R, U, NB>& st, const uint4* const (&rw)[R],
-                                        const uint16_t* const (&rs)[R],
-                                        const uint4* const (&xb)[NB], int c0, int nck, int lane) {
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int c = c0 + u * kWave + lane;
-    const bool ok = c < nck;
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) st.xv[u][b][j] = ok ? xb[b][4 * c + j] : zero4();
-#pragma unroll
-    for (int r = 0; r < R; ++r) st.s[u][r] = ok ? h2f(rs[r][c >> 2]) : 0.f;
-#pragma unroll
-    for (int r = 0; r < R; ++r) st.w[u][r] = ok ? rw[r][c] : zero4();
-  }
-}
-
-template <int R, int U, int NB>
-__device__ __forceinline__ void v5_compute(const V5Stage<R, U, NB>& st, float (&acc)[NB][R]) {
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    h2_t xp[NB][4][4];
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) pair_x(st.xv[u][b][j], xp[b][j]);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const uint32_t words[4] = {st.w[u][r].x, st.w[u][r].y, st.w[u][r].z, st.w[u][r].w};
-      float part[NB];
-#pragma unroll
-      for (int b = 0; b < NB; ++b) part[b] = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        h2_t q[4];
-        unpack_word(words[j], q);
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          part[b] = __builtin_amdgcn_fdot2(q[0], xp[b][j][0], part[b], false);
-          part[b] = __builtin_amdgcn_fdot2(q[1], xp[b][j][1], part[b], false);
-          part[b] = __builtin_amdgcn_fdot2(q[2], xp[b][j][2], part[b], false);
-          part[b] = __builtin_amdgcn_fdot2(q[3], xp[b][j][3], part[b], false);
-        }
-      }
-#pragma unroll
-      for (int b = 0; b < NB; ++b) acc[b][r] = __builtin_fmaf(part[b], st.s[u][r], acc[b][r]);
-    }
-  }
-}
-
-template <int R, int U, int NB, bool kPipe>
-__global__ __launch_bounds__(256) void gemv_v5(const uint4* __restrict__ packed,
-                                               const uint16_t* __restrict__ scales,
-                                               const uint4* __restrict__ x4,
-                                               uint16_t* __restrict__ y, int M, int K, int B) {
-  write_stamp(5);
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int row0 = (blockIdx.x * (blockDim.x >> 6) + wave) * R;
-  if (row0 >= M) return;  // wave-uniform; no barriers in this kernel
-  const int b0 = blockIdx.y * NB;
-  const int nck = K >> 5;
-  const int G = K >> 7;
-  const int xstride = K >> 3;
-
-  const uint4* rw[R];
-  const uint16_t* rs[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int row = min(row0 + r, M - 1);
-    rw[r] = packed + (size_t)row * nck;
-    rs[r] = scales + (size_t)row * G;
-  }
-  const uint4* xb[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) xb[b] = x4 + (size_t)min(b0 + b, B - 1) * xstride;
-
-  float acc[NB][R];
-#pragma unroll
-  for (int b = 0; b < NB; ++b)
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[b][r] = 0.f;
-
-  constexpr int kStep = U * kWave;
-  V5Stage<R, U, NB> sa, sb;
-  if (kPipe) {
-    v5_load(sa, rw, rs, xb, 0, nck, lane);
-    for (int c0 = 0;;) {
-      bool more = c0 + kStep < nck;
-      if (more) v5_load(sb, rw, rs, xb, c0 + kStep, nck, lane);
-      v5_compute(sa, acc);
-      if (!more) break;
-      c0 += kStep;
-      more = c0 + kStep < nck;
-      if (more) v5_load(sa, rw, rs, xb, c0 + kStep, nck, lane);
-      v5_compute(sb, acc);
-      if (!more) break;
-      c0 += kStep;
-    }
-  } else {
-    for (int c0 = 0; c0 < nck; c0 += kStep) {
-      v5_load(sa, rw, rs, xb, c0, nck, lane);
-      v5_compute(sa, acc);
-    }
-  }
-
-#pragma unroll
-  for (int b = 0; b < NB; ++b)
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float t = wave_sum(acc[b][r]);
-      if (lane == 63 && row0 + r < M && b0 + b < B) y[(size_t)(b0 + b) * M + row0 + r] = f2h(t);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// v4: split-K. grid = (row tiles of 4, S). Workgroup (tile, s) computes the
-// fp32 partial of its 4 rows over group slice s and stores it to
-// ws[s][b][row]; the last workgroup of a tile to finish (agent-scope ticket)
-// adds the S partials in slice order and writes fp16 y. One launch, no
-// memset, deterministic. Reference: csrc/gemv_w4a16.cu:264-313, 415-419.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
-                                               const uint16_t* __restrict__ scales,
-                                               const uint4* __restrict__ x4,
-                                               uint16_t* __restrict__ y, float* __restrict__ ws,
-                                               int M, int K, int B) {
-  write_stamp(4);
-  __shared__ int last;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int rows_per_tile = blockDim.x >> 6;
-  const int tile = blockIdx.x;
-  const int row_raw = tile * rows_per_tile + wave;
-  const int row = row_raw < M ? row_raw : M - 1;
-  const int S = gridDim.y;
-  const int split = blockIdx.y;
-  const int G = K >> 7;
-  const int gps = (G + S - 1) / S;
-  const int g0 = min(split * gps, G);
-  const int g1 = min(g0 + gps, G);
-  const int nck = K >> 5;
-  const uint4* rw = packed + (size_t)row * nck;
-  const uint16_t* rs = scales + (size_t)row * G;
-
-  for (int b = 0; b < B; ++b) {
-    const uint4* xb = x4 + (size_t)b * (K >> 3);
-    float acc = 0.f;
-    for (int c = 4 * g0 + lane; c < 4 * g1; c += kWave) {
-      const uint4 w = rw[c];
-      float part = 0.f;
-      h2_t xp[4];
-      pair_x(xb[4 * c + 0], xp);
-      part = dot_word(w.x, xp, part);
-      pair_x(xb[4 * c + 1], xp);
-      part = dot_word(w.y, xp, part);
-      pair_x(xb[4 * c + 2], xp);
-      part = dot_word(w.z, xp, part);
-      pair_x(xb[4 * c + 3], xp);
-      part = dot_word(w.w, xp, part);
-      acc += h2f(rs[c >> 2]) * part;
-    }
-    acc = wave_sum(acc);
-    if (lane == 63 && row_raw < M) ws[((size_t)split * B + b) * M + row] = acc;
-  }
-
-  // Publish this slice, then take a ticket; the last arriver reduces.
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev =
-        __hip_atomic_fetch_add(&g_tickets[tile], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    last = (prev == (unsigned)(S - 1));
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  const int row_base = tile * rows_per_tile;
-  const int n_out = rows_per_tile * B;
-  for (int t = threadIdx.x; t < n_out; t += blockDim.x) {
-    const int r = row_base + (t % rows_per_tile);
-    const int b = t / rows_per_tile;
-    if (r >= M) continue;
-    float sum = 0.f;
-    for (int s = 0; s < S; ++s)
-      sum += ws[((size_t)s * B + b) * M + r];
-    y[(size_t)b * M + r] = f2h(sum);
-  }
-  if (threadIdx.x == 0)
-    __hip_atomic_store(&g_tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// ---------------------------------------------------------------------------
-// Weight-reuse path (stamp 15): each decoded weight is used for up to 16
-// batch rows at once by v_mfma_f32_16x16x32_f16, so latency is flat in B
-// instead of the reference's O(B) re-decode (csrc/gemv_w4a16.cu:364-413).
-// A workgroup of kKs waves owns one 16-row tile; wave w takes groups w,
-// w+kKs, ... (adjacent groups stream side by side). Lane l loads row l%16,
-// bytes [64g + 16(l/16), +16) of group g: four words = four MFMA k-steps
-// that together cover exactly group g, so the fp32 tile result of a group is
-// scaled once (scales staged transposed in LDS) and accumulated. The kKs
-// wave partials are added in LDS in wave order.
-//   A (16x32, weights): lane l -> row l%16, 8 k-slots of lane group l/16
-//   B (32x16, x):       lane l -> batch l%16, same 8 k-slots
-//   D (16x16):          lane l -> rows 4(l/16)+v, batch l%16
-// ---------------------------------------------------------------------------
-constexpr int kReuseWaves = 4;
-constexpr int kReuseBatch = 16;
-
-template <int P>
-__global__ __launch_bounds__(kReuseWaves * 64) void gemv_reuse(
-    const uint4* __restrict__ packed, const uint16_t* __restrict__ scales,
-    const uint4* __restrict__ x4, uint16_t* __restrict__ y, int M, int K, int B) {
-  write_stamp(DK_STAMP_REUSE);
-  extern __shared__ float lds_reuse[];
-  const int G = K >> 7;
-  float* red = lds_reuse;                                                 // [waves][64][4]
-  uint16_t* sT = reinterpret_cast<uint16_t*>(lds_reuse + kReuseWaves * 256);  // [G][16]
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int row0 = blockIdx.x * 16;
-  const int b0 = blockIdx.y * kReuseBatch;
-  const int nck = K >> 5;
-
-  // Stage the tile's scales transposed: sT[g][r] = scales[row0 + r][g].
-  for (int e = threadIdx.x; e < 16 * G; e += blockDim.x) {
-    const int r = e / G, g = e - r * G;
-    const int row = min(row0 + r, M - 1);
-    sT[g * 16 + r] = scales[(size_t)row * G + g];
-  }
-  __syncthreads();
-
-  const int r_lane = lane & 15;   // A row / B batch column
-  const int kq = lane >> 4;       // lane group: 16-byte quarter of a group
-  const int row = min(row0 + r_lane, M - 1);
-  const uint4* rw = packed + (size_t)row * nck + kq;
-  const int b = b0 + r_lane;
-  const bool bok = b < B;
-  const uint4* xb = x4 + (size_t)(bok ? b : 0) * (K >> 3) + 4 * kq;
-
-  f4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int g0 = wave; g0 < G; g0 += kReuseWaves * P) {
-    uint4 w[P];
-    uint4 xv[P][4];
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int g = g0 + p * kReuseWaves;
-      const bool ok = g < G;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) xv[p][j] = (ok && bok) ? xb[16 * g + j] : zero4();
-      w[p] = ok ? rw[4 * g] : zero4();  // word 0 decodes to q = 0
-    }
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int g = g0 + p * kReuseWaves;
-      if (g >= G) break;
-      const uint32_t words[4] = {w[p].x, w[p].y, w[p].z, w[p].w};
-      f4_t c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_word_h8(words[j]), pair_x8(xv[p][j]), c,
-                                                   0, 0, 0);
-      const uint2 s4 = *reinterpret_cast<const uint2*>(sT + g * 16 + 4 * kq);
-      acc[0] = __builtin_fmaf(c[0], h2f((uint16_t)(s4.x & 0xFFFFu)), acc[0]);
-      acc[1] = __builtin_fmaf(c[1], h2f((uint16_t)(s4.x >> 16)), acc[1]);
-      acc[2] = __builtin_fmaf(c[2], h2f((uint16_t)(s4.y & 0xFFFFu)), acc[2]);
-      acc[3] = __builtin_fmaf(c[3], h2f((uint16_t)(s4.y >> 16)), acc[3]);
-    }
-  }
-
-  // Cross-wave reduction of the 16x16 tile, in wave order.
-#pragma unroll
-  for (int v = 0; v < 4; ++v) red[(wave * 64 + lane) * 4 + v] = acc[v];
-  __syncthreads();
-  if (wave == 0) {
-    f4_t t = {0.f, 0.f, 0.f, 0.f};
-    for (int w = 0; w < kReuseWaves; ++w)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) t[v] += red[(w * 64 + lane) * 4 + v];
-    if (bok) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int orow = row0 + 4 * kq + v;
-        if (orow < M) y[(size_t)b * M + orow] = f2h(t[v]);
-      }
-    }
-  }
-}
-
-}  // namespace dk
 
 // ===========================================================================
 // Host side: validation, launch selection and the C ABI.
@@ -531,7 +50,6 @@ int check_launch(const char* what) {
 
 namespace {
 
-using dk::check_launch;
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -542,43 +60,63 @@ int fail(int code, const char* fmt, ...) {
   return dk::set_error(code, "%s", buf);
 }
 
-int hip_fail(hipError_t e, const char* what) { return dk::hip_error(e, what); }
-
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-constexpr int kV5Waves = 4;
+constexpr int kWavesPerBlock = 4;
 constexpr int kV4RowsPerTile = 4;
 
 int clamp_wpr(int wpr) { return std::max(2, std::min(wpr, 8)); }
 
 int lds_limit_bytes() { return 64 * 1024; }
 
+// Launches one kernel on `stream` and reports a launch error as DK_ERR_HIP.
+struct Launch {
+  hipStream_t stream;
+
+  template <typename... KArgs, typename... Args>
+  int operator()(const char* what, void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds,
+                 Args... args) const {
+    hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+    return dk::check_launch(what);
+  }
+};
+
+// v5 stage shapes (R rows per wave, U 16-byte chunks per lane per stage,
+// double-buffered stages or not), chosen from a sweep on MI355X of
+// back-to-back launches over cold weights, B = 1:
+//   M = 4096  (K = 4096, 11008):  one row per wave, no double buffering
+//   M = 11008, K = 4096; M = 28672, K = 8192: two rows per wave
+//   M = 8192, K = 28672: two rows per wave, double-buffered stages
+// Fewer rows per wave keep more waves in flight when rows are few; two rows
+// halve the activation loads once there are enough rows to fill the chip.
+// Larger batch tiles keep more activation registers live and take fewer rows.
 template <int R, int U, int NB, bool kPipe>
-hipError_t launch_v5_t(const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y, int M, int K,
-                       int B, hipStream_t st) {
-  const int rows_per_block = kV5Waves * R;
+int launch_v5_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
+                int M, int K, int B) {
+  const int rows_per_block = kWavesPerBlock * R;
   dim3 grid((M + rows_per_block - 1) / rows_per_block, (B + NB - 1) / NB);
-  hipLaunchKernelGGL((dk::gemv_v5<R, U, NB, kPipe>), grid, dim3(kV5Waves * 64), 0, st, p, s, x, y,
-                     M, K, B);
-  return hipGetLastError();
+  return L("v5 launch", dk::gemv_v5<R, U, NB, kPipe>, grid, dim3(kWavesPerBlock * 64), 0, p, s, x,
+           y, M, K, B);
 }
 
-// Stage shapes per batch tile: (R rows per wave, U chunks per lane per
-// stage). Larger NB keeps more activation registers live, so it takes fewer
-// rows and chunks; stages are double-buffered once a row needs more than one.
 template <int R, int U, int NB>
-hipError_t launch_v5_shape(const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y, int M,
-                           int K, int B, hipStream_t st) {
-  const int nck = K / 32;
-  if (nck <= U * 64) return launch_v5_t<R, U, NB, false>(p, s, x, y, M, K, B, st);
-  return launch_v5_t<R, U, NB, true>(p, s, x, y, M, K, B, st);
+int launch_v5_shape(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
+                    int M, int K, int B) {
+  if (K / 32 <= U * 64) return launch_v5_t<R, U, NB, false>(L, p, s, x, y, M, K, B);
+  return launch_v5_t<R, U, NB, true>(L, p, s, x, y, M, K, B);
 }
 
-hipError_t launch_v5(const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y, int M, int K,
-                     int B, hipStream_t st) {
-  if (B == 1) return launch_v5_shape<4, 2, 1>(p, s, x, y, M, K, B, st);
-  if (B == 2) return launch_v5_shape<4, 1, 2>(p, s, x, y, M, K, B, st);
-  return launch_v5_shape<2, 1, 4>(p, s, x, y, M, K, B, st);
+int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y, int M,
+              int K, int B) {
+  if (B == 1) {
+    if (M >= 8192) {
+      if (K > 16384) return launch_v5_t<2, 1, 1, true>(L, p, s, x, y, M, K, B);
+      return launch_v5_t<2, 1, 1, false>(L, p, s, x, y, M, K, B);
+    }
+    return launch_v5_t<1, 1, 1, false>(L, p, s, x, y, M, K, B);
+  }
+  if (B == 2) return launch_v5_shape<4, 1, 2>(L, p, s, x, y, M, K, B);
+  return launch_v5_shape<2, 1, 4>(L, p, s, x, y, M, K, B);
 }
 
 size_t reuse_lds_bytes(int K) {
@@ -586,11 +124,70 @@ size_t reuse_lds_bytes(int K) {
   return (size_t)dk::kReuseWaves * 256 * sizeof(float) + (size_t)16 * G * sizeof(uint16_t);
 }
 
-size_t v3_lds_bytes(int K) { return (size_t)kV5Waves * (K / DK_GROUP_SIZE) * sizeof(uint16_t); }
+size_t v3_lds_bytes(int K) { return (size_t)kWavesPerBlock * (K / DK_GROUP_SIZE) * sizeof(uint16_t); }
 
 int effective_split(int K, int split_k) {
   const int G = K / DK_GROUP_SIZE;
   return std::max(1, std::min(split_k, G));
+}
+
+int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x, uint16_t* y, int M,
+              int K, int B, const dk_gemv_config* cfg, void* workspace, size_t workspace_bytes,
+              const Launch& L) {
+  int rc = dk_gemv_validate(M, K, B, cfg);
+  if (rc != DK_OK) return rc;
+  if (M <= 0 || K <= 0 || B <= 0) return DK_OK;
+  if (!packed || !scales || !x || !y)
+    return fail(DK_ERR_INVALID_ARGUMENT, "packed, scales, x and y must not be NULL");
+  if (!aligned(packed, 16) || !aligned(x, 16))
+    return fail(DK_ERR_INVALID_ARGUMENT, "packed and x must be 16-byte aligned");
+  if (!aligned(scales, 2) || !aligned(y, 2))
+    return fail(DK_ERR_INVALID_ARGUMENT, "scales and y must be 2-byte aligned");
+  const size_t need = dk_gemv_workspace_bytes(M, K, B, cfg);
+  if (need > 0) {
+    if (!workspace || workspace_bytes < need)
+      return fail(DK_ERR_INVALID_ARGUMENT, "split-K needs a %zu-byte workspace (got %zu)", need,
+                  workspace_bytes);
+    if (!aligned(workspace, 4)) return fail(DK_ERR_INVALID_ARGUMENT, "workspace must be 4-byte aligned");
+  }
+
+  const uint4* p4 = reinterpret_cast<const uint4*>(packed);
+  const uint4* x4 = reinterpret_cast<const uint4*>(x);
+
+  if (cfg->reuse_weights) {
+    dim3 grid((M + 15) / 16, (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
+    return L("reuse launch", dk::gemv_reuse<2>, grid, dim3(dk::kReuseWaves * 64), reuse_lds_bytes(K),
+             p4, scales, x4, y, M, K, B);
+  }
+  const dim3 block4(kWavesPerBlock * 64);
+  const dim3 rows4((M + kWavesPerBlock - 1) / kWavesPerBlock);
+  switch (cfg->version) {
+    case DK_V0:
+      return L("v0 launch", dk::gemv_v0, dim3((M + 255) / 256), dim3(256), 0, packed, scales, x, y,
+               M, K, B);
+    case DK_V1:
+      if (cfg->warps_per_row > 1) {
+        const int wpr = clamp_wpr(cfg->warps_per_row);
+        return L("v1 multiwave launch", dk::gemv_v1_multiwave, dim3(M), dim3(wpr * 64), 0, packed,
+                 scales, x4, y, M, K, B);
+      }
+      return L("v1 launch", dk::gemv_v1, rows4, block4, 0, packed, scales, x4, y, M, K, B);
+    case DK_V2:
+      return L("v2 launch", dk::gemv_v23<false>, rows4, block4, 0, p4, scales, x4, y, M, K, B);
+    case DK_V3:
+      return L("v3 launch", dk::gemv_v23<true>, rows4, block4, v3_lds_bytes(K), p4, scales, x4, y,
+               M, K, B);
+    case DK_V4: {
+      const int S = effective_split(K, cfg->split_k);
+      dim3 grid((M + kV4RowsPerTile - 1) / kV4RowsPerTile, S);
+      return L("v4 launch", dk::gemv_v4, grid, dim3(kV4RowsPerTile * 64), 0, p4, scales, x4, y,
+               static_cast<float*>(workspace), M, K, B);
+    }
+    case DK_V5:
+      return launch_v5(L, p4, scales, x4, y, M, K, B);
+    default:
+      return fail(DK_ERR_INVALID_ARGUMENT, "unknown version %d", cfg->version);
+  }
 }
 
 }  // namespace
@@ -644,90 +241,25 @@ size_t dk_gemv_workspace_bytes(int M, int K, int B, const dk_gemv_config* cfg) {
 int dk_w4a16_gemv(const uint32_t* packed, const uint16_t* scales, const uint16_t* x, uint16_t* y,
                   int M, int K, int B, const dk_gemv_config* cfg, void* workspace,
                   size_t workspace_bytes, hipStream_t stream) {
-  int rc = dk_gemv_validate(M, K, B, cfg);
-  if (rc != DK_OK) return rc;
-  if (M <= 0 || K <= 0 || B <= 0) return DK_OK;
-  if (!packed || !scales || !x || !y)
-    return fail(DK_ERR_INVALID_ARGUMENT, "packed, scales, x and y must not be NULL");
-  if (!aligned(packed, 16) || !aligned(x, 16))
-    return fail(DK_ERR_INVALID_ARGUMENT, "packed and x must be 16-byte aligned");
-  if (!aligned(scales, 2) || !aligned(y, 2))
-    return fail(DK_ERR_INVALID_ARGUMENT, "scales and y must be 2-byte aligned");
-  const size_t need = dk_gemv_workspace_bytes(M, K, B, cfg);
-  if (need > 0) {
-    if (!workspace || workspace_bytes < need)
-      return fail(DK_ERR_INVALID_ARGUMENT, "split-K needs a %zu-byte workspace (got %zu)", need,
-                  workspace_bytes);
-    if (!aligned(workspace, 4)) return fail(DK_ERR_INVALID_ARGUMENT, "workspace must be 4-byte aligned");
-  }
-
-  const uint4* p4 = reinterpret_cast<const uint4*>(packed);
-  const uint4* x4 = reinterpret_cast<const uint4*>(x);
-  hipError_t e = hipSuccess;
-
-  if (cfg->reuse_weights) {
-    dim3 grid((M + 15) / 16, (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
-    hipLaunchKernelGGL(dk::gemv_reuse<2>, grid, dim3(dk::kReuseWaves * 64), reuse_lds_bytes(K),
-                       stream, p4, scales, x4, y, M, K, B);
-    return check_launch("reuse launch");
-  }
-
-  switch (cfg->version) {
-    case DK_V0:
-      hipLaunchKernelGGL(dk::gemv_v0, dim3((M + 255) / 256), dim3(256), 0, stream, packed, scales, x,
-                         y, M, K, B);
-      break;
-    case DK_V1:
-      if (cfg->warps_per_row > 1) {
-        const int wpr = clamp_wpr(cfg->warps_per_row);
-        hipLaunchKernelGGL(dk::gemv_v1_multiwave, dim3(M), dim3(wpr * 64), 0, stream, packed, scales,
-                           x4, y, M, K, B);
-      } else {
-        hipLaunchKernelGGL(dk::gemv_v1, dim3((M + 3) / 4), dim3(256), 0, stream, packed, scales, x4,
-                           y, M, K, B);
-      }
-      break;
-    case DK_V2:
-      hipLaunchKernelGGL(dk::gemv_v23<false>, dim3((M + 3) / 4), dim3(256), 0, stream, p4, scales, x4,
-                         y, M, K, B);
-      break;
-    case DK_V3:
-      hipLaunchKernelGGL(dk::gemv_v23<true>, dim3((M + 3) / 4), dim3(256), v3_lds_bytes(K), stream,
-                         p4, scales, x4, y, M, K, B);
-      break;
-    case DK_V4: {
-      const int S = effective_split(K, cfg->split_k);
-      dim3 grid((M + kV4RowsPerTile - 1) / kV4RowsPerTile, S);
-      hipLaunchKernelGGL(dk::gemv_v4, grid, dim3(kV4RowsPerTile * 64), 0, stream, p4, scales, x4, y,
-                         static_cast<float*>(workspace), M, K, B);
-      break;
-    }
-    case DK_V5:
-      e = launch_v5(p4, scales, x4, y, M, K, B, stream);
-      if (e != hipSuccess) return hip_fail(e, "v5 launch");
-      return DK_OK;
-    default:
-      return fail(DK_ERR_INVALID_ARGUMENT, "unknown version %d", cfg->version);
-  }
-  return check_launch("gemv launch");
+  return gemv_impl(packed, scales, x, y, M, K, B, cfg, workspace, workspace_bytes, Launch{stream});
 }
 
 int dk_last_kernel_stamp(void) {
   hipError_t e = hipDeviceSynchronize();
   if (e != hipSuccess) {
-    hip_fail(e, "hipDeviceSynchronize");
+    dk::hip_error(e, "hipDeviceSynchronize");
     return -1;
   }
   int h = -1;
   e = hipMemcpyFromSymbol(&h, HIP_SYMBOL(dk::g_stamp), sizeof(int), 0, hipMemcpyDeviceToHost);
   if (e != hipSuccess) {
-    hip_fail(e, "read stamp");
+    dk::hip_error(e, "read stamp");
     return -1;
   }
   const int neg = -1;
   e = hipMemcpyToSymbol(HIP_SYMBOL(dk::g_stamp), &neg, sizeof(int), 0, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
-    hip_fail(e, "clear stamp");
+    dk::hip_error(e, "clear stamp");
     return -1;
   }
   return h;

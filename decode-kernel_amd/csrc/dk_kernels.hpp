@@ -1,0 +1,505 @@
+// Every W4A16 GEMV kernel for gfx950, as templates and __global__ functions.
+// Included by exactly one translation unit of the library (dk_gemv.hip),
+// which owns the __device__ globals defined here (dispatch stamp and split-K
+// tickets).
+//
+// Layout in HBM (the reference format, no repacking):
+//   packed uint32 [M, K/8]: row m is K/2 bytes; 16-byte chunk c of a row holds
+//                           weights k = 32c .. 32c+31 (4 words, low nibble first)
+//   scales fp16  [M, K/128]: chunk c of row m uses scales[m, c/4]
+//   x      fp16  [B, K], y fp16 [B, M]
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "dk_device.hpp"
+#include "decode_kernel/dk_gemv.h"
+
+namespace dk {
+
+// ---------------------------------------------------------------------------
+// Dispatch stamp: written by block (0,0) thread 0 of whichever GEMV kernel
+// ran. Host reads and clears it in dk_last_kernel_stamp().
+// Reference: csrc/gemv_w4a16.cu:18-25.
+// ---------------------------------------------------------------------------
+__device__ int g_stamp = -1;
+
+__device__ __forceinline__ void write_stamp(int s) {
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) g_stamp = s;
+}
+
+// Split-K completion tickets, one per row tile. Zero at load; the last
+// workgroup of a tile resets its ticket, so they are zero between launches.
+constexpr int kMaxTickets = 1 << 16;
+__device__ unsigned int g_tickets[kMaxTickets];
+
+// ---------------------------------------------------------------------------
+// v0: one thread per row, scalar decode (the uncoalesced baseline stage).
+// Reference: csrc/gemv_w4a16.cu:70-94.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gemv_v0(const uint32_t* __restrict__ packed,
+                                               const uint16_t* __restrict__ scales,
+                                               const uint16_t* __restrict__ x,
+                                               uint16_t* __restrict__ y, int M, int K, int B) {
+  write_stamp(0);
+  const int row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= M) return;
+  const int words = K >> 3;
+  const int G = K >> 7;
+  const uint32_t* rw = packed + (size_t)row * words;
+  const uint16_t* rs = scales + (size_t)row * G;
+  for (int b = 0; b < B; ++b) {
+    const uint16_t* xb = x + (size_t)b * K;
+    float acc = 0.f;
+    for (int i = 0; i < words; ++i) {
+      const uint32_t w = rw[i];
+      const float s = h2f(rs[i >> 4]);
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        const int q = (int)(w << (28 - 4 * n)) >> 28;
+        acc += s * (float)q * h2f(xb[8 * i + n]);
+      }
+    }
+    y[(size_t)b * M + row] = f2h(acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// v1: one wave64 per row; lane l reads words l, l+64, ... (256 contiguous
+// bytes per wave instruction); one 16-byte x load per word.
+// Reference: csrc/gemv_w4a16.cu:99-128.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gemv_v1(const uint32_t* __restrict__ packed,
+                                               const uint16_t* __restrict__ scales,
+                                               const uint4* __restrict__ x4,
+                                               uint16_t* __restrict__ y, int M, int K, int B) {
+  write_stamp(1);
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int words = K >> 3;
+  const int G = K >> 7;
+  const uint32_t* rw = packed + (size_t)row * words;
+  const uint16_t* rs = scales + (size_t)row * G;
+  for (int b = 0; b < B; ++b) {
+    const uint4* xb = x4 + (size_t)b * words;
+    float acc = 0.f;
+    for (int i = lane; i < words; i += kWave) {
+      h2_t xp[4];
+      pair_x(xb[i], xp);
+      acc += h2f(rs[i >> 4]) * dot_word(rw[i], xp, 0.f);
+    }
+    acc = wave_sum(acc);
+    if (lane == 63) y[(size_t)b * M + row] = f2h(acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// v1 with K split over `wpr` waves of one workgroup per row, LDS reduction in
+// wave order. Stamp 10 + wpr. Reference: csrc/gemv_w4a16.cu:134-172.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(512) void gemv_v1_multiwave(const uint32_t* __restrict__ packed,
+                                                         const uint16_t* __restrict__ scales,
+                                                         const uint4* __restrict__ x4,
+                                                         uint16_t* __restrict__ y, int M, int K,
+                                                         int B) {
+  const int wpr = blockDim.x >> 6;
+  write_stamp(10 + wpr);
+  __shared__ float red[8];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row = blockIdx.x;  // grid is exactly M
+  const int words = K >> 3;
+  const int G = K >> 7;
+  const uint32_t* rw = packed + (size_t)row * words;
+  const uint16_t* rs = scales + (size_t)row * G;
+  for (int b = 0; b < B; ++b) {
+    const uint4* xb = x4 + (size_t)b * words;
+    float acc = 0.f;
+    for (int i = wave * kWave + lane; i < words; i += wpr * kWave) {
+      h2_t xp[4];
+      pair_x(xb[i], xp);
+      acc += h2f(rs[i >> 4]) * dot_word(rw[i], xp, 0.f);
+    }
+    acc = wave_sum(acc);
+    if (lane == 63) red[wave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float t = 0.f;
+      for (int w = 0; w < wpr; ++w) t += red[w];
+      y[(size_t)b * M + row] = f2h(t);
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// v2 / v3: one wave64 per row with 16-byte loads (32 weights per lane per
+// load, 1 KiB per wave instruction). v3 stages the row's group scales in LDS.
+// Reference: csrc/gemv_w4a16.cu:183-257.
+// ---------------------------------------------------------------------------
+template <bool kScalesInLds>
+__global__ __launch_bounds__(256) void gemv_v23(const uint4* __restrict__ packed,
+                                                const uint16_t* __restrict__ scales,
+                                                const uint4* __restrict__ x4,
+                                                uint16_t* __restrict__ y, int M, int K, int B) {
+  write_stamp(kScalesInLds ? 3 : 2);
+  extern __shared__ uint16_t lds_scales[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row_raw = blockIdx.x * (blockDim.x >> 6) + wave;
+  const int row = row_raw < M ? row_raw : M - 1;  // clamp: keep waves alive for the barrier
+  const int nck = K >> 5;
+  const int G = K >> 7;
+  const uint4* rw = packed + (size_t)row * nck;
+  const uint16_t* rs = scales + (size_t)row * G;
+  const uint16_t* sc = rs;
+  if (kScalesInLds) {
+    uint16_t* mine = lds_scales + wave * G;
+    for (int g = lane; g < G; g += kWave) mine[g] = rs[g];
+    __syncthreads();
+    sc = mine;
+  }
+  for (int b = 0; b < B; ++b) {
+    const uint4* xb = x4 + (size_t)b * (K >> 3);
+    float acc = 0.f;
+    for (int c = lane; c < nck; c += kWave) {
+      const uint4 w = rw[c];
+      float part = 0.f;
+      h2_t xp[4];
+      pair_x(xb[4 * c + 0], xp);
+      part = dot_word(w.x, xp, part);
+      pair_x(xb[4 * c + 1], xp);
+      part = dot_word(w.y, xp, part);
+      pair_x(xb[4 * c + 2], xp);
+      part = dot_word(w.z, xp, part);
+      pair_x(xb[4 * c + 3], xp);
+      part = dot_word(w.w, xp, part);
+      acc += h2f(sc[c >> 2]) * part;
+    }
+    acc = wave_sum(acc);
+    if (lane == 63 && row_raw < M) y[(size_t)b * M + row] = f2h(acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// v5: the tuned streaming kernel. Each wave owns R consecutive rows; lane l
+// owns 16-byte chunks l, l+64, ... of every one of them. All loads of a stage
+// (U chunks x R rows of weights, their scales, and the U x NB activation
+// chunks) are issued before any math, activations are paired once per stage
+// and reused for all R rows, and with kPipe the next stage's loads are in
+// flight while the current one is decoded. NB batch rows per launch tile
+// (grid.y covers B). Reference: csrc/gemv_w4a16.cu:318-357.
+// ---------------------------------------------------------------------------
+template <int R, int U, int NB>
+struct V5Stage {
+  uint4 w[U][R];
+  float s[U][R];
+  uint4 xv[U][NB][4];
+};
+
+template <int R, int U, int NB>
+__device__ __forceinline__ void v5_load(V5Stage<R, U, NB>& st, const uint4* const (&rw)[R],
+                                        const uint16_t* const (&rs)[R],
+                                        const uint4* const (&xb)[NB], int c0, int nck, int lane) {
+  // Activations first, then scales, then weights: pairing the activations
+  // only waits for their (L2-resident) loads and overlaps the weights' HBM
+  // latency; issuing the weights first measured slower on MI355X.
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = c0 + u * kWave + lane;
+    const bool ok = c < nck;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) st.xv[u][b][j] = ok ? xb[b][4 * c + j] : zero4();
+#pragma unroll
+    for (int r = 0; r < R; ++r) st.s[u][r] = ok ? h2f(rs[r][c >> 2]) : 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) st.w[u][r] = ok ? rw[r][c] : zero4();
+  }
+}
+
+template <int R, int U, int NB>
+__device__ __forceinline__ void v5_compute(const V5Stage<R, U, NB>& st, float (&acc)[NB][R]) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    h2_t xp[NB][4][4];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pair_x(st.xv[u][b][j], xp[b][j]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t words[4] = {st.w[u][r].x, st.w[u][r].y, st.w[u][r].z, st.w[u][r].w};
+      float part[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) part[b] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        h2_t q[4];
+        unpack_word(words[j], q);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          part[b] = __builtin_amdgcn_fdot2(q[0], xp[b][j][0], part[b], false);
+          part[b] = __builtin_amdgcn_fdot2(q[1], xp[b][j][1], part[b], false);
+          part[b] = __builtin_amdgcn_fdot2(q[2], xp[b][j][2], part[b], false);
+          part[b] = __builtin_amdgcn_fdot2(q[3], xp[b][j][3], part[b], false);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) acc[b][r] = __builtin_fmaf(part[b], st.s[u][r], acc[b][r]);
+    }
+  }
+}
+
+template <int R, int U, int NB, bool kPipe>
+__global__ __launch_bounds__(256) void gemv_v5(const uint4* __restrict__ packed,
+                                               const uint16_t* __restrict__ scales,
+                                               const uint4* __restrict__ x4,
+                                               uint16_t* __restrict__ y, int M, int K, int B) {
+  write_stamp(5);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = (blockIdx.x * (blockDim.x >> 6) + wave) * R;
+  if (row0 >= M) return;  // wave-uniform; no barriers in this kernel
+  const int b0 = blockIdx.y * NB;
+  const int nck = K >> 5;
+  const int G = K >> 7;
+  const int xstride = K >> 3;
+
+  const uint4* rw[R];
+  const uint16_t* rs[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int row = min(row0 + r, M - 1);
+    rw[r] = packed + (size_t)row * nck;
+    rs[r] = scales + (size_t)row * G;
+  }
+  const uint4* xb[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) xb[b] = x4 + (size_t)min(b0 + b, B - 1) * xstride;
+
+  float acc[NB][R];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[b][r] = 0.f;
+
+  constexpr int kStep = U * kWave;
+  V5Stage<R, U, NB> sa, sb;
+  if (kPipe) {
+    v5_load(sa, rw, rs, xb, 0, nck, lane);
+    for (int c0 = 0;;) {
+      bool more = c0 + kStep < nck;
+      if (more) v5_load(sb, rw, rs, xb, c0 + kStep, nck, lane);
+      v5_compute(sa, acc);
+      if (!more) break;
+      c0 += kStep;
+      more = c0 + kStep < nck;
+      if (more) v5_load(sa, rw, rs, xb, c0 + kStep, nck, lane);
+      v5_compute(sb, acc);
+      if (!more) break;
+      c0 += kStep;
+    }
+  } else {
+    for (int c0 = 0; c0 < nck; c0 += kStep) {
+      v5_load(sa, rw, rs, xb, c0, nck, lane);
+      v5_compute(sa, acc);
+    }
+  }
+
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float t = wave_sum(acc[b][r]);
+      if (lane == 63 && row0 + r < M && b0 + b < B) y[(size_t)(b0 + b) * M + row0 + r] = f2h(t);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// v4: split-K. grid = (row tiles of 4, S). Workgroup (tile, s) computes the
+// fp32 partial of its 4 rows over group slice s and stores it to
+// ws[s][b][row]; the last workgroup of a tile to finish adds the S partials
+// in slice order and writes fp16 y. One launch, no memset, deterministic.
+// Reference: csrc/gemv_w4a16.cu:264-313, 415-419 (memset + atomics + convert).
+//
+// Cross-workgroup visibility on an 8-XCD part (one L2 per XCD, not coherent
+// with each other) uses agent-scope atomic stores and loads for the partials
+// (they bypass the non-coherent L2s) and a wait for their completion before
+// the ticket, instead of agent-scope fences: a fence writes back and
+// invalidates a whole L2 per wave and made this kernel ~35x slower.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
+                                               const uint16_t* __restrict__ scales,
+                                               const uint4* __restrict__ x4,
+                                               uint16_t* __restrict__ y, float* __restrict__ ws,
+                                               int M, int K, int B) {
+  write_stamp(4);
+  __shared__ int last;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rows_per_tile = blockDim.x >> 6;
+  const int tile = blockIdx.x;
+  const int row_raw = tile * rows_per_tile + wave;
+  const int row = row_raw < M ? row_raw : M - 1;
+  const int S = gridDim.y;
+  const int split = blockIdx.y;
+  const int G = K >> 7;
+  const int gps = (G + S - 1) / S;
+  const int g0 = min(split * gps, G);
+  const int g1 = min(g0 + gps, G);
+  const int nck = K >> 5;
+  const uint4* rw = packed + (size_t)row * nck;
+  const uint16_t* rs = scales + (size_t)row * G;
+
+  for (int b = 0; b < B; ++b) {
+    const uint4* xb = x4 + (size_t)b * (K >> 3);
+    float acc = 0.f;
+    for (int c = 4 * g0 + lane; c < 4 * g1; c += kWave) {
+      const uint4 w = rw[c];
+      float part = 0.f;
+      h2_t xp[4];
+      pair_x(xb[4 * c + 0], xp);
+      part = dot_word(w.x, xp, part);
+      pair_x(xb[4 * c + 1], xp);
+      part = dot_word(w.y, xp, part);
+      pair_x(xb[4 * c + 2], xp);
+      part = dot_word(w.z, xp, part);
+      pair_x(xb[4 * c + 3], xp);
+      part = dot_word(w.w, xp, part);
+      acc += h2f(rs[c >> 2]) * part;
+    }
+    acc = wave_sum(acc);
+    if (lane == 63 && row_raw < M)
+      __hip_atomic_store(&ws[((size_t)split * B + b) * M + row], acc, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // Every wave's partial stores are complete before the ticket is taken.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev =
+        __hip_atomic_fetch_add(&g_tickets[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = (prev == (unsigned)(S - 1));
+  }
+  __syncthreads();
+  if (!last) return;
+  const int row_base = tile * rows_per_tile;
+  const int n_out = rows_per_tile * B;
+  for (int t = threadIdx.x; t < n_out; t += blockDim.x) {
+    const int r = row_base + (t % rows_per_tile);
+    const int b = t / rows_per_tile;
+    if (r >= M) continue;
+    float sum = 0.f;
+    for (int s = 0; s < S; ++s)
+      sum += __hip_atomic_load(&ws[((size_t)s * B + b) * M + r], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    y[(size_t)b * M + r] = f2h(sum);
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&g_tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// Weight-reuse path (stamp 15): each decoded weight is used for up to 16
+// batch rows at once by v_mfma_f32_16x16x32_f16, so latency is flat in B
+// instead of the reference's O(B) re-decode (csrc/gemv_w4a16.cu:364-413).
+// A workgroup of kKs waves owns one 16-row tile; wave w takes groups w,
+// w+kKs, ... (adjacent groups stream side by side). Lane l loads row l%16,
+// bytes [64g + 16(l/16), +16) of group g: four words = four MFMA k-steps
+// that together cover exactly group g, so the fp32 tile result of a group is
+// scaled once (scales staged transposed in LDS) and accumulated. The kKs
+// wave partials are added in LDS in wave order.
+//   A (16x32, weights): lane l -> row l%16, 8 k-slots of lane group l/16
+//   B (32x16, x):       lane l -> batch l%16, same 8 k-slots
+//   D (16x16):          lane l -> rows 4(l/16)+v, batch l%16
+// ---------------------------------------------------------------------------
+constexpr int kReuseWaves = 4;
+constexpr int kReuseBatch = 16;
+
+template <int P>
+__global__ __launch_bounds__(kReuseWaves * 64) void gemv_reuse(
+    const uint4* __restrict__ packed, const uint16_t* __restrict__ scales,
+    const uint4* __restrict__ x4, uint16_t* __restrict__ y, int M, int K, int B) {
+  write_stamp(DK_STAMP_REUSE);
+  extern __shared__ float lds_reuse[];
+  const int G = K >> 7;
+  float* red = lds_reuse;                                                 // [waves][64][4]
+  uint16_t* sT = reinterpret_cast<uint16_t*>(lds_reuse + kReuseWaves * 256);  // [G][16]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row0 = blockIdx.x * 16;
+  const int b0 = blockIdx.y * kReuseBatch;
+  const int nck = K >> 5;
+
+  // Stage the tile's scales transposed: sT[g][r] = scales[row0 + r][g].
+  for (int e = threadIdx.x; e < 16 * G; e += blockDim.x) {
+    const int r = e / G, g = e - r * G;
+    const int row = min(row0 + r, M - 1);
+    sT[g * 16 + r] = scales[(size_t)row * G + g];
+  }
+  __syncthreads();
+
+  const int r_lane = lane & 15;   // A row / B batch column
+  const int kq = lane >> 4;       // lane group: 16-byte quarter of a group
+  const int row = min(row0 + r_lane, M - 1);
+  const uint4* rw = packed + (size_t)row * nck + kq;
+  const int b = b0 + r_lane;
+  const bool bok = b < B;
+  const uint4* xb = x4 + (size_t)(bok ? b : 0) * (K >> 3) + 4 * kq;
+
+  f4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int g0 = wave; g0 < G; g0 += kReuseWaves * P) {
+    uint4 w[P];
+    uint4 xv[P][4];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int g = g0 + p * kReuseWaves;
+      const bool ok = g < G;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xv[p][j] = (ok && bok) ? xb[16 * g + j] : zero4();
+      w[p] = ok ? rw[4 * g] : zero4();  // word 0 decodes to q = 0
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int g = g0 + p * kReuseWaves;
+      if (g >= G) break;
+      const uint32_t words[4] = {w[p].x, w[p].y, w[p].z, w[p].w};
+      f4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_word_h8(words[j]), pair_x8(xv[p][j]), c,
+                                                   0, 0, 0);
+      const uint2 s4 = *reinterpret_cast<const uint2*>(sT + g * 16 + 4 * kq);
+      acc[0] = __builtin_fmaf(c[0], h2f((uint16_t)(s4.x & 0xFFFFu)), acc[0]);
+      acc[1] = __builtin_fmaf(c[1], h2f((uint16_t)(s4.x >> 16)), acc[1]);
+      acc[2] = __builtin_fmaf(c[2], h2f((uint16_t)(s4.y & 0xFFFFu)), acc[2]);
+      acc[3] = __builtin_fmaf(c[3], h2f((uint16_t)(s4.y >> 16)), acc[3]);
+    }
+  }
+
+  // Cross-wave reduction of the 16x16 tile, in wave order.
+#pragma unroll
+  for (int v = 0; v < 4; ++v) red[(wave * 64 + lane) * 4 + v] = acc[v];
+  __syncthreads();
+  if (wave == 0) {
+    f4_t t = {0.f, 0.f, 0.f, 0.f};
+    for (int w = 0; w < kReuseWaves; ++w)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) t[v] += red[(w * 64 + lane) * 4 + v];
+    if (bok) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int orow = row0 + 4 * kq + v;
+        if (orow < M) y[(size_t)b * M + orow] = f2h(t[v]);
+      }
+    }
+  }
+}
+
+}  // namespace dk
+

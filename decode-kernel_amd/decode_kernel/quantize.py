@@ -28,6 +28,21 @@ SCALE_FLOOR = 1e-8
 _NIBBLE_SHIFTS = tuple(range(0, 32, 4))
 
 
+def _div_fp32(a: torch.Tensor, b) -> torch.Tensor:
+    """Correctly rounded fp32 quotient a / b on any device.
+
+    torch's GPU kernels divide by a Python scalar as a multiplication by its
+    reciprocal, which can differ from IEEE fp32 division in the last bit and
+    then flip a rounded weight. Dividing in float64 and rounding to fp32 gives
+    the correctly rounded fp32 quotient (a double rounding 53 -> 24 bits is
+    innocuous for division of fp32 operands), so CPU and GPU tensors quantize
+    to the same bits.
+    """
+    den = b.double() if isinstance(b, torch.Tensor) else torch.tensor(
+        float(b), dtype=torch.float64, device=a.device)
+    return (a.double() / den).float()
+
+
 def quantize_and_pack(
     weight: torch.Tensor, group_size: int = GROUP_SIZE
 ) -> tuple[torch.Tensor, torch.Tensor]:
@@ -44,8 +59,8 @@ def quantize_and_pack(
         raise ValueError(f"K={k} is not divisible by {NIBBLES_PER_WORD}")
 
     groups = weight.float().reshape(m, k // group_size, group_size)
-    scale = (groups.abs().amax(dim=-1) / float(QMAX)).clamp_min(SCALE_FLOOR)
-    q = torch.round(groups / scale[..., None]).clamp_(QMIN, QMAX).to(torch.int32)
+    scale = _div_fp32(groups.abs().amax(dim=-1), float(QMAX)).clamp_min(SCALE_FLOOR)
+    q = torch.round(_div_fp32(groups, scale[..., None])).clamp_(QMIN, QMAX).to(torch.int32)
 
     # Nibble fields are disjoint, so an int32 sum of the shifted fields is
     # their bitwise OR (the top field wraps to the sign bit, as intended).

@@ -1,9 +1,13 @@
 """Shared benchmark helpers: HIP-event timer, cache flush, bytes and roofs.
 
 Restates bench/common.py of the reference for MI355X:
-  * time_gpu: events around exactly one call per iteration on the stream the
-    kernel runs on, a flush before each iteration outside the events, median
-    and IQR (bench/common.py:64-108); also the mean, which the roofline uses;
+  * time_graph_steps: exactly K GEMV steps back-to-back, captured in one HIP
+    graph over enough weight copies that every step reads cold weights, the
+    replay bracketed by events; per-step time = elapsed / K (the metric);
+  * time_gpu: the reference's protocol, a flush, then events around exactly
+    one call (bench/common.py:64-108); on MI355X the event markers alone add
+    ~6 us, more than a small GEMV takes, so it is reported beside the metric;
+  * time_repeated: back-to-back launches between two events (STREAM probes);
   * the flush defaults to a read-only sweep of 1 GiB (the reference wrote
     64 MB, bench/common.py:54-61): larger than the 256 MB Infinity Cache and
     the 8 x 4 MB L2s, and read-only so the timed kernel never competes with
@@ -26,6 +30,7 @@ import torch
 
 GROUP_SIZE = 128
 FLUSH_BYTES_DEFAULT = 1 << 30
+COLD_WORKING_SET = 640 << 20
 MI355X_HBM_PEAK_GBPS = 8000.0
 
 
@@ -71,7 +76,8 @@ class Flush:
 
 def time_gpu(fn: Callable[[], object], warmup: int, iters: int,
              flush: Optional[Flush] = None) -> dict:
-    """Median / IQR / mean of one `fn()` call between two HIP events."""
+    """Median / IQR / mean of one `fn()` call between two torch events on the
+    current stream (the reference's protocol, bench/common.py:64-108)."""
     stream = torch.cuda.current_stream()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
@@ -91,7 +97,14 @@ def time_gpu(fn: Callable[[], object], warmup: int, iters: int,
         ends[i].record(stream)
     torch.cuda.synchronize()
     wall_s = time.perf_counter() - t0
-    us = sorted(s.elapsed_time(e) * 1000.0 for s, e in zip(starts, ends))
+    out = _stats([s.elapsed_time(e) * 1000.0 for s, e in zip(starts, ends)])
+    out.update({"warmup": warmup, "wall_s_timed_loop": wall_s, "timer": "call_events",
+                "flush": flush.describe() if flush is not None else None})
+    return out
+
+
+def _stats(us: list[float]) -> dict:
+    us = sorted(us)
     n = len(us)
     return {
         "median_us": us[n // 2],
@@ -102,11 +115,77 @@ def time_gpu(fn: Callable[[], object], warmup: int, iters: int,
         "stdev_us": statistics.pstdev(us) if n > 1 else 0.0,
         "min_us": us[0],
         "max_us": us[-1],
-        "warmup": warmup,
-        "iters": iters,
-        "wall_s_timed_loop": wall_s,
-        "flush": flush.describe() if flush is not None else None,
+        "iters": n,
     }
+
+
+def weight_copies(packed: torch.Tensor, scales: torch.Tensor,
+                  min_bytes: int = COLD_WORKING_SET) -> tuple[list, list]:
+    """Enough device copies of (packed, scales) that cycling through them
+    reads more than `min_bytes` (the 256 MB Infinity Cache plus the 8 x 4 MB
+    L2s, with margin) between two uses of the same copy: every GEMV step then
+    reads cold weights from HBM, without a flush kernel in the timed span."""
+    per = packed.numel() * 4 + scales.numel() * 2
+    n = max(2, -(-min_bytes // per))
+    return [packed.clone() for _ in range(n)], [scales.clone() for _ in range(n)]
+
+
+def time_graph_steps(step: Callable[[int], object], steps: int, trials: int = 5,
+                     warmup: int = 1) -> dict:
+    """Per-step time of exactly `steps` back-to-back steps, `step(i)` for
+    i = 0..steps-1, captured in one HIP graph and replayed `trials` times.
+    Each replay is bracketed by events on the stream it runs on (after a
+    synchronize); the per-step time of a replay is its elapsed time / steps.
+    Host launch cost is outside the measurement, so the figure is what the
+    GPU spends per step when the steps run back-to-back, as in a decode pass."""
+    import time
+
+    for i in range(min(steps, 4)):  # eager warm-up: allocator and code objects
+        step(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            step(i)
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    per, walls = [], []
+    for _ in range(trials):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        walls.append(time.perf_counter() - t0)
+        per.append(start.elapsed_time(end) * 1000.0 / steps)
+    out = _stats(per)
+    out.update({"steps": steps, "trials": trials, "timer": "events_around_graph_replay",
+                "wall_s_per_replay": statistics.fmean(walls)})
+    return out, graph
+
+
+def time_repeated(fn: Callable[[], object], reps: int, trials: int = 5) -> dict:
+    """Per-launch time of `reps` back-to-back launches between two events (the
+    STREAM method: the event overhead is shared by `reps` launches)."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(trials):
+        start.record()
+        for _ in range(reps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        per.append(start.elapsed_time(end) * 1000.0 / reps)
+    out = _stats(per)
+    out.update({"reps": reps, "trials": trials, "timer": "events_around_repeated_launches"})
+    return out
 
 
 def gpu_info() -> dict:

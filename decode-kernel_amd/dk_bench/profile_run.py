@@ -1,0 +1,65 @@
+"""Fixed workload for rocprofv3 runs (kernel trace and PMC counters).
+
+    rocprofv3 --pmc FETCH_SIZE -d OUT -- python decode-kernel_amd/dk_bench/profile_run.py --config c0
+
+Runs, each after a 1 GiB read-only flush so every launch starts cold:
+  * `--copies` launches of the d2d copy over a 64 MiB buffer: known traffic
+    (64 MiB read + 64 MiB written) that calibrates FETCH_SIZE / WRITE_SIZE;
+  * `--reps` launches of one GEMV variant at one benchmark configuration.
+Replaces the reference's ncu launcher (bench/ncu_launch.py:13-34).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve()
+sys.path.insert(0, str(HERE.parents[1]))
+sys.path.insert(0, str(HERE.parents[2]))
+
+SHAPES = {"c0": (4096, 4096, 1), "c1": (11008, 4096, 1), "c2": (4096, 11008, 1),
+          "c3b16": (4096, 4096, 16), "c4a": (28672, 8192, 1), "c4b": (8192, 28672, 1)}
+VARIANTS = {"v5": dict(version=5), "v2": dict(version=2), "v4": dict(version=4, split_k=4),
+            "reuse": dict(version=5, reuse_weights=True), "v1": dict(version=1)}
+COPY_BYTES = 64 << 20
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--config", default="c0", choices=sorted(SHAPES))
+    ap.add_argument("--variant", default="v5", choices=sorted(VARIANTS))
+    ap.add_argument("--reps", type=int, default=50)
+    ap.add_argument("--copies", type=int, default=5)
+    args = ap.parse_args()
+
+    import torch
+
+    from decode_kernel import _cuda, gemv
+    from decode_kernel.quantize import quantize_and_pack
+    from dk_bench.common import Flush, bytes_moved_w4
+    from oracle.oracle import make_case
+
+    flush = Flush()
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(args.copies):
+        flush()
+        _cuda.d2d_copy(src, dst)
+    m, k, b = SHAPES[args.config]
+    w, x = make_case(m, k, b, seed=1000)
+    packed, scales = quantize_and_pack(torch.from_numpy(w))
+    pd, sd, xd = packed.cuda(), scales.cuda(), torch.from_numpy(x).cuda()
+    for _ in range(args.reps):
+        flush()
+        gemv(pd, sd, xd, **VARIANTS[args.variant])
+    torch.cuda.synchronize()
+    print(json.dumps({"config": args.config, "variant": args.variant, "M": m, "K": k, "B": b,
+                      "reps": args.reps, "copy_bytes": COPY_BYTES,
+                      "algorithmic_bytes": bytes_moved_w4(m, k, b)}), flush=True)
+
+
+if __name__ == "__main__":
+    main()

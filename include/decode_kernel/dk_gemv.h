@@ -39,7 +39,8 @@ typedef enum dk_kernel_version {
   DK_V2 = 2, /* one wave64 per row, 16-byte coalesced loads */
   DK_V3 = 3, /* v2 with the row's group scales staged in LDS */
   DK_V4 = 4, /* split-K over grid.y, deterministic single-launch reduction */
-  DK_V5 = 5  /* tuned: several rows per wave, x reused from registers */
+  DK_V5 = 5  /* tuned: activations loaded first, shape-selected rows per
+                wave and double-buffered stages */
 } dk_kernel_version;
 
 #define DK_STAMP_REUSE 15
@@ -111,7 +112,7 @@ int dk_stream_recommended_blocks(void);
  * Returns -1 on error as well; see dk_last_error(). */
 int dk_last_kernel_stamp(void);
 
-/* An empty kernel on `stream`: the event-timer floor for the benchmark.
+/* An empty kernel on `stream`: the per-launch floor for the benchmark.
  * No counterpart in the reference. */
 int dk_empty_kernel(hipStream_t stream);
 

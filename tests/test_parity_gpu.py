@@ -185,13 +185,13 @@ def test_minus_eight_nibbles_decode():
     words = np.full((m, k // 8), 0x88888888, dtype=np.uint32)
     words[::2] = 0x7F7F7F7F
     packed = words.view(np.int32)
-    scales = np.full((m, k // 128), 0.5, dtype=np.float16)
+    # Scale 2^-6 keeps |y| ~ 1, where the fp16 output step is far below the gate.
+    scales = np.full((m, k // 128), 2.0 ** -6, dtype=np.float16)
     x = oracle.make_case(1, k, 2, seed=5)[1]
     y_ref = oracle.linear_f64(x, packed, scales)
     pd, sd, xd = (torch.from_numpy(a).cuda() for a in (packed, scales, x))
     for label, kw in PATHS:
-        err = oracle.max_abs_err(_gemv(pd, sd, xd, **kw).float().cpu().numpy(), y_ref)
-        assert err < MAX_ABS, (label, err)
+        _check_against_oracle(_gemv(pd, sd, xd, **kw), y_ref, f"minus8/{label}")
 
 
 def test_c_abi_direct_matches_extension():
@@ -235,3 +235,4 @@ def test_stream_probes():
     assert torch.equal(a, c)
     _cuda.empty_kernel()
     torch.cuda.synchronize()
+
