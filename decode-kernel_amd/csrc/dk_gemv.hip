@@ -82,14 +82,15 @@ struct Launch {
 };
 
 // v5 stage shapes (R rows per wave, U 16-byte chunks per lane per stage,
-// double-buffered stages or not), chosen from a sweep on MI355X of
-// back-to-back launches over cold weights, B = 1:
-//   M = 4096  (K = 4096, 11008):  one row per wave, no double buffering
-//   M = 11008, K = 4096; M = 28672, K = 8192: two rows per wave
-//   M = 8192, K = 28672: two rows per wave, double-buffered stages
-// Fewer rows per wave keep more waves in flight when rows are few; two rows
-// halve the activation loads once there are enough rows to fill the chip.
-// Larger batch tiles keep more activation registers live and take fewer rows.
+// double-buffered stages or not), from a sweep on MI355X of back-to-back
+// launches over cold weights, B = 1 (us per launch):
+//   M = 4096,  K = 4096:  R2 U2 double-buffered 4.20 (R1 U1: 4.91)
+//   M = 11008, K = 4096:  R2 U2 7.10;   M = 4096, K = 11008: R2 U2 7.96
+//   M = 28672, K = 8192:  R2 U2 28.3;   M = 8192, K = 28672: R4 U1 double-buffered 27.9
+// Two rows per wave halve the activation loads and pairing; two chunks per
+// stage keep two weight loads in flight per row; more than that measured
+// slower on this memory system. Wider batch tiles keep more activation
+// registers live and take fewer rows and chunks.
 template <int R, int U, int NB, bool kPipe>
 int launch_v5_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                 int M, int K, int B) {
@@ -109,13 +110,11 @@ int launch_v5_shape(const Launch& L, const uint4* p, const uint16_t* s, const ui
 int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y, int M,
               int K, int B) {
   if (B == 1) {
-    if (M >= 8192) {
-      if (K > 16384) return launch_v5_t<2, 1, 1, true>(L, p, s, x, y, M, K, B);
-      return launch_v5_t<2, 1, 1, false>(L, p, s, x, y, M, K, B);
-    }
-    return launch_v5_t<1, 1, 1, false>(L, p, s, x, y, M, K, B);
+    if (K > 16384) return launch_v5_t<4, 1, 1, true>(L, p, s, x, y, M, K, B);
+    if (K <= 4096 && M <= 4096) return launch_v5_t<2, 2, 1, true>(L, p, s, x, y, M, K, B);
+    return launch_v5_t<2, 2, 1, false>(L, p, s, x, y, M, K, B);
   }
-  if (B == 2) return launch_v5_shape<4, 1, 2>(L, p, s, x, y, M, K, B);
+  if (B == 2) return launch_v5_shape<2, 1, 2>(L, p, s, x, y, M, K, B);
   return launch_v5_shape<2, 1, 4>(L, p, s, x, y, M, K, B);
 }
 
@@ -214,6 +213,9 @@ int dk_gemv_validate(int M, int K, int B, const dk_gemv_config* cfg) {
   if (M <= 0 || K <= 0 || B <= 0) return DK_OK;  // no-op call
   if (K % DK_GROUP_SIZE != 0) return fail(DK_ERR_INVALID_ARGUMENT, "K must be divisible by group size 128");
   if (K > (1 << 28)) return fail(DK_ERR_UNSUPPORTED, "K=%d exceeds the supported 2^28", K);
+  // v5 addresses activations through one buffer descriptor with 32-bit offsets.
+  if ((long long)B * K * 2 > 0x7fffffffLL)
+    return fail(DK_ERR_UNSUPPORTED, "B*K=%lld activation elements exceed 2^30", (long long)B * K);
   if (cfg->reuse_weights) {
     if (reuse_lds_bytes(K) > (size_t)lds_limit_bytes())
       return fail(DK_ERR_UNSUPPORTED, "K=%d needs %zu B of LDS on the reuse path (limit %d)", K,

@@ -184,13 +184,33 @@ __global__ __launch_bounds__(256) void gemv_v23(const uint4* __restrict__ packed
 
 // ---------------------------------------------------------------------------
 // v5: the tuned streaming kernel. Each wave owns R consecutive rows; lane l
-// owns 16-byte chunks l, l+64, ... of every one of them. All loads of a stage
-// (U chunks x R rows of weights, their scales, and the U x NB activation
-// chunks) are issued before any math, activations are paired once per stage
-// and reused for all R rows, and with kPipe the next stage's loads are in
-// flight while the current one is decoded. NB batch rows per launch tile
-// (grid.y covers B). Reference: csrc/gemv_w4a16.cu:318-357.
+// owns 16-byte chunks l, l+64, ... of each of them, U chunks per lane per
+// stage. All loads of a stage are raw buffer loads through SGPR resource
+// descriptors scoped to the wave's rows (a chunk past the row end, or a row
+// past M, is an out-of-range offset that reads 0, so tails need no branches
+// and the loads issue back to back): the NB activation chunks first, then
+// the scales, then the weights with the non-temporal hint (read-once data).
+// Activations are paired once per stage and reused for all R rows; with
+// kPipe the next stage's loads are in flight while this one is decoded.
+// grid.y covers the batch in tiles of NB rows.
+// Reference: csrc/gemv_w4a16.cu:318-357.
 // ---------------------------------------------------------------------------
+constexpr int kOutOfRange = (int)0x80000000;  // beyond any descriptor's num_records
+constexpr int kLoadNonTemporal = 2;            // buffer-load cache policy bit "nt"
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  // dword3 = 0x00020000: raw (stride 0) 32-bit buffer on gfx9-family parts.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+template <int kAux>
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, int offset) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, kAux);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 template <int R, int U, int NB>
 struct V5Stage {
   uint4 w[U][R];
@@ -199,25 +219,38 @@ struct V5Stage {
 };
 
 template <int R, int U, int NB>
-__device__ __forceinline__ void v5_load(V5Stage<R, U, NB>& st, const uint4* const (&rw)[R],
-                                        const uint16_t* const (&rs)[R],
-                                        const uint4* const (&xb)[NB], int c0, int nck, int lane) {
-  // Activations first, then scales, then weights: pairing the activations
-  // only waits for their (L2-resident) loads and overlaps the weights' HBM
-  // latency; issuing the weights first measured slower on MI355X.
+__device__ __forceinline__ void v5_load(V5Stage<R, U, NB>& st, __amdgpu_buffer_rsrc_t rw,
+                                        __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rx,
+                                        int c0, int nck, int G, int K, int b0, int B, int lane) {
+  int c[U];
+  bool ok[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int c = c0 + u * kWave + lane;
-    const bool ok = c < nck;
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) st.xv[u][b][j] = ok ? xb[b][4 * c + j] : zero4();
-#pragma unroll
-    for (int r = 0; r < R; ++r) st.s[u][r] = ok ? h2f(rs[r][c >> 2]) : 0.f;
-#pragma unroll
-    for (int r = 0; r < R; ++r) st.w[u][r] = ok ? rw[r][c] : zero4();
+    c[u] = c0 + u * kWave + lane;
+    ok[u] = c[u] < nck;
   }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int off = (ok[u] && b0 + b < B) ? (b0 + b) * K * 2 + c[u] * 64 : kOutOfRange;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) st.xv[u][b][j] = buffer_load16<0>(rx, off + 16 * j);
+    }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int off = ok[u] ? (r * G + (c[u] >> 2)) * 2 : kOutOfRange;
+      st.s[u][r] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0));
+    }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int off = ok[u] ? (r * nck + c[u]) * 16 : kOutOfRange;
+      st.w[u][r] = buffer_load16<kLoadNonTemporal>(rw, off);
+    }
 }
 
 template <int R, int U, int NB>
@@ -266,19 +299,12 @@ __global__ __launch_bounds__(256) void gemv_v5(const uint4* __restrict__ packed,
   const int b0 = blockIdx.y * NB;
   const int nck = K >> 5;
   const int G = K >> 7;
-  const int xstride = K >> 3;
-
-  const uint4* rw[R];
-  const uint16_t* rs[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int row = min(row0 + r, M - 1);
-    rw[r] = packed + (size_t)row * nck;
-    rs[r] = scales + (size_t)row * G;
-  }
-  const uint4* xb[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) xb[b] = x4 + (size_t)min(b0 + b, B - 1) * xstride;
+  const int rows = min(R, M - row0);
+  // Descriptors cover only this wave's rows and the activations: every valid
+  // offset stays below 2^31 and rows past M read as zero.
+  const auto rw = buffer_rsrc(packed + (size_t)row0 * nck, (uint32_t)(rows * (K / 2)));
+  const auto rs = buffer_rsrc(scales + (size_t)row0 * G, (uint32_t)(rows * G * 2));
+  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
 
   float acc[NB][R];
 #pragma unroll
@@ -289,22 +315,22 @@ __global__ __launch_bounds__(256) void gemv_v5(const uint4* __restrict__ packed,
   constexpr int kStep = U * kWave;
   V5Stage<R, U, NB> sa, sb;
   if (kPipe) {
-    v5_load(sa, rw, rs, xb, 0, nck, lane);
+    v5_load(sa, rw, rs, rx, 0, nck, G, K, b0, B, lane);
     for (int c0 = 0;;) {
       bool more = c0 + kStep < nck;
-      if (more) v5_load(sb, rw, rs, xb, c0 + kStep, nck, lane);
+      if (more) v5_load(sb, rw, rs, rx, c0 + kStep, nck, G, K, b0, B, lane);
       v5_compute(sa, acc);
       if (!more) break;
       c0 += kStep;
       more = c0 + kStep < nck;
-      if (more) v5_load(sa, rw, rs, xb, c0 + kStep, nck, lane);
+      if (more) v5_load(sa, rw, rs, rx, c0 + kStep, nck, G, K, b0, B, lane);
       v5_compute(sb, acc);
       if (!more) break;
       c0 += kStep;
     }
   } else {
     for (int c0 = 0; c0 < nck; c0 += kStep) {
-      v5_load(sa, rw, rs, xb, c0, nck, lane);
+      v5_load(sa, rw, rs, rx, c0, nck, G, K, b0, B, lane);
       v5_compute(sa, acc);
     }
   }
