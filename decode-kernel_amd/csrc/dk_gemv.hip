@@ -118,10 +118,16 @@ int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x
   return launch_v5_shape<2, 1, 4>(L, p, s, x, y, M, K, B);
 }
 
-size_t reuse_lds_bytes(int K) {
-  const int G = K / DK_GROUP_SIZE;
-  return (size_t)dk::kReuseWaves * 256 * sizeof(float) + (size_t)16 * G * sizeof(uint16_t);
+// Waves per 16-row tile on the reuse path (K split across them). Measured on
+// MI355X, back-to-back over cold weights, M = 4096, K = 4096: 16 waves give
+// 5.3 / 6.0 us at B = 1 / 4 and 8 waves 7.9 us at B = 16 (4 waves: 8.3-9.5);
+// with 512 or more tiles (M >= 8192) 8 waves per tile are enough.
+int reuse_waves(int M, int B) {
+  const int tiles = (M + 15) / 16;
+  return (tiles >= 512 || B > 4) ? 8 : 16;
 }
+
+size_t reuse_lds_bytes(int K) { return dk::reuse_lds_bytes_for(16, K); }
 
 size_t v3_lds_bytes(int K) { return (size_t)kWavesPerBlock * (K / DK_GROUP_SIZE) * sizeof(uint16_t); }
 
@@ -155,7 +161,10 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
 
   if (cfg->reuse_weights) {
     dim3 grid((M + 15) / 16, (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
-    return L("reuse launch", dk::gemv_reuse<2>, grid, dim3(dk::kReuseWaves * 64), reuse_lds_bytes(K),
+    if (reuse_waves(M, B) == 16)
+      return L("reuse launch", dk::gemv_reuse<16>, grid, dim3(16 * 64),
+               dk::reuse_lds_bytes_for(16, K), p4, scales, x4, y, M, K, B);
+    return L("reuse launch", dk::gemv_reuse<8>, grid, dim3(8 * 64), dk::reuse_lds_bytes_for(8, K),
              p4, scales, x4, y, M, K, B);
   }
   const dim3 block4(kWavesPerBlock * 64);

@@ -431,36 +431,42 @@ __global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
 
 // ---------------------------------------------------------------------------
 // Weight-reuse path (stamp 15): each decoded weight is used for up to 16
-// batch rows at once by v_mfma_f32_16x16x32_f16, so latency is flat in B
-// instead of the reference's O(B) re-decode (csrc/gemv_w4a16.cu:364-413).
-// A workgroup of kKs waves owns one 16-row tile; wave w takes groups w,
-// w+kKs, ... (adjacent groups stream side by side). Lane l loads row l%16,
-// bytes [64g + 16(l/16), +16) of group g: four words = four MFMA k-steps
-// that together cover exactly group g, so the fp32 tile result of a group is
-// scaled once (scales staged transposed in LDS) and accumulated. The kKs
-// wave partials are added in LDS in wave order.
+// batch rows at once by v_mfma_f32_16x16x32_f16, so latency is nearly flat
+// in B instead of the reference's O(B) re-decode (csrc/gemv_w4a16.cu:364-413).
+// A workgroup of KS waves owns one 16-row tile; wave w takes groups w, w+KS,
+// ... (adjacent groups stream side by side). Lane l loads row l%16, bytes
+// [64g + 16(l/16), +16) of group g: four words = four MFMA k-steps that
+// together cover exactly group g, so the fp32 tile result of a group is
+// scaled once (scales staged transposed in LDS) and accumulated. The KS wave
+// partials are added in LDS in wave order. Loads are raw buffer loads; rows
+// past M and batch rows past B read zero through out-of-range offsets.
 //   A (16x32, weights): lane l -> row l%16, 8 k-slots of lane group l/16
 //   B (32x16, x):       lane l -> batch l%16, same 8 k-slots
 //   D (16x16):          lane l -> rows 4(l/16)+v, batch l%16
 // ---------------------------------------------------------------------------
-constexpr int kReuseWaves = 4;
 constexpr int kReuseBatch = 16;
 
-template <int P>
-__global__ __launch_bounds__(kReuseWaves * 64) void gemv_reuse(
-    const uint4* __restrict__ packed, const uint16_t* __restrict__ scales,
-    const uint4* __restrict__ x4, uint16_t* __restrict__ y, int M, int K, int B) {
+__host__ __device__ constexpr size_t reuse_lds_bytes_for(int ks, int K) {
+  return (size_t)ks * 256 * sizeof(float) + (size_t)16 * (K / kGroupSize) * sizeof(uint16_t);
+}
+
+template <int KS>
+__global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ packed,
+                                                      const uint16_t* __restrict__ scales,
+                                                      const uint4* __restrict__ x4,
+                                                      uint16_t* __restrict__ y, int M, int K,
+                                                      int B) {
   write_stamp(DK_STAMP_REUSE);
   extern __shared__ float lds_reuse[];
   const int G = K >> 7;
-  float* red = lds_reuse;                                                 // [waves][64][4]
-  uint16_t* sT = reinterpret_cast<uint16_t*>(lds_reuse + kReuseWaves * 256);  // [G][16]
+  const int nck = K >> 5;
+  float* red = lds_reuse;                                             // [KS][64][4]
+  uint16_t* sT = reinterpret_cast<uint16_t*>(lds_reuse + KS * 256);   // [G][16]
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row0 = blockIdx.x * 16;
   const int b0 = blockIdx.y * kReuseBatch;
-  const int nck = K >> 5;
 
   // Stage the tile's scales transposed: sT[g][r] = scales[row0 + r][g].
   for (int e = threadIdx.x; e < 16 * G; e += blockDim.x) {
@@ -470,42 +476,33 @@ __global__ __launch_bounds__(kReuseWaves * 64) void gemv_reuse(
   }
   __syncthreads();
 
-  const int r_lane = lane & 15;   // A row / B batch column
-  const int kq = lane >> 4;       // lane group: 16-byte quarter of a group
-  const int row = min(row0 + r_lane, M - 1);
-  const uint4* rw = packed + (size_t)row * nck + kq;
+  const int r_lane = lane & 15;  // A row / B batch column
+  const int kq = lane >> 4;      // lane group: 16-byte quarter of a group
   const int b = b0 + r_lane;
-  const bool bok = b < B;
-  const uint4* xb = x4 + (size_t)(bok ? b : 0) * (K >> 3) + 4 * kq;
+  const int rows = min(16, M - row0);
+  const auto rw = buffer_rsrc(packed + (size_t)row0 * nck, (uint32_t)(rows * (K / 2)));
+  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
+  const int xbase = b < B ? b * K * 2 + kq * 64 : kOutOfRange;
+  const int wbase = (r_lane * nck + kq) * 16;
 
   f4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int g0 = wave; g0 < G; g0 += kReuseWaves * P) {
-    uint4 w[P];
-    uint4 xv[P][4];
+  for (int g = wave; g < G; g += KS) {
+    uint4 xv[4];
+    const int xo = b < B ? xbase + g * 256 : kOutOfRange;
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int g = g0 + p * kReuseWaves;
-      const bool ok = g < G;
+    for (int j = 0; j < 4; ++j) xv[j] = buffer_load16<0>(rx, xo + 16 * j);
+    const uint4 w = buffer_load16<kLoadNonTemporal>(rw, wbase + g * 64);
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    f4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xv[p][j] = (ok && bok) ? xb[16 * g + j] : zero4();
-      w[p] = ok ? rw[4 * g] : zero4();  // word 0 decodes to q = 0
-    }
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int g = g0 + p * kReuseWaves;
-      if (g >= G) break;
-      const uint32_t words[4] = {w[p].x, w[p].y, w[p].z, w[p].w};
-      f4_t c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_word_h8(words[j]), pair_x8(xv[p][j]), c,
-                                                   0, 0, 0);
-      const uint2 s4 = *reinterpret_cast<const uint2*>(sT + g * 16 + 4 * kq);
-      acc[0] = __builtin_fmaf(c[0], h2f((uint16_t)(s4.x & 0xFFFFu)), acc[0]);
-      acc[1] = __builtin_fmaf(c[1], h2f((uint16_t)(s4.x >> 16)), acc[1]);
-      acc[2] = __builtin_fmaf(c[2], h2f((uint16_t)(s4.y & 0xFFFFu)), acc[2]);
-      acc[3] = __builtin_fmaf(c[3], h2f((uint16_t)(s4.y >> 16)), acc[3]);
-    }
+    for (int j = 0; j < 4; ++j)
+      c = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_word_h8(words[j]), pair_x8(xv[j]), c, 0,
+                                                 0, 0);
+    const uint2 s4 = *reinterpret_cast<const uint2*>(sT + g * 16 + 4 * kq);
+    acc[0] = __builtin_fmaf(c[0], h2f((uint16_t)(s4.x & 0xFFFFu)), acc[0]);
+    acc[1] = __builtin_fmaf(c[1], h2f((uint16_t)(s4.x >> 16)), acc[1]);
+    acc[2] = __builtin_fmaf(c[2], h2f((uint16_t)(s4.y & 0xFFFFu)), acc[2]);
+    acc[3] = __builtin_fmaf(c[3], h2f((uint16_t)(s4.y >> 16)), acc[3]);
   }
 
   // Cross-wave reduction of the 16x16 tile, in wave order.
@@ -514,10 +511,10 @@ __global__ __launch_bounds__(kReuseWaves * 64) void gemv_reuse(
   __syncthreads();
   if (wave == 0) {
     f4_t t = {0.f, 0.f, 0.f, 0.f};
-    for (int w = 0; w < kReuseWaves; ++w)
+    for (int w = 0; w < KS; ++w)
 #pragma unroll
       for (int v = 0; v < 4; ++v) t[v] += red[(w * 64 + lane) * 4 + v];
-    if (bok) {
+    if (b < B) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int orow = row0 + 4 * kq + v;
@@ -528,4 +525,3 @@ __global__ __launch_bounds__(kReuseWaves * 64) void gemv_reuse(
 }
 
 }  // namespace dk
-
