@@ -106,6 +106,15 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Workgroups are dealt to the 8 XCDs of an MI355X round-robin (workgroup i
+// to XCD i % 8). Renumber them so XCD x handles one contiguous range of
+// workgroup ids: a bijection on [0, n) for any n, so correctness does not
+// depend on the dealing order; it only changes which XCD streams which rows.
+__device__ __forceinline__ int xcd_contiguous_block(int wg, int n) {
+  const int q = n >> 3, r = n & 7, x = wg & 7;
+  return x * q + (x < r ? x : r) + (wg >> 3);
+}
+
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 

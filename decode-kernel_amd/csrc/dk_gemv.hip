@@ -84,20 +84,24 @@ struct Launch {
 // v5 stage shapes (R rows per wave, U 16-byte chunks per lane per stage,
 // double-buffered stages or not), from a sweep on MI355X of back-to-back
 // launches over cold weights, B = 1 (us per launch):
-//   M = 4096,  K = 4096:  R2 U2 double-buffered 4.20 (R1 U1: 4.91)
+//   M = 4096,  K = 4096:  R2 U2 double-buffered 4.13 (R1 U1: 4.91)
 //   M = 11008, K = 4096:  R2 U2 7.10;   M = 4096, K = 11008: R2 U2 7.96
 //   M = 28672, K = 8192:  R2 U2 28.3;   M = 8192, K = 28672: R4 U1 double-buffered 27.9
 // Two rows per wave halve the activation loads and pairing; two chunks per
 // stage keep two weight loads in flight per row; more than that measured
 // slower on this memory system. Wider batch tiles keep more activation
 // registers live and take fewer rows and chunks.
+// Two waves per workgroup: measured 2-4% faster than four with the XCD
+// renumbering (finer-grained blocks of rows per XCD).
+constexpr int kV5WavesPerBlock = 2;
+
 template <int R, int U, int NB, bool kPipe>
 int launch_v5_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                 int M, int K, int B) {
-  const int rows_per_block = kWavesPerBlock * R;
+  const int rows_per_block = kV5WavesPerBlock * R;
   dim3 grid((M + rows_per_block - 1) / rows_per_block, (B + NB - 1) / NB);
-  return L("v5 launch", dk::gemv_v5<R, U, NB, kPipe>, grid, dim3(kWavesPerBlock * 64), 0, p, s, x,
-           y, M, K, B);
+  return L("v5 launch", dk::gemv_v5<R, U, NB, kPipe>, grid, dim3(kV5WavesPerBlock * 64), 0, p, s,
+           x, y, M, K, B);
 }
 
 template <int R, int U, int NB>
