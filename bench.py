@@ -78,6 +78,8 @@ def parse_args():
     ap.add_argument("--flush", choices=["read", "write", "none"], default="read")
     ap.add_argument("--flush-bytes", type=int, default=1 << 30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-quantizer", action="store_true",
+                    help="skip the device quantizer measurement")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="budget of the CPU baseline sample")
     ap.add_argument("--out", type=Path, default=None, help="also write the full JSON here")
@@ -188,6 +190,57 @@ def cpu_baseline(packed, scales, x, budget_s):
     }
 
 
+def bench_quantizer(roof_gbps, cpu_seconds):
+    """The device quantizer (dk_quantize_pack_f32) at the largest weight,
+    c4a 28672 x 8192 (235 M weights, 940 MB fp32 read per launch, more than
+    the Infinity Cache holds), checked bit-for-bit against the torch
+    formulation on the same GPU before it is timed. The oracle's numpy
+    quantizer is timed beside it on a bounded row sample on this host."""
+    import numpy as np
+    import torch
+
+    from decode_kernel import _cuda
+    from decode_kernel.quantize import quantize_and_pack_torch
+    from dk_bench.common import time_repeated
+    from oracle import oracle
+
+    m, k = 28672, 8192
+    gen = torch.Generator(device="cuda").manual_seed(3000)
+    w = torch.randn(m, k, device="cuda", generator=gen) * 0.02
+    packed, scales = _cuda.quantize_and_pack(w)
+    tp, ts = quantize_and_pack_torch(w)
+    if not (torch.equal(packed, tp) and torch.equal(scales.view(torch.int16), ts.view(torch.int16))):
+        raise RuntimeError("device quantizer differs from the torch formulation at c4a")
+    del tp, ts
+    st = time_repeated(lambda: _cuda.quantize_and_pack(w), reps=20)
+    moved = m * k * 4 + m * k // 2 + (m * k // 128) * 2
+    out = {
+        "shape": [m, k], "bytes_moved": moved, "p50_us": st["median_us"], "iqr_us": st["iqr_us"],
+        "gbps": moved / (st["median_us"] * 1e3), "weights_per_s": m * k / (st["median_us"] * 1e-6),
+        "timer": "events around 20 back-to-back launches, p50 of 5 trials",
+    }
+    out["pct_of_read_roof"] = 100.0 * out["gbps"] / roof_gbps
+    rows = 1024
+    wc = w[:rows].cpu().numpy()
+    del w, packed, scales
+    torch.cuda.empty_cache()
+    oracle.quantize_and_pack(wc)
+    times = []
+    t_end = time.perf_counter() + cpu_seconds
+    while time.perf_counter() < t_end and len(times) < 50:
+        t0 = time.perf_counter_ns()
+        oracle.quantize_and_pack(wc)
+        times.append((time.perf_counter_ns() - t0) / 1e9)
+    times.sort()
+    med = times[len(times) // 2]
+    out["cpu_baseline"] = {
+        "weights_per_s": rows * k / med, "kind": "port", "cores": 1,
+        "sample": f"oracle.quantize_and_pack (numpy) on {rows} rows of c4a, median of {len(times)}",
+        "seconds_for_c4a_extrapolated": m * k / (rows * k / med),
+    }
+    return out
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -269,6 +322,13 @@ def main():
             del copies, xd, p_cpu, s_cpu, x_cpu
             torch.cuda.empty_cache()
 
+    quant = None
+    if not args.no_quantizer:
+        log("[bench] device quantizer at c4a")
+        quant = bench_quantizer(roof["gbps"], min(args.cpu_seconds, 5.0))
+        log(f"   quantize_and_pack {quant['p50_us']:8.2f} us  {quant['gbps']:8.1f} GB/s  "
+            f"{quant['pct_of_read_roof']:5.1f}% of read roof")
+
     traffic = None
     if PROFILE_TRAFFIC.exists():
         try:
@@ -312,6 +372,7 @@ def main():
             "algorithmic_bytes": headline["bytes_moved"],
         },
         "cpu_baseline": cpu,
+        "quantizer": quant,
         "configs": {
             key: {"M": r["M"], "K": r["K"], "batch": r["batch"],
                   "same_size_read_gbps": (round(r["same_size_read"]["gbps"], 1)

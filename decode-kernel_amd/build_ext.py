@@ -33,7 +33,7 @@ BUILD = PKG_ROOT / "_build"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = os.environ.get("DK_OFFLOAD_ARCH", "gfx950")
 
-HIP_SOURCES = [CSRC / "dk_gemv.hip", CSRC / "dk_stream.hip"]
+HIP_SOURCES = [CSRC / "dk_gemv.hip", CSRC / "dk_stream.hip", CSRC / "dk_quant.hip"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",

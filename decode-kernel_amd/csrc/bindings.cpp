@@ -14,6 +14,7 @@
 #include <torch/extension.h>
 
 #include <cstdint>
+#include <vector>
 
 #include "decode_kernel/dk_gemv.h"
 
@@ -146,6 +147,28 @@ void stream_write(torch::Tensor dst) {
                "stream_write");
 }
 
+// Device quantizer: fp32 W [M, K] on the GPU -> (packed int32 [M, K/8],
+// scales fp16 [M, K/128]). Reference: python/decode_kernel/quantize.py:26-51.
+std::vector<torch::Tensor> quantize_and_pack(torch::Tensor w) {
+  TORCH_CHECK(w.is_cuda(), "w must be a CUDA tensor");
+  TORCH_CHECK(w.scalar_type() == torch::kFloat32, "w must be fp32");
+  TORCH_CHECK(w.dim() == 2, "weight must be [M, K]");
+  TORCH_CHECK(w.size(1) % kGroupSize == 0, "K=", w.size(1), " is not divisible by group_size=128");
+  TORCH_CHECK(w.size(0) <= INT32_MAX && w.size(1) <= INT32_MAX, "M and K must fit in int32");
+  c10::DeviceGuard guard(w.device());
+  auto wc = w.contiguous();
+  const int M = static_cast<int>(wc.size(0));
+  const int K = static_cast<int>(wc.size(1));
+  auto packed = torch::empty({M, K / kNibblesPerWord}, wc.options().dtype(torch::kInt32));
+  auto scales = torch::empty({M, K / kGroupSize}, wc.options().dtype(torch::kFloat16));
+  check_status(dk_quantize_pack_f32(wc.data_ptr<float>(), M, K,
+                                    reinterpret_cast<uint32_t*>(packed.data_ptr<int32_t>()),
+                                    reinterpret_cast<uint16_t*>(scales.data_ptr<at::Half>()),
+                                    current_stream(wc)),
+               "quantize_and_pack");
+  return {packed, scales};
+}
+
 int stream_recommended_blocks() {
   const int blocks = dk_stream_recommended_blocks();
   TORCH_CHECK(blocks > 0, "stream_recommended_blocks failed: ", dk_last_error());
@@ -169,6 +192,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("w4a16_gemv", &w4a16_gemv, "W4A16 GEMV", py::arg("packed"), py::arg("scales"),
         py::arg("x"), py::arg("version") = 5, py::arg("split_k") = 4,
         py::arg("reuse_weights") = false, py::arg("warps_per_row") = 1);
+  m.def("quantize_and_pack", &quantize_and_pack,
+        "fp32 W [M, K] -> (packed int32 [M, K/8], scales fp16 [M, K/128]) on the GPU",
+        py::arg("w"));
   m.def("d2d_copy", &d2d_copy, "Aligned device-to-device copy", py::arg("src"), py::arg("dst"));
   m.def("stream_read", &stream_read, "Read-only STREAM sum-reduction (one float partial per block)",
         py::arg("src"), py::arg("partials"));

@@ -47,6 +47,7 @@ _SIGNATURES = {
         [_P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
          ctypes.POINTER(GemvConfig), _P, ctypes.c_size_t, _P],
     ),
+    "dk_quantize_pack_f32": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, _P, _P, _P]),
     "dk_d2d_copy": (ctypes.c_int, [_P, _P, ctypes.c_size_t, _P]),
     "dk_stream_read": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_int, _P]),
     "dk_stream_write": (ctypes.c_int, [_P, ctypes.c_size_t, ctypes.c_int, _P]),

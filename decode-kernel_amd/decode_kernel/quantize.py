@@ -13,7 +13,10 @@ Format (identical to python/decode_kernel/quantize.py:1-15 of the reference):
   never produces it.
 
 These functions run on whatever device the input tensor lives on; they are
-the format producer, not the GEMV (which only exists as a HIP kernel).
+the format producer, not the GEMV (which only exists as a HIP kernel). On a
+GPU tensor with the default group size, quantize_and_pack runs the HIP
+quantizer of the extension (bit-exact with the CPU path); other group sizes
+use the torch formulation below on either device.
 """
 
 from __future__ import annotations
@@ -57,7 +60,27 @@ def quantize_and_pack(
         raise ValueError(f"K={k} is not divisible by group_size={group_size}")
     if k % NIBBLES_PER_WORD != 0:
         raise ValueError(f"K={k} is not divisible by {NIBBLES_PER_WORD}")
+    if weight.is_cuda and group_size == GROUP_SIZE:
+        # Device tensors go through the HIP quantizer (one pass over W, no
+        # temporaries); it needs the built extension like the GEMV does.
+        from . import _cuda
 
+        packed, scales = _cuda.quantize_and_pack(weight.float().contiguous())
+        return packed, scales
+    return quantize_and_pack_torch(weight, group_size)
+
+
+def quantize_and_pack_torch(
+    weight: torch.Tensor, group_size: int = GROUP_SIZE
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """The quantizer as torch tensor arithmetic, on the input's device.
+
+    Same result bits as the HIP quantizer; used for CPU tensors, other group
+    sizes, and as the second formulation the GPU quantizer is checked against.
+    """
+    m, k = weight.shape
+    if k % group_size != 0 or k % NIBBLES_PER_WORD != 0:
+        raise ValueError(f"K={k} is not divisible by group_size={group_size} and 8")
     groups = weight.float().reshape(m, k // group_size, group_size)
     scale = _div_fp32(groups.abs().amax(dim=-1), float(QMAX)).clamp_min(SCALE_FLOOR)
     q = torch.round(_div_fp32(groups, scale[..., None])).clamp_(QMIN, QMAX).to(torch.int32)

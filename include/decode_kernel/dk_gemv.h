@@ -91,6 +91,15 @@ int dk_w4a16_gemv(const uint32_t* packed, const uint16_t* scales,
                   const dk_gemv_config* cfg, void* workspace,
                   size_t workspace_bytes, hipStream_t stream);
 
+/* Quantize fp32 W[M, K] (row-major, 16-byte aligned) into the format above:
+ * packed [M, K/8] and fp16 scales [M, K/128], bit-exact with the reference
+ * quantizer on fp32 input: per 128-group scale = max(amax/7, 1e-8) in fp32,
+ * q = clamp(round_half_even(w/scale), -7, 7), scale stored as fp16 (RNE).
+ * Replaces quantize_and_pack on device tensors
+ * (python/decode_kernel/quantize.py:26-51). Inputs must be finite. */
+int dk_quantize_pack_f32(const float* w, int M, int K, uint32_t* packed,
+                         uint16_t* scales, hipStream_t stream);
+
 /* STREAM probes. Reference: include/decode_kernel/gemv_w4a16.h:38-43,
  * csrc/gemv_w4a16.cu:593-626. `bytes` must be a multiple of 16.
  * dk_stream_read writes one fp32 partial sum per block into `partials`
@@ -121,7 +130,7 @@ const char* dk_last_error(void);
 
 /* ABI version of this header, (major << 16) | minor. */
 int dk_abi_version(void);
-#define DK_ABI_VERSION ((1 << 16) | 0)
+#define DK_ABI_VERSION ((1 << 16) | 1)
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.dk_abi_version() == (1 << 16) | 0
+    assert lib.dk_abi_version() == (1 << 16) | 1
 
 
 def test_default_config_matches_reference(lib):
@@ -120,17 +120,31 @@ def test_probe_argument_checks(lib):
     assert lib.dk_d2d_copy(0x10000, 0x10008, 16, None) == _abi.DK_ERR_INVALID_ARGUMENT
 
 
+def test_quantizer_argument_checks(lib):
+    # Every check runs on the host before a launch; empty problems are no-ops.
+    assert lib.dk_quantize_pack_f32(None, 0, 128, None, None, None) == _abi.DK_OK
+    assert lib.dk_quantize_pack_f32(None, 4, 0, None, None, None) == _abi.DK_OK
+    assert lib.dk_quantize_pack_f32(None, -1, 128, None, None, None) == _abi.DK_ERR_INVALID_ARGUMENT
+    fake = 0x10000
+    rc = lib.dk_quantize_pack_f32(fake, 4, 200, fake, fake, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "group_size=128" in lib.dk_last_error().decode()
+    rc = lib.dk_quantize_pack_f32(None, 4, 128, fake, fake, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "NULL" in lib.dk_last_error().decode()
+    rc = lib.dk_quantize_pack_f32(fake + 4, 4, 128, fake, fake, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "aligned" in lib.dk_last_error().decode()
+
+
 def test_torch_extension_surface():
     from decode_kernel import _cuda
 
     for name in ("w4a16_gemv", "d2d_copy", "stream_read", "stream_write",
-                 "stream_recommended_blocks", "last_kernel_stamp"):
+                 "stream_recommended_blocks", "last_kernel_stamp", "quantize_and_pack"):
         assert hasattr(_cuda, name), name
     doc = _cuda.w4a16_gemv.__doc__
     for pat in (r"version: [\w.]*Int = 5", r"split_k: [\w.]*Int = 4",
                 r"reuse_weights: bool = False", r"warps_per_row: [\w.]*Int = 1"):
         assert re.search(pat, doc), (pat, doc)
-    assert _cuda.ABI_VERSION == (1 << 16) | 0
+    assert _cuda.ABI_VERSION == (1 << 16) | 1
 
 
 def test_extension_rejects_cpu_tensors():
