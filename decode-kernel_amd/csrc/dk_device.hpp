@@ -6,8 +6,8 @@
 // with the IEEE-754 binary16 exponent trick: OR an offset-binary nibble u
 // (0..15) into the mantissa of 1024.0 (0x6400) to get the fp16 value 1024+u,
 // then subtract 1032 to get q = u - 8 exactly. Two nibbles 16 bits apart are
-// decoded by one AND/OR, so a word costs one XOR, one shift, four AND/OR
-// (fused to v_bitop3_b32 on gfx950) and four packed fp16 ops: about 1.1 VALU
+// decoded by one AND/XOR, so a word costs one shift, four AND/XOR (each one
+// v_bitop3_b32 on gfx950) and four packed fp16 ops: about 1.1 VALU
 // operations per weight, and every step is exact.
 //
 // The pairs come out as (q0,q4), (q1,q5), (q2,q6), (q3,q7). Activations are
@@ -33,19 +33,23 @@ __device__ __forceinline__ h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2
 // Decode the 8 signed nibbles of `w` (nibble n = bits 4n..4n+3, two's
 // complement, reference layout include/decode_kernel/gemv_w4a16.h:29-30)
 // into q[j] = (q_j, q_{j+4}) for j = 0..3.
+//
+// The two's-complement -> offset-binary flip (XOR of the nibble's top bit)
+// and the OR of the 0x6400 exponent are one XOR with a constant after the
+// mask: (w & M) ^ (0x6400.. | sign bits inside M). AND-then-XOR is a single
+// v_bitop3_b32, so a pair costs one logic op and one packed fp16 op.
 __device__ __forceinline__ void unpack_word(uint32_t w, h2_t (&q)[4]) {
-  const uint32_t u = w ^ 0x88888888u;  // two's complement -> offset binary
-  const uint32_t v = u >> 8;
+  const uint32_t v = w >> 8;
   const h2_t sub = {(_Float16)-1032.0f, (_Float16)-1032.0f};
   const h2_t sixteenth = {(_Float16)0.0625f, (_Float16)0.0625f};
   const h2_t sub16 = {(_Float16)-72.0f, (_Float16)-72.0f};
-  // Low nibble of each 16-bit half: fp16 1024 + u.
-  q[0] = as_h2((u & 0x000F000Fu) | 0x64006400u) + sub;
-  q[2] = as_h2((v & 0x000F000Fu) | 0x64006400u) + sub;
+  // Low nibble of each 16-bit half: fp16 1024 + u, u = nibble ^ 8.
+  q[0] = as_h2((w & 0x000F000Fu) ^ 0x64086408u) + sub;
+  q[2] = as_h2((v & 0x000F000Fu) ^ 0x64086408u) + sub;
   // Second nibble of each half lands in mantissa bits 4..7: 1024 + 16u,
   // and (1024 + 16u)/16 - 72 = u - 8.
-  q[1] = as_h2((u & 0x00F000F0u) | 0x64006400u) * sixteenth + sub16;
-  q[3] = as_h2((v & 0x00F000F0u) | 0x64006400u) * sixteenth + sub16;
+  q[1] = as_h2((w & 0x00F000F0u) ^ 0x64806480u) * sixteenth + sub16;
+  q[3] = as_h2((v & 0x00F000F0u) ^ 0x64806480u) * sixteenth + sub16;
 }
 
 // Pair eight consecutive fp16 activations (one 16-byte load: .x=(x0,x1),
