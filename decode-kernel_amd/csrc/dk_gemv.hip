@@ -81,45 +81,49 @@ struct Launch {
   }
 };
 
-// v5 stage shapes (R rows per wave, U 16-byte chunks per lane per stage,
-// double-buffered stages or not), from a sweep on MI355X of back-to-back
-// launches over cold weights, B = 1 (us per launch):
-//   M = 4096,  K = 4096:  R2 U2 double-buffered 4.13 (R1 U1: 4.91)
-//   M = 11008, K = 4096:  R2 U2 7.10;   M = 4096, K = 11008: R2 U2 7.96
-//   M = 28672, K = 8192:  R2 U2 28.3;   M = 8192, K = 28672: R4 U1 double-buffered 27.9
+// v5 stage shapes (R rows per wave, U 16-byte chunks per lane per stage),
+// from a sweep on MI355X of back-to-back
+// launches over cold weights, B = 1 (us per launch; R rows, U chunks):
+//   M = 4096,  K = 4096:  R2 U2 3.92 (double-buffered 4.03; R4 U1 4.61)
+//   M = 11008, K = 4096:  R2 U2 6.73 (R4 U1 7.39)
+//   M = 4096,  K = 11008: R2 U2 7.22 (R4 U1 9.77)
+//   M = 28672, K = 8192:  R4 U1 24.66 (R2 U2 27.14)
+//   M = 8192,  K = 28672: R4 U1 23.36 (double-buffered 24.22; R2 U2 28.55)
+//   M = 8192,  K = 3584:  R4 U1 5.35, R2 U2 5.35; M = 3584, K = 8192: R2 U2 5.56
+// Double-buffered stages (the next stage's loads issued before this stage's
+// math) measured slower everywhere once the decode is 13 ops per word: the
+// other waves on the SIMD hide the load latency instead.
+// B > 1, M = K = 4096 (us per launch; NB activation rows per tile):
+//   B = 2:  R2 U1 NB2 4.81 (R4 U1 NB2 5.47; R2 U1 NB4 6.17)
+//   B = 4:  R4 U1 NB2 6.05 (R2 U1 NB4 6.81); B = 8: R4 U1 NB2 9.68 (11.71)
+//   B = 16: R4 U1 NB2 16.82 (21.73); M = 8192, K = 28672, B = 4: 56.0 (69.0)
 // Two rows per wave halve the activation loads and pairing; two chunks per
 // stage keep two weight loads in flight per row; more than that measured
-// slower on this memory system. Wider batch tiles keep more activation
-// registers live and take fewer rows and chunks.
+// slower on this memory system. With a batch, more rows per wave pay for
+// the extra activation registers; tiles of four batch rows were slower.
 // Two waves per workgroup: measured 2-4% faster than four with the XCD
 // renumbering (finer-grained blocks of rows per XCD).
 constexpr int kV5WavesPerBlock = 2;
 
-template <int R, int U, int NB, bool kPipe>
+template <int R, int U, int NB>
 int launch_v5_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                 int M, int K, int B) {
   const int rows_per_block = kV5WavesPerBlock * R;
   dim3 grid((M + rows_per_block - 1) / rows_per_block, (B + NB - 1) / NB);
-  return L("v5 launch", dk::gemv_v5<R, U, NB, kPipe>, grid, dim3(kV5WavesPerBlock * 64), 0, p, s,
-           x, y, M, K, B);
-}
-
-template <int R, int U, int NB>
-int launch_v5_shape(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
-                    int M, int K, int B) {
-  if (K / 32 <= U * 64) return launch_v5_t<R, U, NB, false>(L, p, s, x, y, M, K, B);
-  return launch_v5_t<R, U, NB, true>(L, p, s, x, y, M, K, B);
+  return L("v5 launch", dk::gemv_v5<R, U, NB>, grid, dim3(kV5WavesPerBlock * 64), 0, p, s, x, y,
+           M, K, B);
 }
 
 int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y, int M,
               int K, int B) {
   if (B == 1) {
-    if (K > 16384) return launch_v5_t<4, 1, 1, true>(L, p, s, x, y, M, K, B);
-    if (K <= 4096 && M <= 4096) return launch_v5_t<2, 2, 1, true>(L, p, s, x, y, M, K, B);
-    return launch_v5_t<2, 2, 1, false>(L, p, s, x, y, M, K, B);
+    // Four rows per wave once both dimensions are large: still >= 2048 waves,
+    // and half the activation loads and pairing per weight.
+    if (M >= 8192 && K >= 8192) return launch_v5_t<4, 1, 1>(L, p, s, x, y, M, K, B);
+    return launch_v5_t<2, 2, 1>(L, p, s, x, y, M, K, B);
   }
-  if (B == 2) return launch_v5_shape<2, 1, 2>(L, p, s, x, y, M, K, B);
-  return launch_v5_shape<2, 1, 4>(L, p, s, x, y, M, K, B);
+  if (B == 2) return launch_v5_t<2, 1, 2>(L, p, s, x, y, M, K, B);
+  return launch_v5_t<4, 1, 2>(L, p, s, x, y, M, K, B);
 }
 
 // Waves per 16-row tile on the reuse path (K split across them). Measured on

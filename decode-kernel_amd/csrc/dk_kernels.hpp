@@ -190,8 +190,9 @@ __global__ __launch_bounds__(256) void gemv_v23(const uint4* __restrict__ packed
 // past M, is an out-of-range offset that reads 0, so tails need no branches
 // and the loads issue back to back): the NB activation chunks first, then
 // the scales, then the weights with the non-temporal hint (read-once data).
-// Activations are paired once per stage and reused for all R rows; with
-// kPipe the next stage's loads are in flight while this one is decoded.
+// Activations are paired once per stage and reused for all R rows. Load
+// latency is hidden by the other waves on the SIMD, not by double buffering
+// inside a wave (which measured slower once the decode was 13 ops per word).
 // grid.y covers the batch in tiles of NB rows; workgroup ids are renumbered
 // so each XCD streams one contiguous block of rows (measured 2-5% faster).
 // Reference: csrc/gemv_w4a16.cu:318-357.
@@ -287,7 +288,7 @@ __device__ __forceinline__ void v5_compute(const V5Stage<R, U, NB>& st, float (&
   }
 }
 
-template <int R, int U, int NB, bool kPipe>
+template <int R, int U, int NB>
 __global__ __launch_bounds__(256) void gemv_v5(const uint4* __restrict__ packed,
                                                const uint16_t* __restrict__ scales,
                                                const uint4* __restrict__ x4,
@@ -315,26 +316,10 @@ __global__ __launch_bounds__(256) void gemv_v5(const uint4* __restrict__ packed,
     for (int r = 0; r < R; ++r) acc[b][r] = 0.f;
 
   constexpr int kStep = U * kWave;
-  V5Stage<R, U, NB> sa, sb;
-  if (kPipe) {
-    v5_load(sa, rw, rs, rx, 0, nck, G, K, b0, B, lane);
-    for (int c0 = 0;;) {
-      bool more = c0 + kStep < nck;
-      if (more) v5_load(sb, rw, rs, rx, c0 + kStep, nck, G, K, b0, B, lane);
-      v5_compute(sa, acc);
-      if (!more) break;
-      c0 += kStep;
-      more = c0 + kStep < nck;
-      if (more) v5_load(sa, rw, rs, rx, c0 + kStep, nck, G, K, b0, B, lane);
-      v5_compute(sb, acc);
-      if (!more) break;
-      c0 += kStep;
-    }
-  } else {
-    for (int c0 = 0; c0 < nck; c0 += kStep) {
-      v5_load(sa, rw, rs, rx, c0, nck, G, K, b0, B, lane);
-      v5_compute(sa, acc);
-    }
+  V5Stage<R, U, NB> st;
+  for (int c0 = 0; c0 < nck; c0 += kStep) {
+    v5_load(st, rw, rs, rx, c0, nck, G, K, b0, B, lane);
+    v5_compute(st, acc);
   }
 
 #pragma unroll

@@ -39,8 +39,8 @@ typedef enum dk_kernel_version {
   DK_V2 = 2, /* one wave64 per row, 16-byte coalesced loads */
   DK_V3 = 3, /* v2 with the row's group scales staged in LDS */
   DK_V4 = 4, /* split-K over grid.y, deterministic single-launch reduction */
-  DK_V5 = 5  /* tuned: activations loaded first, shape-selected rows per
-                wave and double-buffered stages */
+  DK_V5 = 5  /* tuned: raw buffer loads (activations first), shape-selected
+                rows per wave and activation rows per tile */
 } dk_kernel_version;
 
 #define DK_STAMP_REUSE 15
