@@ -80,6 +80,7 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-quantizer", action="store_true",
                     help="skip the device quantizer measurement")
+    ap.add_argument("--no-mlp", action="store_true", help="skip the MLP decode step measurement")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="budget of the CPU baseline sample")
     ap.add_argument("--out", type=Path, default=None, help="also write the full JSON here")
@@ -241,6 +242,63 @@ def bench_quantizer(roof_gbps, cpu_seconds):
     return out
 
 
+MLP_SHAPES = {
+    "llama7b": (11008, 4096),
+    "llama70b_tp8": (3584, 8192),
+    "llama70b": (28672, 8192),
+}
+
+
+def bench_mlp(roof_gbps, steps):
+    """One MLP decode step (gate/up fused with SiLU*mul, then the down GEMV)
+    at B = 1 per shape, back-to-back in a HIP graph over weight copies that
+    total > 640 MB (cold weights), against the unfused composition a
+    caller of gemv() writes: three GEMVs and a SiLU*mul between them."""
+    import torch
+
+    from decode_kernel import gemv, mlp_decode, quantize_and_pack
+    from dk_bench.common import time_graph_steps
+    from oracle import oracle
+
+    out = {}
+    for name, (i, h) in MLP_SHAPES.items():
+        gen = torch.Generator(device="cuda").manual_seed(4000 + i)
+        one = []
+        for shape in ((i, h), (i, h), (h, i)):
+            one += list(quantize_and_pack(torch.randn(*shape, device="cuda", generator=gen) * 0.02))
+        nbytes = sum(t.numel() * t.element_size() for t in one)
+        copies = [one] + [[t.clone() for t in one] for _ in range(max(1, (640 << 20) // nbytes))]
+        x = torch.randn(1, h, device="cuda", generator=gen).half()
+        y0 = mlp_decode(x, *copies[0])
+        n = len(copies)
+
+        ys = []
+        st, graph = time_graph_steps(lambda k: ys.append(mlp_decode(x, *copies[k % n])), steps=steps)
+        if not torch.equal(ys[-1], y0):
+            raise RuntimeError(f"mlp {name}: graph replay output differs from the eager step")
+        del graph, ys
+
+        def unfused(k):
+            gp, gs, up, us, dp, ds = copies[k % n]
+            g = gemv(gp, gs, x)
+            u = gemv(up, us, x)
+            return gemv(dp, ds, (torch.nn.functional.silu(g.float()) * u.float()).half())
+
+        st_u, graph = time_graph_steps(unfused, steps=steps)
+        del graph
+        moved = oracle.mlp_bytes(i, h, 1)
+        out[name] = {
+            "I": i, "H": h, "batch": 1, "bytes_moved": moved, "weight_copies": n,
+            "fused_p50_us": st["median_us"], "fused_gbps": moved / (st["median_us"] * 1e3),
+            "fused_pct_of_read_roof": 100.0 * moved / (st["median_us"] * 1e3) / roof_gbps,
+            "unfused_p50_us": st_u["median_us"], "speedup": st_u["median_us"] / st["median_us"],
+            "launches": {"fused": 2, "unfused": 6},
+        }
+        del copies
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -322,6 +380,14 @@ def main():
             del copies, xd, p_cpu, s_cpu, x_cpu
             torch.cuda.empty_cache()
 
+    mlp = None
+    if not args.no_mlp:
+        log("[bench] MLP decode step (fused gate/up + SiLU*mul, then down), B=1")
+        mlp = bench_mlp(roof["gbps"], steps=args.other_steps)
+        for name, r in mlp.items():
+            log(f"   {name:13s} fused {r['fused_p50_us']:8.2f} us  {r['fused_gbps']:8.1f} GB/s  "
+                f"{r['fused_pct_of_read_roof']:5.1f}% of read roof; unfused {r['unfused_p50_us']:8.2f} us")
+
     quant = None
     if not args.no_quantizer:
         log("[bench] device quantizer at c4a")
@@ -373,6 +439,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "quantizer": quant,
+        "mlp": mlp,
         "configs": {
             key: {"M": r["M"], "K": r["K"], "batch": r["batch"],
                   "same_size_read_gbps": (round(r["same_size_read"]["gbps"], 1)

@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "decode_kernel/dk_gemv.h"
+#include "decode_kernel/dk_mlp.h"
 
 namespace {
 
@@ -175,6 +176,79 @@ int stream_recommended_blocks() {
   return blocks;
 }
 
+namespace {
+
+const uint32_t* words(const torch::Tensor& t) {
+  return reinterpret_cast<const uint32_t*>(t.data_ptr<int32_t>());
+}
+const uint16_t* halves(const torch::Tensor& t) {
+  return reinterpret_cast<const uint16_t*>(t.data_ptr<at::Half>());
+}
+
+// Gate and up are [I, H] in the GEMV format; x is [B, H].
+void check_gate_up(const torch::Tensor& gate, const torch::Tensor& gate_scales,
+                   const torch::Tensor& up, const torch::Tensor& up_scales,
+                   const torch::Tensor& x) {
+  check_gemv_inputs(gate, gate_scales, x);
+  check_gemv_inputs(up, up_scales, x);
+  TORCH_CHECK(gate.sizes() == up.sizes() && gate_scales.sizes() == up_scales.sizes(),
+              "gate and up must have the same shape [I, H/8] and scales [I, H/128]");
+}
+
+}  // namespace
+
+// h = fp16(silu(gate x) * (up x)): the fused gate/up projection of an MLP
+// decode step. No counterpart in the reference (it composes its gemv).
+torch::Tensor gate_up_silu(torch::Tensor gate, torch::Tensor gate_scales, torch::Tensor up,
+                           torch::Tensor up_scales, torch::Tensor x) {
+  check_gate_up(gate, gate_scales, up, up_scales, x);
+  const int I = static_cast<int>(gate.size(0));
+  const int H = static_cast<int>(gate.size(1) * kNibblesPerWord);
+  const int B = static_cast<int>(x.size(0));
+  c10::DeviceGuard guard(x.device());
+  auto h = torch::empty({B, I}, x.options());
+  if (H == 0) return h.zero_();  // g = u = 0 and silu(0) * 0 = 0
+  check_status(dk_gate_up_silu(words(gate), halves(gate_scales), words(up), halves(up_scales),
+                               halves(x), reinterpret_cast<uint16_t*>(h.data_ptr<at::Half>()), I, H,
+                               B, current_stream(x)),
+               "gate_up_silu");
+  return h;
+}
+
+// y = down fp16(silu(gate x) * (up x)): one MLP decode step, two launches.
+torch::Tensor mlp_decode(torch::Tensor gate, torch::Tensor gate_scales, torch::Tensor up,
+                         torch::Tensor up_scales, torch::Tensor down, torch::Tensor down_scales,
+                         torch::Tensor x) {
+  check_gate_up(gate, gate_scales, up, up_scales, x);
+  const int I = static_cast<int>(gate.size(0));
+  const int H = static_cast<int>(gate.size(1) * kNibblesPerWord);
+  const int B = static_cast<int>(x.size(0));
+  TORCH_CHECK(down.is_cuda() && down_scales.is_cuda() && down.device() == x.device() &&
+                  down_scales.device() == x.device(),
+              "down and its scales must be CUDA tensors on x's device");
+  TORCH_CHECK(down.scalar_type() == torch::kInt32 && down_scales.scalar_type() == torch::kFloat16,
+              "down must be int32 and its scales fp16");
+  TORCH_CHECK(down.dim() == 2 && down_scales.dim() == 2 && down.is_contiguous() &&
+                  down_scales.is_contiguous(),
+              "down [H, I/8] and scales [H, I/128] must be contiguous 2-D tensors");
+  TORCH_CHECK(I % kGroupSize == 0, "I must be divisible by group size 128");
+  TORCH_CHECK(down.size(0) == H && down.size(1) * kNibblesPerWord == I,
+              "down must be [H, I/8] for gate/up [I, H/8]");
+  TORCH_CHECK(down_scales.size(0) == H && down_scales.size(1) == I / kGroupSize,
+              "down scales must be [H, I/128]");
+  c10::DeviceGuard guard(x.device());
+  auto y = torch::empty({B, H}, x.options());
+  if (I == 0) return y.zero_();
+  const size_t ws_bytes = dk_mlp_workspace_bytes(I, H, B);
+  auto ws = torch::empty({static_cast<int64_t>(ws_bytes / 2) + 8}, x.options());
+  check_status(dk_mlp_decode(words(gate), halves(gate_scales), words(up), halves(up_scales),
+                             words(down), halves(down_scales), halves(x),
+                             reinterpret_cast<uint16_t*>(y.data_ptr<at::Half>()), I, H, B,
+                             ws.data_ptr(), ws.nbytes(), current_stream(x)),
+               "mlp_decode");
+  return y;
+}
+
 int last_kernel_stamp() { return dk_last_kernel_stamp(); }
 
 void empty_kernel() {
@@ -195,6 +269,13 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("quantize_and_pack", &quantize_and_pack,
         "fp32 W [M, K] -> (packed int32 [M, K/8], scales fp16 [M, K/128]) on the GPU",
         py::arg("w"));
+  m.def("gate_up_silu", &gate_up_silu,
+        "Fused MLP gate/up projection: fp16(silu(gate x) * (up x)) -> [B, I]", py::arg("gate"),
+        py::arg("gate_scales"), py::arg("up"), py::arg("up_scales"), py::arg("x"));
+  m.def("mlp_decode", &mlp_decode,
+        "MLP decode step: down fp16(silu(gate x) * (up x)) -> [B, H]", py::arg("gate"),
+        py::arg("gate_scales"), py::arg("up"), py::arg("up_scales"), py::arg("down"),
+        py::arg("down_scales"), py::arg("x"));
   m.def("d2d_copy", &d2d_copy, "Aligned device-to-device copy", py::arg("src"), py::arg("dst"));
   m.def("stream_read", &stream_read, "Read-only STREAM sum-reduction (one float partial per block)",
         py::arg("src"), py::arg("partials"));

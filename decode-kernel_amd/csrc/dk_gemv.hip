@@ -7,7 +7,8 @@
 // decode with packed fp16 math, v_dot2_f32_f16 or MFMA products with fp32
 // accumulation, DPP wave reductions and a single-launch split-K.
 //
-// The kernels themselves are in dk_kernels.hpp.
+// The kernels themselves are in dk_kernels.hpp; the fused gate/up kernel of
+// the MLP decode step (dk_mlp.h) is in dk_mlp.hpp and shares the stamp.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -17,7 +18,9 @@
 
 #include "dk_host.hpp"
 #include "dk_kernels.hpp"
+#include "dk_mlp.hpp"
 #include "decode_kernel/dk_gemv.h"
+#include "decode_kernel/dk_mlp.h"
 
 // ===========================================================================
 // Host side: validation, launch selection and the C ABI.
@@ -124,6 +127,26 @@ int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x
   }
   if (B == 2) return launch_v5_t<2, 1, 2>(L, p, s, x, y, M, K, B);
   return launch_v5_t<4, 1, 2>(L, p, s, x, y, M, K, B);
+}
+
+// Fused gate/up (rows per matrix per wave, chunks per stage, batch tile):
+// the v5 shapes with the two matrices counted as 2R rows.
+template <int R, int U, int NB>
+int launch_gate_up_t(const Launch& L, const uint4* g, const uint16_t* gs, const uint4* u,
+                     const uint16_t* us, const uint4* x, uint16_t* h, int I, int H, int B) {
+  const int rows_per_block = kV5WavesPerBlock * R;
+  dim3 grid((I + rows_per_block - 1) / rows_per_block, (B + NB - 1) / NB);
+  return L("gate/up launch", dk::gate_up_silu<R, U, NB>, grid, dim3(kV5WavesPerBlock * 64), 0, g,
+           gs, u, us, x, h, I, H, B);
+}
+
+int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const uint4* u,
+                   const uint16_t* us, const uint4* x, uint16_t* h, int I, int H, int B) {
+  if (B == 1) {
+    if (I >= 8192 && H >= 8192) return launch_gate_up_t<2, 1, 1>(L, g, gs, u, us, x, h, I, H, B);
+    return launch_gate_up_t<1, 2, 1>(L, g, gs, u, us, x, h, I, H, B);
+  }
+  return launch_gate_up_t<1, 1, 2>(L, g, gs, u, us, x, h, I, H, B);
 }
 
 // Waves per 16-row tile on the reuse path (K split across them). Measured on
@@ -282,6 +305,60 @@ int dk_last_kernel_stamp(void) {
     return -1;
   }
   return h;
+}
+
+int dk_gate_up_silu(const uint32_t* gate_packed, const uint16_t* gate_scales,
+                    const uint32_t* up_packed, const uint16_t* up_scales, const uint16_t* x,
+                    uint16_t* h, int I, int H, int B, hipStream_t stream) {
+  if (I <= 0 || H <= 0 || B <= 0) return DK_OK;
+  if (H % DK_GROUP_SIZE != 0)
+    return fail(DK_ERR_INVALID_ARGUMENT, "H=%d must be divisible by group size 128", H);
+  if (H > (1 << 28)) return fail(DK_ERR_UNSUPPORTED, "H=%d exceeds the supported 2^28", H);
+  if ((long long)B * H * 2 > 0x7fffffffLL)
+    return fail(DK_ERR_UNSUPPORTED, "B*H=%lld activation elements exceed 2^30", (long long)B * H);
+  if (!gate_packed || !gate_scales || !up_packed || !up_scales || !x || !h)
+    return fail(DK_ERR_INVALID_ARGUMENT, "gate, up, their scales, x and h must not be NULL");
+  if (!aligned(gate_packed, 16) || !aligned(up_packed, 16) || !aligned(x, 16))
+    return fail(DK_ERR_INVALID_ARGUMENT, "gate, up and x must be 16-byte aligned");
+  if (!aligned(gate_scales, 2) || !aligned(up_scales, 2) || !aligned(h, 2))
+    return fail(DK_ERR_INVALID_ARGUMENT, "scales and h must be 2-byte aligned");
+  return launch_gate_up(Launch{stream}, reinterpret_cast<const uint4*>(gate_packed), gate_scales,
+                        reinterpret_cast<const uint4*>(up_packed), up_scales,
+                        reinterpret_cast<const uint4*>(x), h, I, H, B);
+}
+
+size_t dk_mlp_workspace_bytes(int I, int H, int B) {
+  if (I <= 0 || H <= 0 || B <= 0) return 0;
+  return (size_t)B * (size_t)I * sizeof(uint16_t);
+}
+
+int dk_mlp_decode(const uint32_t* gate_packed, const uint16_t* gate_scales,
+                  const uint32_t* up_packed, const uint16_t* up_scales,
+                  const uint32_t* down_packed, const uint16_t* down_scales, const uint16_t* x,
+                  uint16_t* y, int I, int H, int B, void* workspace, size_t workspace_bytes,
+                  hipStream_t stream) {
+  if (I <= 0 || H <= 0 || B <= 0) return DK_OK;
+  if (I % DK_GROUP_SIZE != 0)
+    return fail(DK_ERR_INVALID_ARGUMENT, "I=%d must be divisible by group size 128", I);
+  const size_t need = dk_mlp_workspace_bytes(I, H, B);
+  if (!workspace || workspace_bytes < need)
+    return fail(DK_ERR_INVALID_ARGUMENT, "the MLP step needs a %zu-byte workspace (got %zu)", need,
+                workspace_bytes);
+  if (!aligned(workspace, 16)) return fail(DK_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+  dk_gemv_config cfg;
+  dk_gemv_config_default(&cfg);
+  // Validate the down projection before anything is launched.
+  int rc = dk_gemv_validate(H, I, B, &cfg);
+  if (rc != DK_OK) return rc;
+  if (!down_packed || !down_scales || !y)
+    return fail(DK_ERR_INVALID_ARGUMENT, "down, its scales and y must not be NULL");
+  if (!aligned(down_packed, 16)) return fail(DK_ERR_INVALID_ARGUMENT, "down must be 16-byte aligned");
+  if (!aligned(down_scales, 2) || !aligned(y, 2))
+    return fail(DK_ERR_INVALID_ARGUMENT, "scales and y must be 2-byte aligned");
+  uint16_t* h = static_cast<uint16_t*>(workspace);
+  rc = dk_gate_up_silu(gate_packed, gate_scales, up_packed, up_scales, x, h, I, H, B, stream);
+  if (rc != DK_OK) return rc;
+  return gemv_impl(down_packed, down_scales, h, y, H, I, B, &cfg, nullptr, 0, Launch{stream});
 }
 
 const char* dk_last_error(void) { return dk::g_err.c_str(); }

@@ -220,10 +220,14 @@ struct V5Stage {
   uint4 xv[U][NB][4];
 };
 
-template <int R, int U, int NB>
+// Loads one stage: rows r < kSplit come from (rw, rs), rows r >= kSplit
+// from (rw2, rs2) as their row r - kSplit (the fused gate/up kernel streams
+// two matrices against one activation load; plain v5 has kSplit = R).
+template <int R, int U, int NB, int kSplit = R>
 __device__ __forceinline__ void v5_load(V5Stage<R, U, NB>& st, __amdgpu_buffer_rsrc_t rw,
                                         __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rx,
-                                        int c0, int nck, int G, int K, int b0, int B, int lane) {
+                                        int c0, int nck, int G, int K, int b0, int B, int lane,
+                                        __amdgpu_buffer_rsrc_t rw2, __amdgpu_buffer_rsrc_t rs2) {
   int c[U];
   bool ok[U];
 #pragma unroll
@@ -243,16 +247,25 @@ __device__ __forceinline__ void v5_load(V5Stage<R, U, NB>& st, __amdgpu_buffer_r
   for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int off = ok[u] ? (r * G + (c[u] >> 2)) * 2 : kOutOfRange;
-      st.s[u][r] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0));
+      const int rr = r < kSplit ? r : r - kSplit;
+      const int off = ok[u] ? (rr * G + (c[u] >> 2)) * 2 : kOutOfRange;
+      st.s[u][r] = h2f(__builtin_amdgcn_raw_buffer_load_b16(r < kSplit ? rs : rs2, off, 0, 0));
     }
 #pragma unroll
   for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int off = ok[u] ? (r * nck + c[u]) * 16 : kOutOfRange;
-      st.w[u][r] = buffer_load16<kLoadNonTemporal>(rw, off);
+      const int rr = r < kSplit ? r : r - kSplit;
+      const int off = ok[u] ? (rr * nck + c[u]) * 16 : kOutOfRange;
+      st.w[u][r] = buffer_load16<kLoadNonTemporal>(r < kSplit ? rw : rw2, off);
     }
+}
+
+template <int R, int U, int NB>
+__device__ __forceinline__ void v5_load(V5Stage<R, U, NB>& st, __amdgpu_buffer_rsrc_t rw,
+                                        __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rx,
+                                        int c0, int nck, int G, int K, int b0, int B, int lane) {
+  v5_load<R, U, NB, R>(st, rw, rs, rx, c0, nck, G, K, b0, B, lane, rw, rs);
 }
 
 template <int R, int U, int NB>

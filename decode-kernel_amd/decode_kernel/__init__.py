@@ -6,6 +6,8 @@ Same op API as python/decode_kernel/__init__.py of the reference: `gemv`,
 `cuda_available`. The compute path is the `decode_kernel._cuda` extension
 over the C ABI in include/decode_kernel/dk_gemv.h; there is no CPU fallback,
 and calling `gemv` without the built extension raises ImportError.
+`mlp_decode`, `gate_up_silu` and `QuantizedMLP` (decode_kernel.mlp) run a
+Llama-style MLP decode step on the same kernels (include/decode_kernel/dk_mlp.h).
 """
 
 from __future__ import annotations
@@ -14,13 +16,17 @@ from typing import Optional
 
 import torch
 
+from .mlp import QuantizedMLP, gate_up_silu, mlp_decode
 from .quantize import GROUP_SIZE, dequantize, quantize_and_pack
 
 __all__ = [
     "GROUP_SIZE",
+    "QuantizedMLP",
     "cuda_available",
     "dequantize",
+    "gate_up_silu",
     "gemv",
+    "mlp_decode",
     "quantize_and_pack",
     "w4a16_linear",
 ]

@@ -1,4 +1,4 @@
-"""ctypes view of the C ABI in include/decode_kernel/dk_gemv.h.
+"""ctypes view of the C ABI in include/decode_kernel/dk_gemv.h and dk_mlp.h.
 
 This is the binding a non-torch host (or a maintainer wiring the library into
 another runtime) would write: plain pointers, sizes and a hipStream_t handle.
@@ -48,6 +48,16 @@ _SIGNATURES = {
          ctypes.POINTER(GemvConfig), _P, ctypes.c_size_t, _P],
     ),
     "dk_quantize_pack_f32": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, _P, _P, _P]),
+    "dk_gate_up_silu": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P],
+    ),
+    "dk_mlp_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "dk_mlp_decode": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P,
+         ctypes.c_size_t, _P],
+    ),
     "dk_d2d_copy": (ctypes.c_int, [_P, _P, ctypes.c_size_t, _P]),
     "dk_stream_read": (ctypes.c_int, [_P, _P, ctypes.c_size_t, ctypes.c_int, _P]),
     "dk_stream_write": (ctypes.c_int, [_P, ctypes.c_size_t, ctypes.c_int, _P]),

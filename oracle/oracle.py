@@ -11,6 +11,9 @@ Restates, function by function:
   linear_fp32         python/decode_kernel/reference.py:17-26
   max_abs_err         python/decode_kernel/reference.py:29-30
   bytes_moved_w4, flop_gemv   bench/common.py:111-125
+  silu_f64, gate_up_silu_f64, mlp_decode_f64: no reference counterpart;
+    the MLP decode step composed from the reference's gemv (linear_f64
+    here) and SiLU, x * sigmoid(x), as torch.nn.functional.silu defines it
 Nibble semantics: csrc/gemv_w4a16.cu:27-29; layout: include/decode_kernel/gemv_w4a16.h:29-33.
 
 How each function is pinned (tests/test_oracle.py):
@@ -25,6 +28,10 @@ How each function is pinned (tests/test_oracle.py):
   * linear_fp32: one-hot activations (each output equals one scaled weight),
     all-ones activations (per-group sums), brute-force pure-Python loops on
     tiny shapes, and the C restatement's float64 GEMV.
+  * silu_f64: silu(0) = 0, the identity silu(-v) = silu(v) - v, limits at
+    +-40, and agreement with v * scipy.special.expit(v).
+  * gate_up_silu_f64 / mlp_decode_f64: brute-force pure-Python loops on tiny
+    shapes, and one-hot activations that select single scaled weights.
 The reference ships no golden-vector files; tests/golden/ holds fixtures this
 oracle generated after being pinned as above, to catch regressions.
 """
@@ -129,3 +136,32 @@ def make_case(m: int, k: int, batch: int, seed: int, w_std: float = 0.02):
     w = (rng.standard_normal((m, k), dtype=np.float32) * np.float32(w_std)).astype(np.float32)
     x = rng.standard_normal((batch, k), dtype=np.float32).astype(np.float16)
     return w, x
+
+
+def silu_f64(v: np.ndarray) -> np.ndarray:
+    """SiLU in float64: v / (1 + exp(-v)) (torch.nn.functional.silu's definition)."""
+    v = np.asarray(v, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        return v / (1.0 + np.exp(-v))
+
+
+def gate_up_silu_f64(x, gate_packed, gate_scales, up_packed, up_scales) -> np.ndarray:
+    """h[B, I] = silu(Wg x) * (Wu x) in float64, before any fp16 rounding."""
+    g = linear_f64(x, gate_packed, gate_scales)
+    u = linear_f64(x, up_packed, up_scales)
+    return silu_f64(g) * u
+
+
+def mlp_decode_f64(x, gate_packed, gate_scales, up_packed, up_scales, down_packed,
+                   down_scales) -> np.ndarray:
+    """y[B, H] = Wd fp16(silu(Wg x) * (Wu x)) in float64 around the one fp16
+    rounding of h that the step's interface has (h is an fp16 tensor)."""
+    h = gate_up_silu_f64(x, gate_packed, gate_scales, up_packed, up_scales).astype(np.float16)
+    return linear_f64(h, down_packed, down_scales)
+
+
+def mlp_bytes(i: int, h: int, batch: int) -> int:
+    """Algorithmic HBM bytes of one MLP decode step: the three weight
+    matrices and their scales, x, h written and read back, and y."""
+    w = 3 * (i * h // 2 + i * h // GROUP_SIZE * 2)
+    return w + batch * h * 2 + 2 * batch * i * 2 + batch * h * 2

@@ -134,11 +134,38 @@ def test_quantizer_argument_checks(lib):
     assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "aligned" in lib.dk_last_error().decode()
 
 
+def test_mlp_argument_checks(lib):
+    fake = 0x10000
+    assert lib.dk_mlp_workspace_bytes(11008, 4096, 2) == 2 * 11008 * 2
+    assert lib.dk_mlp_workspace_bytes(0, 4096, 2) == 0
+    # Empty problems return before touching any pointer.
+    assert lib.dk_gate_up_silu(None, None, None, None, None, None, 0, 128, 1, None) == _abi.DK_OK
+    assert lib.dk_mlp_decode(None, None, None, None, None, None, None, None, 128, 128, 0, None, 0,
+                             None) == _abi.DK_OK
+    rc = lib.dk_gate_up_silu(fake, fake, fake, fake, fake, fake, 4, 200, 1, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "128" in lib.dk_last_error().decode()
+    rc = lib.dk_gate_up_silu(fake, fake, None, fake, fake, fake, 4, 128, 1, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "NULL" in lib.dk_last_error().decode()
+    rc = lib.dk_gate_up_silu(fake, fake, fake + 8, fake, fake, fake, 4, 128, 1, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "16-byte" in lib.dk_last_error().decode()
+    # The MLP step checks I % 128 and its workspace before any launch.
+    rc = lib.dk_mlp_decode(fake, fake, fake, fake, fake, fake, fake, fake, 200, 128, 1, fake, 4096,
+                           None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "I=200" in lib.dk_last_error().decode()
+    rc = lib.dk_mlp_decode(fake, fake, fake, fake, fake, fake, fake, fake, 256, 128, 2, fake, 100,
+                           None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "1024-byte workspace" in lib.dk_last_error().decode()
+    rc = lib.dk_mlp_decode(fake, fake, fake, fake, None, fake, fake, fake, 256, 128, 2, fake, 1024,
+                           None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "NULL" in lib.dk_last_error().decode()
+
+
 def test_torch_extension_surface():
     from decode_kernel import _cuda
 
     for name in ("w4a16_gemv", "d2d_copy", "stream_read", "stream_write",
-                 "stream_recommended_blocks", "last_kernel_stamp", "quantize_and_pack"):
+                 "stream_recommended_blocks", "last_kernel_stamp", "quantize_and_pack",
+                 "gate_up_silu", "mlp_decode"):
         assert hasattr(_cuda, name), name
     doc = _cuda.w4a16_gemv.__doc__
     for pat in (r"version: [\w.]*Int = 5", r"split_k: [\w.]*Int = 4",

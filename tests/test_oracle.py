@@ -248,3 +248,72 @@ def test_golden_fixtures_reproduce():
         assert np.array_equal(packed, data[f"{n}/packed"]), n
         assert np.array_equal(scales.view(np.uint16), data[f"{n}/scales"].view(np.uint16)), n
         assert np.array_equal(oracle.linear_f64(x, packed, scales), data[f"{n}/y"]), n
+
+
+# ------------------------------------------------------- MLP decode step ---
+def test_silu_closed_forms():
+    from scipy.special import expit
+
+    assert oracle.silu_f64(0.0) == 0.0
+    v = np.linspace(-30, 30, 601)
+    # silu(-v) = -v * sigmoid(-v) = -v * (1 - sigmoid(v)) = silu(v) - v
+    np.testing.assert_allclose(oracle.silu_f64(-v), oracle.silu_f64(v) - v, rtol=0, atol=1e-12)
+    np.testing.assert_allclose(oracle.silu_f64(v), v * expit(v), rtol=1e-14, atol=1e-300)
+    assert abs(oracle.silu_f64(40.0) - 40.0) < 1e-15 * 40 * 1e3
+    assert 0 > oracle.silu_f64(-40.0) > -1e-15
+    assert oracle.silu_f64(1.0) == pytest.approx(1.0 / (1.0 + np.e ** -1.0), rel=1e-15)
+
+
+def _brute_linear(x, packed, scales):
+    q = [[((int(packed[m, i // 8]) >> (4 * (i % 8))) & 0xF) for i in range(packed.shape[1] * 8)]
+         for m in range(packed.shape[0])]
+    q = [[v - 16 if v >= 8 else v for v in row] for row in q]
+    out = []
+    for b in range(x.shape[0]):
+        row = []
+        for m in range(packed.shape[0]):
+            acc = 0.0
+            for k in range(len(q[m])):
+                acc += float(scales[m, k // 128]) * q[m][k] * float(x[b, k])
+            row.append(acc)
+        out.append(row)
+    return out
+
+
+def test_gate_up_and_mlp_brute_force_tiny():
+    import math
+
+    rng = np.random.Generator(np.random.PCG64(99))
+    I, H, B = 128, 128, 2
+    gp, gs = oracle.quantize_and_pack(rng.standard_normal((I, H)).astype(np.float32) * 0.1)
+    up, us = oracle.quantize_and_pack(rng.standard_normal((I, H)).astype(np.float32) * 0.1)
+    dp, ds = oracle.quantize_and_pack(rng.standard_normal((H, I)).astype(np.float32) * 0.1)
+    x = rng.standard_normal((B, H)).astype(np.float16)
+    g, u = _brute_linear(x, gp, gs), _brute_linear(x, up, us)
+    h_ref = np.array([[g[b][i] / (1 + math.exp(-g[b][i])) * u[b][i] for i in range(I)]
+                      for b in range(B)])
+    h = oracle.gate_up_silu_f64(x, gp, gs, up, us)
+    np.testing.assert_allclose(h, h_ref, rtol=1e-12, atol=1e-12)
+    y_ref = np.array(_brute_linear(h_ref.astype(np.float16), dp, ds))
+    y = oracle.mlp_decode_f64(x, gp, gs, up, us, dp, ds)
+    np.testing.assert_allclose(y, y_ref, rtol=1e-12, atol=1e-12)
+
+
+def test_gate_up_one_hot_selects_weights():
+    # x = e_k: g = Wg[:, k], u = Wu[:, k] exactly (scale * q).
+    rng = np.random.Generator(np.random.PCG64(5))
+    I, H = 64, 256
+    gp, gs = oracle.quantize_and_pack(rng.standard_normal((I, H)).astype(np.float32))
+    up, us = oracle.quantize_and_pack(rng.standard_normal((I, H)).astype(np.float32))
+    x = np.zeros((1, H), np.float16)
+    x[0, 131] = 1.0
+    wg = oracle.dequantize(gp, gs, dtype=np.float64)[:, 131]
+    wu = oracle.dequantize(up, us, dtype=np.float64)[:, 131]
+    h = oracle.gate_up_silu_f64(x, gp, gs, up, us)[0]
+    np.testing.assert_array_equal(h, wg / (1 + np.exp(-wg)) * wu)
+
+
+def test_mlp_bytes_formula():
+    # 7B MLP: three 11008 x 4096 int4 matrices plus fp16 scales, x, h twice, y.
+    w = 11008 * 4096 // 2 + 11008 * 32 * 2
+    assert oracle.mlp_bytes(11008, 4096, 1) == 3 * w + 4096 * 2 + 2 * 11008 * 2 + 4096 * 2
