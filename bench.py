@@ -44,21 +44,23 @@ METRIC = "HBM read GB/s & % of measured read roof, W4A16 GEMV 4096x4096 B=1; p50
 # name -> (M, K, batches, variants timed). The headline is c0 B=1 with the
 # default op (v5). Seeds follow the config index.
 CONFIGS = {
-    "c0": (4096, 4096, [1], ["v0", "v1", "v1_wpr2", "v1_wpr4", "v2", "v3", "v4", "v5", "reuse"]),
-    "c1": (11008, 4096, [1], ["v5", "v4", "reuse"]),
-    "c2": (4096, 11008, [1], ["v5", "v4", "reuse"]),
+    "c0": (4096, 4096, [1], ["v0", "v1", "v1_wpr2", "v1_wpr4", "v2", "v3", "v4", "v5", "reuse",
+                             "v5_paired"]),
+    "c1": (11008, 4096, [1], ["v5", "v4", "reuse", "v5_paired"]),
+    "c2": (4096, 11008, [1], ["v5", "v4", "reuse", "v5_paired"]),
     "c3": (4096, 4096, [1, 2, 4, 8, 16], ["reuse", "v5", "v4"]),
-    "c4a": (28672, 8192, [1], ["v5", "v4", "reuse"]),
-    "c4b": (8192, 28672, [1], ["v5", "v4", "reuse"]),
+    "c4a": (28672, 8192, [1], ["v5", "v4", "reuse", "v5_paired"]),
+    "c4b": (8192, 28672, [1], ["v5", "v4", "reuse", "v5_paired"]),
 }
 VARIANTS = {
     "v0": dict(version=0), "v1": dict(version=1), "v1_wpr2": dict(version=1, warps_per_row=2),
     "v1_wpr4": dict(version=1, warps_per_row=4), "v2": dict(version=2), "v3": dict(version=3),
     "v4": dict(version=4, split_k=4), "v5": dict(version=5),
     "reuse": dict(version=5, reuse_weights=True),
+    "v5_paired": None,  # the v5 GEMV on weights repacked into the paired layout
 }
 EXPECTED_STAMP = {"v0": 0, "v1": 1, "v1_wpr2": 12, "v1_wpr4": 14, "v2": 2, "v3": 3, "v4": 4,
-                  "v5": 5, "reuse": 15}
+                  "v5": 5, "reuse": 15, "v5_paired": 25}
 PROFILE_TRAFFIC = REPO / "profiles" / "traffic_c0_v5.json"
 
 
@@ -108,7 +110,15 @@ def bench_variant(ext, copies, x, variant, steps, y_ref=None, call_level_flush=N
 
     pk, sc = copies
     kw = VARIANTS[variant]
-    y0 = ext.w4a16_gemv(pk[0], sc[0], x, **kw)
+    if variant == "v5_paired":
+        pk = [ext.repack_paired(p) for p in pk]
+
+        def call(p, s, xx):
+            return ext.w4a16_gemv_paired(p, s, xx)
+    else:
+        def call(p, s, xx):
+            return ext.w4a16_gemv(p, s, xx, **kw)
+    y0 = call(pk[0], sc[0], x)
     stamp = int(ext.last_kernel_stamp())
     if stamp != EXPECTED_STAMP[variant]:
         raise RuntimeError(f"{variant}: dispatch stamp {stamp}, expected {EXPECTED_STAMP[variant]}")
@@ -116,8 +126,7 @@ def bench_variant(ext, copies, x, variant, steps, y_ref=None, call_level_flush=N
         raise RuntimeError(f"{variant}: output differs from the checked headline output")
     n = len(pk)
     ys = []
-    st, graph = time_graph_steps(lambda i: ys.append(ext.w4a16_gemv(pk[i % n], sc[i % n], x, **kw)),
-                                 steps=steps)
+    st, graph = time_graph_steps(lambda i: ys.append(call(pk[i % n], sc[i % n], x)), steps=steps)
     # Every replayed step recomputes the same product: the last one must equal
     # the eager result bit for bit (graph replays checked against eager work).
     if not torch_equal(ys[-1], y0):
@@ -135,9 +144,9 @@ def bench_variant(ext, copies, x, variant, steps, y_ref=None, call_level_flush=N
     if call_level_flush is not None:
         from decode_kernel import gemv
 
-        call = time_gpu(lambda: gemv(pk[0], sc[0], x, **kw), warmup=20, iters=300,
-                        flush=call_level_flush)
-        row["call_events"] = {k2: call[k2] for k2 in ("median_us", "iqr_us", "mean_us", "iters")}
+        ev = time_gpu(lambda: gemv(pk[0], sc[0], x, **kw), warmup=20, iters=300,
+                      flush=call_level_flush)
+        row["call_events"] = {k2: ev[k2] for k2 in ("median_us", "iqr_us", "mean_us", "iters")}
     return row
 
 

@@ -249,6 +249,62 @@ torch::Tensor mlp_decode(torch::Tensor gate, torch::Tensor gate_scales, torch::T
   return y;
 }
 
+namespace {
+
+void check_words(const torch::Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be a CUDA tensor");
+  TORCH_CHECK(t.scalar_type() == torch::kInt32, name, " must be int32 (uint32 bit pattern)");
+  TORCH_CHECK(t.dim() == 2 && t.is_contiguous(), name, " must be a contiguous [M, K/8] tensor");
+  TORCH_CHECK((t.size(1) * kNibblesPerWord) % kGroupSize == 0,
+              "K must be divisible by group size 128");
+  TORCH_CHECK(t.size(0) <= INT32_MAX && t.size(1) * kNibblesPerWord <= INT32_MAX,
+              "M and K must fit in int32");
+}
+
+}  // namespace
+
+// Offline repack into the kernel-native paired layout, and its inverse.
+// No counterpart in the reference (its format is the API format here too).
+torch::Tensor repack_paired(torch::Tensor packed) {
+  check_words(packed, "packed");
+  c10::DeviceGuard guard(packed.device());
+  auto out = torch::empty_like(packed);
+  check_status(dk_repack_paired(words(packed), reinterpret_cast<uint32_t*>(out.data_ptr<int32_t>()),
+                                static_cast<int>(packed.size(0)),
+                                static_cast<int>(packed.size(1) * kNibblesPerWord),
+                                current_stream(packed)),
+               "repack_paired");
+  return out;
+}
+
+torch::Tensor unpack_paired(torch::Tensor paired) {
+  check_words(paired, "paired");
+  c10::DeviceGuard guard(paired.device());
+  auto out = torch::empty_like(paired);
+  check_status(dk_unpack_paired(words(paired), reinterpret_cast<uint32_t*>(out.data_ptr<int32_t>()),
+                                static_cast<int>(paired.size(0)),
+                                static_cast<int>(paired.size(1) * kNibblesPerWord),
+                                current_stream(paired)),
+               "unpack_paired");
+  return out;
+}
+
+// The v5 GEMV on paired weights (stamp 25); checks as w4a16_gemv.
+torch::Tensor w4a16_gemv_paired(torch::Tensor paired, torch::Tensor scales, torch::Tensor x) {
+  check_gemv_inputs(paired, scales, x);
+  const int M = static_cast<int>(paired.size(0));
+  const int K = static_cast<int>(paired.size(1) * kNibblesPerWord);
+  const int B = static_cast<int>(x.size(0));
+  c10::DeviceGuard guard(x.device());
+  auto y = torch::empty({B, M}, x.options());
+  if (K == 0) return y.zero_();
+  check_status(dk_w4a16_gemv_paired(words(paired), halves(scales), halves(x),
+                                    reinterpret_cast<uint16_t*>(y.data_ptr<at::Half>()), M, K, B,
+                                    current_stream(x)),
+               "w4a16_gemv_paired");
+  return y;
+}
+
 int last_kernel_stamp() { return dk_last_kernel_stamp(); }
 
 void empty_kernel() {
@@ -276,6 +332,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "MLP decode step: down fp16(silu(gate x) * (up x)) -> [B, H]", py::arg("gate"),
         py::arg("gate_scales"), py::arg("up"), py::arg("up_scales"), py::arg("down"),
         py::arg("down_scales"), py::arg("x"));
+  m.def("repack_paired", &repack_paired,
+        "Repack int32 [M, K/8] weights into the kernel-native paired layout", py::arg("packed"));
+  m.def("unpack_paired", &unpack_paired, "Inverse of repack_paired (bit for bit)",
+        py::arg("paired"));
+  m.def("w4a16_gemv_paired", &w4a16_gemv_paired, "v5 W4A16 GEMV on paired-layout weights",
+        py::arg("paired"), py::arg("scales"), py::arg("x"));
   m.def("d2d_copy", &d2d_copy, "Aligned device-to-device copy", py::arg("src"), py::arg("dst"));
   m.def("stream_read", &stream_read, "Read-only STREAM sum-reduction (one float partial per block)",
         py::arg("src"), py::arg("partials"));

@@ -52,6 +52,12 @@ __device__ __forceinline__ void unpack_word(uint32_t w, h2_t (&q)[4]) {
   q[3] = as_h2((v & 0x00F000F0u) ^ 0x64806480u) * sixteenth + sub16;
 }
 
+// The kernel-native "paired" layout (an offline repack of the format above,
+// dk_repack_paired) permutes each word's two's-complement nibbles so that
+// q_{2j} sits at bits 4j..4j+3 and q_{2j+1} at bits 16+4j..19+4j. The same
+// unpack_word then yields (q0,q1), (q2,q3), (q4,q5), (q6,q7): the natural
+// fp16 pairs of eight consecutive activations, which need no v_perm.
+
 // Pair eight consecutive fp16 activations (one 16-byte load: .x=(x0,x1),
 // .y=(x2,x3), .z=(x4,x5), .w=(x6,x7)) to match unpack_word's order.
 __device__ __forceinline__ void pair_x(const uint4& xv, h2_t (&p)[4]) {
@@ -91,6 +97,26 @@ __device__ __forceinline__ h8_t pair_x8(const uint4& xv) {
   r[4] = p[2][0]; r[5] = p[2][1]; r[6] = p[3][0]; r[7] = p[3][1];
   return r;
 }
+
+// Weight layouts the streaming kernels read: how a word decodes and how
+// eight activations are paired to match it.
+struct LayoutLogical {
+  static constexpr int kStamp = 5;
+  static constexpr bool kLoadsFirst = false;
+  static __device__ __forceinline__ void unpack(uint32_t w, h2_t (&q)[4]) { unpack_word(w, q); }
+  static __device__ __forceinline__ void pair(const uint4& xv, h2_t (&p)[4]) { pair_x(xv, p); }
+};
+struct LayoutPaired {
+  static constexpr int kStamp = 25;
+  static constexpr bool kLoadsFirst = true;
+  static __device__ __forceinline__ void unpack(uint32_t w, h2_t (&q)[4]) { unpack_word(w, q); }
+  static __device__ __forceinline__ void pair(const uint4& xv, h2_t (&p)[4]) {
+    p[0] = as_h2(xv.x);  // (x0, x1)
+    p[1] = as_h2(xv.y);  // (x2, x3)
+    p[2] = as_h2(xv.z);  // (x4, x5)
+    p[3] = as_h2(xv.w);  // (x6, x7)
+  }
+};
 
 template <int kCtrl, int kRowMask = 0xF>
 __device__ __forceinline__ float dpp(float v) {

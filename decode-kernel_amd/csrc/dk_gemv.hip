@@ -108,29 +108,36 @@ struct Launch {
 // renumbering (finer-grained blocks of rows per XCD).
 constexpr int kV5WavesPerBlock = 2;
 
-template <int R, int U, int NB>
+template <int R, int U, int NB, typename Layout>
 int launch_v5_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                 int M, int K, int B) {
   const int rows_per_block = kV5WavesPerBlock * R;
   dim3 grid((M + rows_per_block - 1) / rows_per_block, (B + NB - 1) / NB);
-  return L("v5 launch", dk::gemv_v5<R, U, NB>, grid, dim3(kV5WavesPerBlock * 64), 0, p, s, x, y,
-           M, K, B);
+  return L("v5 launch", dk::gemv_v5<R, U, NB, Layout>, grid, dim3(kV5WavesPerBlock * 64), 0, p, s,
+           x, y, M, K, B);
 }
 
+template <typename Layout = dk::LayoutLogical>
 int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y, int M,
               int K, int B) {
   if (B == 1) {
     // Four rows per wave once both dimensions are large: still >= 2048 waves,
     // and half the activation loads and pairing per weight.
-    if (M >= 8192 && K >= 8192) return launch_v5_t<4, 1, 1>(L, p, s, x, y, M, K, B);
-    return launch_v5_t<2, 2, 1>(L, p, s, x, y, M, K, B);
+    if (M >= 8192 && K >= 8192) return launch_v5_t<4, 1, 1, Layout>(L, p, s, x, y, M, K, B);
+    return launch_v5_t<2, 2, 1, Layout>(L, p, s, x, y, M, K, B);
   }
-  if (B == 2) return launch_v5_t<2, 1, 2>(L, p, s, x, y, M, K, B);
-  return launch_v5_t<4, 1, 2>(L, p, s, x, y, M, K, B);
+  if (B == 2) return launch_v5_t<2, 1, 2, Layout>(L, p, s, x, y, M, K, B);
+  return launch_v5_t<4, 1, 2, Layout>(L, p, s, x, y, M, K, B);
 }
 
-// Fused gate/up (rows per matrix per wave, chunks per stage, batch tile):
-// the v5 shapes with the two matrices counted as 2R rows.
+// Fused gate/up (R rows of each matrix per wave, U chunks per stage, NB
+// batch rows per tile), from a sweep on MI355X, back-to-back over cold
+// weights (us per launch for both matrices):
+//   I = 11008, H = 4096:  R2 U1 10.71 (R1 U2 10.84; two v5 GEMVs 13.6)
+//   I = 14336, H = 4096:  R2 U2 12.81, R2 U1 13.04 (R1 U2 13.34)
+//   I = 3584,  H = 8192:  R2 U1 8.16 (R1 U2 9.06; R4 U1 11.33)
+//   I = 28672, H = 8192:  R4 U1 41.37 (R2 U1 44.60; two v5 GEMVs 49.3)
+//   I = 11008, H = 4096, B = 4: R2 U1 NB2 22.14 (R1 U1 NB2 27.48)
 template <int R, int U, int NB>
 int launch_gate_up_t(const Launch& L, const uint4* g, const uint16_t* gs, const uint4* u,
                      const uint16_t* us, const uint4* x, uint16_t* h, int I, int H, int B) {
@@ -143,10 +150,10 @@ int launch_gate_up_t(const Launch& L, const uint4* g, const uint16_t* gs, const 
 int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const uint4* u,
                    const uint16_t* us, const uint4* x, uint16_t* h, int I, int H, int B) {
   if (B == 1) {
-    if (I >= 8192 && H >= 8192) return launch_gate_up_t<2, 1, 1>(L, g, gs, u, us, x, h, I, H, B);
-    return launch_gate_up_t<1, 2, 1>(L, g, gs, u, us, x, h, I, H, B);
+    if (I >= 16384 && H >= 8192) return launch_gate_up_t<4, 1, 1>(L, g, gs, u, us, x, h, I, H, B);
+    return launch_gate_up_t<2, 1, 1>(L, g, gs, u, us, x, h, I, H, B);
   }
-  return launch_gate_up_t<1, 1, 2>(L, g, gs, u, us, x, h, I, H, B);
+  return launch_gate_up_t<2, 1, 2>(L, g, gs, u, us, x, h, I, H, B);
 }
 
 // Waves per 16-row tile on the reuse path (K split across them). Measured on
@@ -305,6 +312,23 @@ int dk_last_kernel_stamp(void) {
     return -1;
   }
   return h;
+}
+
+int dk_w4a16_gemv_paired(const uint32_t* paired, const uint16_t* scales, const uint16_t* x,
+                         uint16_t* y, int M, int K, int B, hipStream_t stream) {
+  dk_gemv_config cfg;
+  dk_gemv_config_default(&cfg);
+  int rc = dk_gemv_validate(M, K, B, &cfg);
+  if (rc != DK_OK) return rc;
+  if (M <= 0 || K <= 0 || B <= 0) return DK_OK;
+  if (!paired || !scales || !x || !y)
+    return fail(DK_ERR_INVALID_ARGUMENT, "paired, scales, x and y must not be NULL");
+  if (!aligned(paired, 16) || !aligned(x, 16))
+    return fail(DK_ERR_INVALID_ARGUMENT, "paired and x must be 16-byte aligned");
+  if (!aligned(scales, 2) || !aligned(y, 2))
+    return fail(DK_ERR_INVALID_ARGUMENT, "scales and y must be 2-byte aligned");
+  return launch_v5<dk::LayoutPaired>(Launch{stream}, reinterpret_cast<const uint4*>(paired), scales,
+                                     reinterpret_cast<const uint4*>(x), y, M, K, B);
 }
 
 int dk_gate_up_silu(const uint32_t* gate_packed, const uint16_t* gate_scales,

@@ -53,7 +53,76 @@ __global__ __launch_bounds__(256) void quantize_pack_kernel(const float4* __rest
   if ((i & 15) == 0) scales[i >> 4] = f2h(scale);
 }
 
+// Reference word (nibble n at bits 4n) <-> paired word (even nibbles in the
+// low half, odd nibbles in the high half, in order): a fixed permutation of
+// the eight two's-complement nibbles.
+__device__ __forceinline__ uint32_t to_paired(uint32_t w) {
+  uint32_t p = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    p |= ((w >> (8 * j)) & 0xFu) << (4 * j);
+    p |= ((w >> (8 * j + 4)) & 0xFu) << (16 + 4 * j);
+  }
+  return p;
+}
+
+__device__ __forceinline__ uint32_t from_paired(uint32_t p) {
+  uint32_t w = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    w |= ((p >> (4 * j)) & 0xFu) << (8 * j);
+    w |= ((p >> (16 + 4 * j)) & 0xFu) << (8 * j + 4);
+  }
+  return w;
+}
+
+template <bool kToPaired>
+__global__ __launch_bounds__(256) void repack_kernel(const uint4* __restrict__ src,
+                                                     uint4* __restrict__ dst, long long n4) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n4) return;
+  uint4 v = src[i];
+  if (kToPaired) {
+    v = make_uint4(to_paired(v.x), to_paired(v.y), to_paired(v.z), to_paired(v.w));
+  } else {
+    v = make_uint4(from_paired(v.x), from_paired(v.y), from_paired(v.z), from_paired(v.w));
+  }
+  dst[i] = v;
+}
+
 }  // namespace dk
+
+namespace {
+
+template <bool kToPaired>
+int repack(const uint32_t* src, uint32_t* dst, int M, int K, hipStream_t stream) {
+  if (M < 0 || K < 0) return dk::set_error(DK_ERR_INVALID_ARGUMENT, "M and K must be >= 0");
+  if (M == 0 || K == 0) return DK_OK;
+  if (K % DK_GROUP_SIZE != 0)
+    return dk::set_error(DK_ERR_INVALID_ARGUMENT, "K=%d is not divisible by group_size=128", K);
+  if (!src || !dst) return dk::set_error(DK_ERR_INVALID_ARGUMENT, "src and dst must not be NULL");
+  if (reinterpret_cast<uintptr_t>(src) % 16 != 0 || reinterpret_cast<uintptr_t>(dst) % 16 != 0)
+    return dk::set_error(DK_ERR_INVALID_ARGUMENT, "src and dst must be 16-byte aligned");
+  // K % 128 == 0, so every row is a whole number of 16-byte chunks.
+  const long long n4 = (long long)M * (K / 32);
+  const long long blocks = (n4 + 255) / 256;
+  if (blocks > 0x7fffffffLL) return dk::set_error(DK_ERR_UNSUPPORTED, "M*K too large");
+  hipLaunchKernelGGL(dk::repack_kernel<kToPaired>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     reinterpret_cast<const uint4*>(src), reinterpret_cast<uint4*>(dst), n4);
+  return dk::check_launch("repack launch");
+}
+
+}  // namespace
+
+extern "C" int dk_repack_paired(const uint32_t* packed, uint32_t* paired, int M, int K,
+                                hipStream_t stream) {
+  return repack<true>(packed, paired, M, K, stream);
+}
+
+extern "C" int dk_unpack_paired(const uint32_t* paired, uint32_t* packed, int M, int K,
+                                hipStream_t stream) {
+  return repack<false>(paired, packed, M, K, stream);
+}
 
 extern "C" int dk_quantize_pack_f32(const float* w, int M, int K, uint32_t* packed,
                                     uint16_t* scales, hipStream_t stream) {

@@ -7,7 +7,9 @@ Same op API as python/decode_kernel/__init__.py of the reference: `gemv`,
 over the C ABI in include/decode_kernel/dk_gemv.h; there is no CPU fallback,
 and calling `gemv` without the built extension raises ImportError.
 `mlp_decode`, `gate_up_silu` and `QuantizedMLP` (decode_kernel.mlp) run a
-Llama-style MLP decode step on the same kernels (include/decode_kernel/dk_mlp.h).
+Llama-style MLP decode step on the same kernels (include/decode_kernel/dk_mlp.h);
+`repack_paired` / `gemv_paired` (decode_kernel.layout) use the kernel-native
+paired weight layout.
 """
 
 from __future__ import annotations
@@ -16,6 +18,7 @@ from typing import Optional
 
 import torch
 
+from .layout import gemv_paired, repack_paired, unpack_paired
 from .mlp import QuantizedMLP, gate_up_silu, mlp_decode
 from .quantize import GROUP_SIZE, dequantize, quantize_and_pack
 
@@ -26,8 +29,11 @@ __all__ = [
     "dequantize",
     "gate_up_silu",
     "gemv",
+    "gemv_paired",
     "mlp_decode",
     "quantize_and_pack",
+    "repack_paired",
+    "unpack_paired",
     "w4a16_linear",
 ]
 

@@ -48,6 +48,12 @@ _SIGNATURES = {
          ctypes.POINTER(GemvConfig), _P, ctypes.c_size_t, _P],
     ),
     "dk_quantize_pack_f32": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, _P, _P, _P]),
+    "dk_repack_paired": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.c_int, _P]),
+    "dk_unpack_paired": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.c_int, _P]),
+    "dk_w4a16_gemv_paired": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P],
+    ),
     "dk_gate_up_silu": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P],

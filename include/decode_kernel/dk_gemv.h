@@ -91,6 +91,27 @@ int dk_w4a16_gemv(const uint32_t* packed, const uint16_t* scales,
                   const dk_gemv_config* cfg, void* workspace,
                   size_t workspace_bytes, hipStream_t stream);
 
+/* Kernel-native "paired" weight layout: the same two's-complement int4
+ * nibbles and scales, with each word's nibbles permuted so that q_{2j} is at
+ * bits 4j..4j+3 and q_{2j+1} at bits 16+4j..19+4j (j = 0..3). The decode
+ * then yields the natural activation pairs (x_{2j}, x_{2j+1}), so the GEMV
+ * skips the activation pairing permutes. Scales are unchanged. An offline
+ * repack of packed [M, K/8]; dk_unpack_paired inverts it bit for bit.
+ * No counterpart in the reference, whose format (quantize.py:1-15) is the
+ * API format here too. */
+#define DK_STAMP_PAIRED 25
+
+int dk_repack_paired(const uint32_t* packed, uint32_t* paired, int M, int K,
+                     hipStream_t stream);
+int dk_unpack_paired(const uint32_t* paired, uint32_t* packed, int M, int K,
+                     hipStream_t stream);
+
+/* The v5 GEMV on paired weights (stamp DK_STAMP_PAIRED); arguments, checks
+ * and results as dk_w4a16_gemv with the default configuration. */
+int dk_w4a16_gemv_paired(const uint32_t* paired, const uint16_t* scales,
+                         const uint16_t* x, uint16_t* y, int M, int K, int B,
+                         hipStream_t stream);
+
 /* Quantize fp32 W[M, K] (row-major, 16-byte aligned) into the format above:
  * packed [M, K/8] and fp16 scales [M, K/128], bit-exact with the reference
  * quantizer on fp32 input: per 128-group scale = max(amax/7, 1e-8) in fp32,

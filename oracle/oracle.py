@@ -11,6 +11,8 @@ Restates, function by function:
   linear_fp32         python/decode_kernel/reference.py:17-26
   max_abs_err         python/decode_kernel/reference.py:29-30
   bytes_moved_w4, flop_gemv   bench/common.py:111-125
+  repack_paired, unpack_paired: no reference counterpart; the kernel-native
+    nibble order (q_{2j} at bits 4j, q_{2j+1} at bits 16+4j)
   silu_f64, gate_up_silu_f64, mlp_decode_f64: no reference counterpart;
     the MLP decode step composed from the reference's gemv (linear_f64
     here) and SiLU, x * sigmoid(x), as torch.nn.functional.silu defines it
@@ -28,6 +30,9 @@ How each function is pinned (tests/test_oracle.py):
   * linear_fp32: one-hot activations (each output equals one scaled weight),
     all-ones activations (per-group sums), brute-force pure-Python loops on
     tiny shapes, and the C restatement's float64 GEMV.
+  * repack_paired / unpack_paired: hand-permuted words (0x76543210 ->
+    0x75316420, 0x09ABCDEF -> 0x0ACE9BDF), inverse round trip, and the
+    per-nibble definition on random words.
   * silu_f64: silu(0) = 0, the identity silu(-v) = silu(v) - v, limits at
     +-40, and agreement with v * scipy.special.expit(v).
   * gate_up_silu_f64 / mlp_decode_f64: brute-force pure-Python loops on tiny
@@ -165,3 +170,23 @@ def mlp_bytes(i: int, h: int, batch: int) -> int:
     matrices and their scales, x, h written and read back, and y."""
     w = 3 * (i * h // 2 + i * h // GROUP_SIZE * 2)
     return w + batch * h * 2 + 2 * batch * i * 2 + batch * h * 2
+
+
+def repack_paired(packed: np.ndarray) -> np.ndarray:
+    """API-format words -> paired words: nibble 2j to bits 4j, nibble 2j+1 to bits 16+4j."""
+    w = np.asarray(packed).astype(np.uint32)
+    p = np.zeros_like(w)
+    for j in range(4):
+        p |= ((w >> np.uint32(8 * j)) & np.uint32(0xF)) << np.uint32(4 * j)
+        p |= ((w >> np.uint32(8 * j + 4)) & np.uint32(0xF)) << np.uint32(16 + 4 * j)
+    return p.view(np.int32)
+
+
+def unpack_paired(paired: np.ndarray) -> np.ndarray:
+    """Inverse of repack_paired."""
+    p = np.asarray(paired).astype(np.uint32)
+    w = np.zeros_like(p)
+    for j in range(4):
+        w |= ((p >> np.uint32(4 * j)) & np.uint32(0xF)) << np.uint32(8 * j)
+        w |= ((p >> np.uint32(16 + 4 * j)) & np.uint32(0xF)) << np.uint32(8 * j + 4)
+    return w.view(np.int32)

@@ -160,12 +160,29 @@ def test_mlp_argument_checks(lib):
     assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "NULL" in lib.dk_last_error().decode()
 
 
+def test_paired_layout_argument_checks(lib):
+    fake = 0x10000
+    assert lib.dk_repack_paired(None, None, 0, 128, None) == _abi.DK_OK
+    rc = lib.dk_repack_paired(fake, fake, 4, 200, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "group_size=128" in lib.dk_last_error().decode()
+    rc = lib.dk_unpack_paired(fake + 4, fake, 4, 128, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "16-byte" in lib.dk_last_error().decode()
+    assert lib.dk_w4a16_gemv_paired(None, None, None, None, 0, 128, 1, None) == _abi.DK_OK
+    rc = lib.dk_w4a16_gemv_paired(None, None, None, None, 4, 128, 1, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "NULL" in lib.dk_last_error().decode()
+    rc = lib.dk_w4a16_gemv_paired(fake, fake, fake, fake, 4, 200, 1, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "group size" in lib.dk_last_error().decode()
+    rc = lib.dk_w4a16_gemv_paired(fake + 8, fake, fake, fake, 4, 128, 1, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "16-byte" in lib.dk_last_error().decode()
+
+
 def test_torch_extension_surface():
     from decode_kernel import _cuda
 
     for name in ("w4a16_gemv", "d2d_copy", "stream_read", "stream_write",
                  "stream_recommended_blocks", "last_kernel_stamp", "quantize_and_pack",
-                 "gate_up_silu", "mlp_decode"):
+                 "gate_up_silu", "mlp_decode", "repack_paired", "unpack_paired",
+                 "w4a16_gemv_paired"):
         assert hasattr(_cuda, name), name
     doc = _cuda.w4a16_gemv.__doc__
     for pat in (r"version: [\w.]*Int = 5", r"split_k: [\w.]*Int = 4",

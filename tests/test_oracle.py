@@ -317,3 +317,25 @@ def test_mlp_bytes_formula():
     # 7B MLP: three 11008 x 4096 int4 matrices plus fp16 scales, x, h twice, y.
     w = 11008 * 4096 // 2 + 11008 * 32 * 2
     assert oracle.mlp_bytes(11008, 4096, 1) == 3 * w + 4096 * 2 + 2 * 11008 * 2 + 4096 * 2
+
+
+# ------------------------------------------------------- paired layout ---
+def test_paired_layout_hand_words():
+    w = np.array([[0x76543210, 0x09ABCDEF]], dtype=np.uint32).view(np.int32)
+    p = oracle.repack_paired(w).view(np.uint32)
+    assert int(p[0, 0]) == 0x75316420
+    assert int(p[0, 1]) == 0x0ACE9BDF
+    np.testing.assert_array_equal(oracle.unpack_paired(oracle.repack_paired(w)), w)
+
+
+def test_paired_layout_per_nibble_definition():
+    rng = np.random.Generator(np.random.PCG64(17))
+    w = rng.integers(0, 1 << 32, size=(8, 64), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    p = oracle.repack_paired(w).view(np.uint32)
+    for (m, i), word in np.ndenumerate(w.view(np.uint32)):
+        nib = [(int(word) >> (4 * n)) & 0xF for n in range(8)]
+        pw = int(p[m, i])
+        for j in range(4):
+            assert (pw >> (4 * j)) & 0xF == nib[2 * j]
+            assert (pw >> (16 + 4 * j)) & 0xF == nib[2 * j + 1]
+    np.testing.assert_array_equal(oracle.unpack_paired(oracle.repack_paired(w)), w)
