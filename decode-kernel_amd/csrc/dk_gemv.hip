@@ -156,16 +156,37 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
   return launch_gate_up_t<2, 1, 2>(L, g, gs, u, us, x, h, I, H, B);
 }
 
-// Waves per 16-row tile on the reuse path (K split across them). Measured on
-// MI355X, back-to-back over cold weights, M = 4096, K = 4096: 16 waves give
-// 5.3 / 6.0 us at B = 1 / 4 and 8 waves 7.9 us at B = 16 (4 waves: 8.3-9.5);
-// with 512 or more tiles (M >= 8192) 8 waves per tile are enough.
-int reuse_waves(int M, int B) {
+// Reuse-path shapes (waves per 16-row tile, groups per stage, scales staged
+// in LDS or loaded directly), measured on MI355X back-to-back over cold
+// weights (us per launch):
+//   M = K = 4096:  B = 1: direct KS16 UG2 4.86 (staged KS16 5.20)
+//                  B = 4: direct KS16 UG2 5.48 (staged KS16 5.84)
+//                  B = 16: direct KS8 UG1 7.34 (staged KS8 7.76)
+//   M = 11008, K = 4096, B = 16: direct KS8 17.60, staged KS8 17.47
+//   M = 28672, K = 8192, B = 1: staged KS8 36.0 (direct KS8 38.3)
+//   M = 8192, K = 28672: B = 1 staged KS8 35.7 (direct 42.3); B = 16 staged KS8 72.2
+// Staged scales win once rows are long (the LDS copy is amortised over many
+// groups; direct scale loads add four loads per group); with 512 or more
+// tiles (M >= 8192) 8 waves per tile are enough.
+enum class ReuseShape { kDirect16x2, kDirect8x1, kStaged16, kStaged8 };
+
+ReuseShape reuse_shape(int M, int K, int B) {
   const int tiles = (M + 15) / 16;
-  return (tiles >= 512 || B > 4) ? 8 : 16;
+  // Rows too long for the staged copy in LDS take the direct path too.
+  const bool fits = dk::reuse_lds_bytes_for(16, K, true) <= (size_t)lds_limit_bytes();
+  if (K <= 4096 || !fits)
+    return (B <= 4 && tiles < 512) ? ReuseShape::kDirect16x2 : ReuseShape::kDirect8x1;
+  return (tiles >= 512 || B > 4) ? ReuseShape::kStaged8 : ReuseShape::kStaged16;
 }
 
-size_t reuse_lds_bytes(int K) { return dk::reuse_lds_bytes_for(16, K); }
+size_t reuse_lds_bytes(int M, int K, int B) {
+  switch (reuse_shape(M, K, B)) {
+    case ReuseShape::kDirect16x2: return dk::reuse_lds_bytes_for(16, K, false);
+    case ReuseShape::kDirect8x1: return dk::reuse_lds_bytes_for(8, K, false);
+    case ReuseShape::kStaged16: return dk::reuse_lds_bytes_for(16, K, true);
+    default: return dk::reuse_lds_bytes_for(8, K, true);
+  }
+}
 
 size_t v3_lds_bytes(int K) { return (size_t)kWavesPerBlock * (K / DK_GROUP_SIZE) * sizeof(uint16_t); }
 
@@ -199,11 +220,21 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
 
   if (cfg->reuse_weights) {
     dim3 grid((M + 15) / 16, (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
-    if (reuse_waves(M, B) == 16)
-      return L("reuse launch", dk::gemv_reuse<16>, grid, dim3(16 * 64),
-               dk::reuse_lds_bytes_for(16, K), p4, scales, x4, y, M, K, B);
-    return L("reuse launch", dk::gemv_reuse<8>, grid, dim3(8 * 64), dk::reuse_lds_bytes_for(8, K),
-             p4, scales, x4, y, M, K, B);
+    const size_t lds = reuse_lds_bytes(M, K, B);
+    switch (reuse_shape(M, K, B)) {
+      case ReuseShape::kDirect16x2:
+        return L("reuse launch", dk::gemv_reuse<16, 2, false>, grid, dim3(16 * 64), lds, p4, scales,
+                 x4, y, M, K, B);
+      case ReuseShape::kDirect8x1:
+        return L("reuse launch", dk::gemv_reuse<8, 1, false>, grid, dim3(8 * 64), lds, p4, scales,
+                 x4, y, M, K, B);
+      case ReuseShape::kStaged16:
+        return L("reuse launch", dk::gemv_reuse<16, 1, true>, grid, dim3(16 * 64), lds, p4, scales,
+                 x4, y, M, K, B);
+      default:
+        return L("reuse launch", dk::gemv_reuse<8, 1, true>, grid, dim3(8 * 64), lds, p4, scales,
+                 x4, y, M, K, B);
+    }
   }
   const dim3 block4(kWavesPerBlock * 64);
   const dim3 rows4((M + kWavesPerBlock - 1) / kWavesPerBlock);
@@ -264,9 +295,9 @@ int dk_gemv_validate(int M, int K, int B, const dk_gemv_config* cfg) {
   if ((long long)B * K * 2 > 0x7fffffffLL)
     return fail(DK_ERR_UNSUPPORTED, "B*K=%lld activation elements exceed 2^30", (long long)B * K);
   if (cfg->reuse_weights) {
-    if (reuse_lds_bytes(K) > (size_t)lds_limit_bytes())
+    if (reuse_lds_bytes(M, K, B) > (size_t)lds_limit_bytes())
       return fail(DK_ERR_UNSUPPORTED, "K=%d needs %zu B of LDS on the reuse path (limit %d)", K,
-                  reuse_lds_bytes(K), lds_limit_bytes());
+                  reuse_lds_bytes(M, K, B), lds_limit_bytes());
   } else if (cfg->version == DK_V3) {
     if (v3_lds_bytes(K) > (size_t)lds_limit_bytes())
       return fail(DK_ERR_UNSUPPORTED, "K=%d needs %zu B of LDS on v3 (limit %d)", K, v3_lds_bytes(K),

@@ -442,72 +442,114 @@ __global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
 // ... (adjacent groups stream side by side). Lane l loads row l%16, bytes
 // [64g + 16(l/16), +16) of group g: four words = four MFMA k-steps that
 // together cover exactly group g, so the fp32 tile result of a group is
-// scaled once (scales staged transposed in LDS) and accumulated. The KS wave
-// partials are added in LDS in wave order. Loads are raw buffer loads; rows
-// past M and batch rows past B read zero through out-of-range offsets.
+// scaled once and accumulated. The KS wave partials are added in LDS in wave
+// order. Loads are raw buffer loads; rows past M and batch rows past B read
+// zero through out-of-range offsets.
 //   A (16x32, weights): lane l -> row l%16, 8 k-slots of lane group l/16
 //   B (32x16, x):       lane l -> batch l%16, same 8 k-slots
 //   D (16x16):          lane l -> rows 4(l/16)+v, batch l%16
+// Scales, two ways (kStaged):
+//   * staged: the tile's scales are copied transposed into LDS first, then
+//     one group per iteration (best for long rows, where the copy is
+//     amortised over many groups);
+//   * direct: no staging round trip before the first weight load; each lane
+//     loads the four scales of its D rows with the activations and weights,
+//     UG groups per stage (best for K <= 4096: 3-6% at M = K = 4096).
 // ---------------------------------------------------------------------------
 constexpr int kReuseBatch = 16;
 
-__host__ __device__ constexpr size_t reuse_lds_bytes_for(int ks, int K) {
-  return (size_t)ks * 256 * sizeof(float) + (size_t)16 * (K / kGroupSize) * sizeof(uint16_t);
+__host__ __device__ constexpr size_t reuse_lds_bytes_for(int ks, int K, bool staged) {
+  return (size_t)ks * 256 * sizeof(float) +
+         (staged ? (size_t)16 * (K / kGroupSize) * sizeof(uint16_t) : 0);
 }
 
-template <int KS>
+template <int KS, int UG, bool kStaged>
 __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ packed,
                                                       const uint16_t* __restrict__ scales,
                                                       const uint4* __restrict__ x4,
                                                       uint16_t* __restrict__ y, int M, int K,
                                                       int B) {
+  static_assert(!kStaged || UG == 1, "the staged variant takes one group per iteration");
   write_stamp(DK_STAMP_REUSE);
   extern __shared__ float lds_reuse[];
   const int G = K >> 7;
   const int nck = K >> 5;
   float* red = lds_reuse;                                             // [KS][64][4]
-  uint16_t* sT = reinterpret_cast<uint16_t*>(lds_reuse + KS * 256);   // [G][16]
+  uint16_t* sT = reinterpret_cast<uint16_t*>(lds_reuse + KS * 256);   // [G][16], staged only
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row0 = blockIdx.x * 16;
   const int b0 = blockIdx.y * kReuseBatch;
 
-  // Stage the tile's scales transposed: sT[g][r] = scales[row0 + r][g].
-  for (int e = threadIdx.x; e < 16 * G; e += blockDim.x) {
-    const int r = e / G, g = e - r * G;
-    const int row = min(row0 + r, M - 1);
-    sT[g * 16 + r] = scales[(size_t)row * G + g];
+  if (kStaged) {
+    // sT[g][r] = scales[row0 + r][g].
+    for (int e = threadIdx.x; e < 16 * G; e += blockDim.x) {
+      const int r = e / G, g = e - r * G;
+      const int row = min(row0 + r, M - 1);
+      sT[g * 16 + r] = scales[(size_t)row * G + g];
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   const int r_lane = lane & 15;  // A row / B batch column
   const int kq = lane >> 4;      // lane group: 16-byte quarter of a group
   const int b = b0 + r_lane;
   const int rows = min(16, M - row0);
   const auto rw = buffer_rsrc(packed + (size_t)row0 * nck, (uint32_t)(rows * (K / 2)));
+  const auto rs = buffer_rsrc(scales + (size_t)row0 * G, (uint32_t)(rows * G * 2));
   const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
   const int xbase = b < B ? b * K * 2 + kq * 64 : kOutOfRange;
   const int wbase = (r_lane * nck + kq) * 16;
 
   f4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int g = wave; g < G; g += KS) {
-    uint4 xv[4];
-    const int xo = b < B ? xbase + g * 256 : kOutOfRange;
+  for (int g0 = wave; g0 < G; g0 += KS * UG) {
+    uint4 xv[UG][4];
+    uint4 w[UG];
+    float sc[UG][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xv[j] = buffer_load16<0>(rx, xo + 16 * j);
-    const uint4 w = buffer_load16<kLoadNonTemporal>(rw, wbase + g * 64);
-    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-    f4_t c = {0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < UG; ++u) {
+      const int g = g0 + u * KS;
+      const int xo = (b < B && g < G) ? xbase + g * 256 : kOutOfRange;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      c = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_word_h8(words[j]), pair_x8(xv[j]), c, 0,
-                                                 0, 0);
-    const uint2 s4 = *reinterpret_cast<const uint2*>(sT + g * 16 + 4 * kq);
-    acc[0] = __builtin_fmaf(c[0], h2f((uint16_t)(s4.x & 0xFFFFu)), acc[0]);
-    acc[1] = __builtin_fmaf(c[1], h2f((uint16_t)(s4.x >> 16)), acc[1]);
-    acc[2] = __builtin_fmaf(c[2], h2f((uint16_t)(s4.y & 0xFFFFu)), acc[2]);
-    acc[3] = __builtin_fmaf(c[3], h2f((uint16_t)(s4.y >> 16)), acc[3]);
+      for (int j = 0; j < 4; ++j) xv[u][j] = buffer_load16<0>(rx, xo + 16 * j);
+    }
+    if (!kStaged) {
+#pragma unroll
+      for (int u = 0; u < UG; ++u) {
+        const int g = g0 + u * KS;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int off = g < G ? ((4 * kq + v) * G + g) * 2 : kOutOfRange;
+          sc[u][v] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0));
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UG; ++u) {
+      const int g = g0 + u * KS;
+      w[u] = buffer_load16<kLoadNonTemporal>(rw, g < G ? wbase + g * 64 : kOutOfRange);
+    }
+    if (kStaged) {
+      const uint2 s4 = *reinterpret_cast<const uint2*>(sT + g0 * 16 + 4 * kq);
+      sc[0][0] = h2f((uint16_t)(s4.x & 0xFFFFu));
+      sc[0][1] = h2f((uint16_t)(s4.x >> 16));
+      sc[0][2] = h2f((uint16_t)(s4.y & 0xFFFFu));
+      sc[0][3] = h2f((uint16_t)(s4.y >> 16));
+    }
+#pragma unroll
+    for (int u = 0; u < UG; ++u) {
+      const uint32_t words[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+      f4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_word_h8(words[j]), pair_x8(xv[u][j]), c,
+                                                   0, 0, 0);
+      // A group past G loaded zeros (weights, and scales on the direct path),
+      // so it adds nothing.
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(c[v], sc[u][v], acc[v]);
+    }
   }
 
   // Cross-wave reduction of the 16x16 tile, in wave order.
@@ -516,9 +558,9 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ 
   __syncthreads();
   if (wave == 0) {
     f4_t t = {0.f, 0.f, 0.f, 0.f};
-    for (int w = 0; w < KS; ++w)
+    for (int w2 = 0; w2 < KS; ++w2)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) t[v] += red[(w * 64 + lane) * 4 + v];
+      for (int v = 0; v < 4; ++v) t[v] += red[(w2 * 64 + lane) * 4 + v];
     if (b < B) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
