@@ -5,7 +5,9 @@
 Runs, each after a 1 GiB read-only flush so every launch starts cold:
   * `--copies` launches of the d2d copy over a 64 MiB buffer: known traffic
     (64 MiB read + 64 MiB written) that calibrates FETCH_SIZE / WRITE_SIZE;
-  * `--reps` launches of one GEMV variant at one benchmark configuration.
+  * `--reps` launches of one GEMV variant at one benchmark configuration, or
+    of another operation on the path (the MLP step, the paired-layout GEMV,
+    the device quantizer: `--config mlp7b|mlp70b|paired_c0|paired_c4b|quant_c4a`).
 Replaces the reference's ncu launcher (bench/ncu_launch.py:13-34).
 """
 
@@ -27,9 +29,60 @@ VARIANTS = {"v5": dict(version=5), "v2": dict(version=2), "v4": dict(version=4, 
 COPY_BYTES = 64 << 20
 
 
+def _mlp(i: int, h: int):
+    def run(reps, flush):
+        import torch
+
+        from decode_kernel import mlp_decode, quantize_and_pack
+
+        gen = torch.Generator(device="cuda").manual_seed(i)
+        ws = []
+        for shape in ((i, h), (i, h), (h, i)):
+            ws += list(quantize_and_pack(torch.randn(*shape, device="cuda", generator=gen) * 0.02))
+        x = torch.randn(1, h, device="cuda", generator=gen).half()
+        for _ in range(reps):
+            flush()
+            mlp_decode(x, *ws)
+    return run
+
+
+def _paired(m: int, k: int):
+    def run(reps, flush):
+        import torch
+
+        from decode_kernel import gemv_paired, quantize_and_pack, repack_paired
+
+        gen = torch.Generator(device="cuda").manual_seed(m)
+        p, s = quantize_and_pack(torch.randn(m, k, device="cuda", generator=gen) * 0.02)
+        p = repack_paired(p)
+        x = torch.randn(1, k, device="cuda", generator=gen).half()
+        for _ in range(reps):
+            flush()
+            gemv_paired(p, s, x)
+    return run
+
+
+def _quant(reps, flush):
+    import torch
+
+    from decode_kernel import _cuda
+
+    w = torch.randn(28672, 8192, device="cuda") * 0.02
+    for _ in range(reps):
+        flush()
+        _cuda.quantize_and_pack(w)
+
+
+# Other operations on the path, by name: the MLP step at the Llama-7B and
+# 70B shapes, the paired-layout GEMV at c0 and c4b, the device quantizer.
+OTHER_OPS = {"mlp7b": _mlp(11008, 4096), "mlp70b": _mlp(28672, 8192),
+             "paired_c0": _paired(4096, 4096), "paired_c4b": _paired(8192, 28672),
+             "quant_c4a": _quant}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("--config", default="c0", choices=sorted(SHAPES))
+    ap.add_argument("--config", default="c0", choices=sorted(SHAPES) + sorted(OTHER_OPS))
     ap.add_argument("--variant", default="v5", choices=sorted(VARIANTS))
     ap.add_argument("--reps", type=int, default=50)
     ap.add_argument("--copies", type=int, default=5)
@@ -48,6 +101,12 @@ def main() -> None:
     for _ in range(args.copies):
         flush()
         _cuda.d2d_copy(src, dst)
+    if args.config in OTHER_OPS:
+        OTHER_OPS[args.config](args.reps, flush)
+        torch.cuda.synchronize()
+        print(json.dumps({"config": args.config, "reps": args.reps, "copy_bytes": COPY_BYTES}),
+              flush=True)
+        return
     m, k, b = SHAPES[args.config]
     w, x = make_case(m, k, b, seed=1000)
     packed, scales = quantize_and_pack(torch.from_numpy(w))
