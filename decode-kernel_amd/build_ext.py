@@ -41,6 +41,11 @@ HIP_FLAGS = [
     "-fPIC",
     # Packed FP32 instructions are disabled for every kernel on this target.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Kernel arguments preloaded into SGPRs at wave launch (gfx950 supports
+    # it; the compiler adds a prologue that loads them on firmware without
+    # it). A v5 wave then issues its first HBM load without waiting on a
+    # scalar load of its arguments: 2.5% at M = K = 4096.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-command-line-argument",
 ]

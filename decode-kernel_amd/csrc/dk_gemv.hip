@@ -106,7 +106,7 @@ struct Launch {
 // the extra activation registers; tiles of four batch rows were slower.
 // Two waves per workgroup: measured 2-4% faster than four with the XCD
 // renumbering (finer-grained blocks of rows per XCD).
-constexpr int kV5WavesPerBlock = 2;
+constexpr int kV5WavesPerBlock = dk::kStreamWaves;
 
 template <int R, int U, int NB, typename Layout>
 int launch_v5_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,

@@ -198,6 +198,10 @@ __global__ __launch_bounds__(256) void gemv_v23(const uint4* __restrict__ packed
 // Reference: csrc/gemv_w4a16.cu:318-357.
 // ---------------------------------------------------------------------------
 constexpr int kOutOfRange = (int)0x80000000;  // beyond any descriptor's num_records
+// Waves per workgroup of the streaming kernels (v5 and the fused gate/up):
+// a compile-time constant, so no wave reads the dispatch packet's workgroup
+// size before issuing its first load.
+constexpr int kStreamWaves = 2;
 constexpr int kLoadNonTemporal = 2;            // buffer-load cache policy bit "nt"
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
@@ -302,7 +306,7 @@ __device__ __forceinline__ void v5_compute(const V5Stage<R, U, NB>& st, float (&
 }
 
 template <int R, int U, int NB, typename Layout = LayoutLogical>
-__global__ __launch_bounds__(256) void gemv_v5(const uint4* __restrict__ packed,
+__global__ __launch_bounds__(kStreamWaves * 64) void gemv_v5(const uint4* __restrict__ packed,
                                                const uint16_t* __restrict__ scales,
                                                const uint4* __restrict__ x4,
                                                uint16_t* __restrict__ y, int M, int K, int B) {
@@ -310,7 +314,7 @@ __global__ __launch_bounds__(256) void gemv_v5(const uint4* __restrict__ packed,
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wg = xcd_contiguous_block(blockIdx.x, gridDim.x);
-  const int row0 = (wg * (blockDim.x >> 6) + wave) * R;
+  const int row0 = (wg * kStreamWaves + wave) * R;
   if (row0 >= M) return;  // wave-uniform; no barriers in this kernel
   const int b0 = blockIdx.y * NB;
   const int nck = K >> 5;

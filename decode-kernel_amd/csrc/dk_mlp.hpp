@@ -29,7 +29,7 @@ constexpr int kStampGateUp = 20;
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + expf(-v)); }
 
 template <int R, int U, int NB>
-__global__ __launch_bounds__(256) void gate_up_silu(const uint4* __restrict__ gate,
+__global__ __launch_bounds__(kStreamWaves * 64) void gate_up_silu(const uint4* __restrict__ gate,
                                                     const uint16_t* __restrict__ gate_scales,
                                                     const uint4* __restrict__ up,
                                                     const uint16_t* __restrict__ up_scales,
@@ -39,7 +39,7 @@ __global__ __launch_bounds__(256) void gate_up_silu(const uint4* __restrict__ ga
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wg = xcd_contiguous_block(blockIdx.x, gridDim.x);
-  const int row0 = (wg * (blockDim.x >> 6) + wave) * R;
+  const int row0 = (wg * kStreamWaves + wave) * R;
   if (row0 >= I) return;  // wave-uniform; no barriers in this kernel
   const int b0 = blockIdx.y * NB;
   const int nck = H >> 5;
