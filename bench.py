@@ -443,7 +443,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": MI355X_HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": achieved / MI355X_HBM_PEAK_GBPS, "traffic": traffic,
-            "kernel": "dk::gemv_v5<2, 2, 1>", "mean_us": headline["mean_us"],
+            "kernel": "dk::gemv_v5<2, 2, 1, dk::LayoutLogical>", "mean_us": headline["mean_us"],
             "algorithmic_bytes": headline["bytes_moved"],
         },
         "cpu_baseline": cpu,
