@@ -66,7 +66,6 @@ int fail(int code, const char* fmt, ...) {
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 constexpr int kWavesPerBlock = 4;
-constexpr int kV4RowsPerTile = 4;
 
 int clamp_wpr(int wpr) { return std::max(2, std::min(wpr, 8)); }
 
@@ -144,7 +143,7 @@ int launch_gate_up_t(const Launch& L, const uint4* g, const uint16_t* gs, const 
   const int rows_per_block = kV5WavesPerBlock * R;
   dim3 grid((I + rows_per_block - 1) / rows_per_block, (B + NB - 1) / NB);
   return L("gate/up launch", dk::gate_up_silu<R, U, NB>, grid, dim3(kV5WavesPerBlock * 64), 0, g,
-           gs, u, us, x, h, I, H, B);
+           gs, u, us, x, I, H, B, h);
 }
 
 int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const uint4* u,
@@ -194,6 +193,13 @@ int effective_split(int K, int split_k) {
   const int G = K / DK_GROUP_SIZE;
   return std::max(1, std::min(split_k, G));
 }
+
+// v4 workspace: fp32 partials [S, B, M], then one uint32 ticket per tile.
+size_t v4_partials(int M, int K, int B, const dk_gemv_config* cfg) {
+  return (size_t)effective_split(K, cfg->split_k) * (size_t)B * (size_t)M;
+}
+
+size_t v4_tickets(int M) { return ((size_t)M + dk::kV4TileRows - 1) / dk::kV4TileRows; }
 
 int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x, uint16_t* y, int M,
               int K, int B, const dk_gemv_config* cfg, void* workspace, size_t workspace_bytes,
@@ -256,9 +262,11 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
                M, K, B);
     case DK_V4: {
       const int S = effective_split(K, cfg->split_k);
-      dim3 grid((M + kV4RowsPerTile - 1) / kV4RowsPerTile, S);
-      return L("v4 launch", dk::gemv_v4, grid, dim3(kV4RowsPerTile * 64), 0, p4, scales, x4, y,
-               static_cast<float*>(workspace), M, K, B);
+      dim3 grid((M + dk::kV4TileRows - 1) / dk::kV4TileRows, S);
+      float* partials = static_cast<float*>(workspace);
+      auto* tickets = reinterpret_cast<unsigned int*>(partials + v4_partials(M, K, B, cfg));
+      return L("v4 launch", dk::gemv_v4, grid, dim3(dk::kV4TileRows * 64), 0, p4, scales, x4, y,
+               partials, tickets, M, K, B);
     }
     case DK_V5:
       return launch_v5(L, p4, scales, x4, y, M, K, B);
@@ -302,11 +310,6 @@ int dk_gemv_validate(int M, int K, int B, const dk_gemv_config* cfg) {
     if (v3_lds_bytes(K) > (size_t)lds_limit_bytes())
       return fail(DK_ERR_UNSUPPORTED, "K=%d needs %zu B of LDS on v3 (limit %d)", K, v3_lds_bytes(K),
                   lds_limit_bytes());
-  } else if (cfg->version == DK_V4) {
-    const long tiles = ((long)M + kV4RowsPerTile - 1) / kV4RowsPerTile;
-    if (tiles > dk::kMaxTickets)
-      return fail(DK_ERR_UNSUPPORTED, "M=%d exceeds the split-K ticket table (%d rows)", M,
-                  dk::kMaxTickets * kV4RowsPerTile);
   }
   return DK_OK;
 }
@@ -315,7 +318,7 @@ size_t dk_gemv_workspace_bytes(int M, int K, int B, const dk_gemv_config* cfg) {
   if (dk_gemv_validate(M, K, B, cfg) != DK_OK) return 0;
   if (M <= 0 || K <= 0 || B <= 0) return 0;
   if (cfg->reuse_weights || cfg->version != DK_V4) return 0;
-  return (size_t)effective_split(K, cfg->split_k) * (size_t)B * (size_t)M * sizeof(float);
+  return v4_partials(M, K, B, cfg) * sizeof(float) + v4_tickets(M) * sizeof(unsigned int);
 }
 
 int dk_w4a16_gemv(const uint32_t* packed, const uint16_t* scales, const uint16_t* x, uint16_t* y,

@@ -28,11 +28,6 @@ __device__ __forceinline__ void write_stamp(int s) {
   if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) g_stamp = s;
 }
 
-// Split-K completion tickets, one per row tile. Zero at load; the last
-// workgroup of a tile resets its ticket, so they are zero between launches.
-constexpr int kMaxTickets = 1 << 16;
-__device__ unsigned int g_tickets[kMaxTickets];
-
 // ---------------------------------------------------------------------------
 // v0: one thread per row, scalar decode (the uncoalesced baseline stage).
 // Reference: csrc/gemv_w4a16.cu:70-94.
@@ -313,7 +308,9 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemv_v5(const uint4* __rest
   write_stamp(Layout::kStamp);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wg = xcd_contiguous_block(blockIdx.x, gridDim.x);
+  // The grid size follows from M (it is the launch's), so no hidden argument
+  // is read before the first load.
+  const int wg = xcd_contiguous_block(blockIdx.x, (M + kStreamWaves * R - 1) / (kStreamWaves * R));
   const int row0 = (wg * kStreamWaves + wave) * R;
   if (row0 >= M) return;  // wave-uniform; no barriers in this kernel
   const int b0 = blockIdx.y * NB;
@@ -357,8 +354,14 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemv_v5(const uint4* __rest
 // v4: split-K. grid = (row tiles of 4, S). Workgroup (tile, s) computes the
 // fp32 partial of its 4 rows over group slice s and stores it to
 // ws[s][b][row]; the last workgroup of a tile to finish adds the S partials
-// in slice order and writes fp16 y. One launch, no memset, deterministic.
+// in slice order and writes fp16 y. One launch, deterministic.
 // Reference: csrc/gemv_w4a16.cu:264-313, 415-419 (memset + atomics + convert).
+//
+// The completion tickets (one uint32 per tile) live in the caller's
+// workspace after the partials, so launches on different streams with their
+// own workspaces never share them. They must be zero when a launch starts;
+// the last workgroup of each tile resets its ticket, so a workspace that was
+// zeroed once stays valid for every later launch that uses it in turn.
 //
 // Cross-workgroup visibility on an 8-XCD part (one L2 per XCD, not coherent
 // with each other) uses agent-scope atomic stores and loads for the partials
@@ -366,16 +369,19 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemv_v5(const uint4* __rest
 // the ticket, instead of agent-scope fences: a fence writes back and
 // invalidates a whole L2 per wave and made this kernel ~35x slower.
 // ---------------------------------------------------------------------------
+constexpr int kV4TileRows = 4;  // rows per workgroup and ticket tile: one wave per row
+
 __global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
                                                const uint16_t* __restrict__ scales,
                                                const uint4* __restrict__ x4,
                                                uint16_t* __restrict__ y, float* __restrict__ ws,
-                                               int M, int K, int B) {
+                                               unsigned int* __restrict__ tickets, int M, int K,
+                                               int B) {
   write_stamp(4);
   __shared__ int last;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int rows_per_tile = blockDim.x >> 6;
+  const int rows_per_tile = kV4TileRows;
   const int tile = blockIdx.x;
   const int row_raw = tile * rows_per_tile + wave;
   const int row = row_raw < M ? row_raw : M - 1;
@@ -417,7 +423,7 @@ __global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
   __syncthreads();
   if (threadIdx.x == 0) {
     const unsigned prev =
-        __hip_atomic_fetch_add(&g_tickets[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(&tickets[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last = (prev == (unsigned)(S - 1));
   }
   __syncthreads();
@@ -435,7 +441,7 @@ __global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
     y[(size_t)b * M + r] = f2h(sum);
   }
   if (threadIdx.x == 0)
-    __hip_atomic_store(&g_tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------

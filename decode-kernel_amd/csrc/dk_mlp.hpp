@@ -33,12 +33,16 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gate_up_silu(const uint4* _
                                                     const uint16_t* __restrict__ gate_scales,
                                                     const uint4* __restrict__ up,
                                                     const uint16_t* __restrict__ up_scales,
-                                                    const uint4* __restrict__ x4,
-                                                    uint16_t* __restrict__ h, int I, int H, int B) {
+                                                    const uint4* __restrict__ x4, int I, int H,
+                                                    int B, uint16_t* __restrict__ h) {
+  // h is the last argument: with 15 argument dwords not all fit the preload
+  // registers, and h is only needed after the sums.
   write_stamp(kStampGateUp);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wg = xcd_contiguous_block(blockIdx.x, gridDim.x);
+  // The grid size follows from I (it is the launch's), so no hidden argument
+  // is read before the first load.
+  const int wg = xcd_contiguous_block(blockIdx.x, (I + kStreamWaves * R - 1) / (kStreamWaves * R));
   const int row0 = (wg * kStreamWaves + wave) * R;
   if (row0 >= I) return;  // wave-uniform; no barriers in this kernel
   const int b0 = blockIdx.y * NB;

@@ -66,9 +66,14 @@ typedef enum dk_status {
 void dk_gemv_config_default(dk_gemv_config* cfg);
 
 /* Bytes of device workspace dk_w4a16_gemv needs for this call (0 for every
- * variant except split-K v4, which keeps fp32 partials [split_k, B, M]). No
- * counterpart in the reference, whose v4 took an fp32 [B, M] buffer
- * (include/decode_kernel/gemv_w4a16.h:33). Returns 0 for invalid arguments. */
+ * variant except split-K v4: fp32 partials [split_k', B, M], split_k' =
+ * min(split_k, K/128), followed by one uint32 completion ticket per 4-row
+ * tile, ceil(M/4)). The ticket area must be zero when a v4 call starts;
+ * every v4 call leaves it zero again, so a workspace zeroed once can be
+ * reused by later calls that run one after another (each stream its own
+ * workspace). No counterpart in the reference, whose v4 took an fp32 [B, M]
+ * buffer zeroed per call (include/decode_kernel/gemv_w4a16.h:33,
+ * csrc/bindings.cpp:65-68). Returns 0 for invalid arguments. */
 size_t dk_gemv_workspace_bytes(int M, int K, int B, const dk_gemv_config* cfg);
 
 /* Host-side argument check of dk_w4a16_gemv without launching anything

@@ -101,9 +101,11 @@ def test_null_and_misaligned_pointers_rejected(lib):
 
 def test_split_k_workspace_contract(lib):
     cfg = _abi.default_config(lib, version=4, split_k=4)
-    # [split_k, B, M] fp32 partials; split is capped at the group count.
-    assert lib.dk_gemv_workspace_bytes(4096, 4096, 2, ctypes.byref(cfg)) == 4 * 2 * 4096 * 4
-    assert lib.dk_gemv_workspace_bytes(64, 256, 1, ctypes.byref(cfg)) == 2 * 1 * 64 * 4
+    # [split_k, B, M] fp32 partials (split capped at the group count), then
+    # one uint32 ticket per 4-row tile.
+    assert lib.dk_gemv_workspace_bytes(4096, 4096, 2, ctypes.byref(cfg)) == 4 * 2 * 4096 * 4 + 1024 * 4
+    assert lib.dk_gemv_workspace_bytes(64, 256, 1, ctypes.byref(cfg)) == 2 * 1 * 64 * 4 + 16 * 4
+    assert lib.dk_gemv_workspace_bytes(65, 256, 1, ctypes.byref(cfg)) == 2 * 1 * 65 * 4 + 17 * 4
     for v in (0, 1, 2, 3, 5):
         c = _abi.default_config(lib, version=v)
         assert lib.dk_gemv_workspace_bytes(4096, 4096, 1, ctypes.byref(c)) == 0

@@ -205,7 +205,7 @@ def test_c_abi_direct_matches_extension():
     for label, kw in PATHS:
         cfg = _abi.default_config(lib, **{kk: int(v) for kk, v in kw.items()})
         ws_bytes = lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(cfg))
-        ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device="cuda")
+        ws = torch.zeros(max(ws_bytes // 4, 1), dtype=torch.float32, device="cuda")
         y = torch.empty(b, m, dtype=torch.float16, device="cuda")
         rc = lib.dk_w4a16_gemv(pd.data_ptr(), sd.data_ptr(), xd.data_ptr(), y.data_ptr(), m, k, b,
                                ctypes.byref(cfg), ws.data_ptr() if ws_bytes else None, ws_bytes,
@@ -236,3 +236,63 @@ def test_stream_probes():
     _cuda.empty_kernel()
     torch.cuda.synchronize()
 
+
+
+def test_v4_concurrent_streams_do_not_share_tickets():
+    # Two split-K GEMVs with the same tile count run at the same time on two
+    # streams: each uses its own workspace tickets, so both must be exact.
+    from decode_kernel import gemv
+
+    cases = []
+    for seed in (1, 2):
+        w, x = oracle.make_case(4096, 4096, 1, seed=300 + seed)
+        p, s = oracle.quantize_and_pack(w)
+        cases.append((torch.from_numpy(p).cuda(), torch.from_numpy(s).cuda(),
+                      torch.from_numpy(x).cuda(), oracle.linear_f64(x, p, s)))
+    refs = [gemv(p, s, x, version=4, split_k=8) for p, s, x, _ in cases]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    outs = [[], []]
+    for _ in range(20):
+        for i, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                p, s, x, _ = cases[i]
+                outs[i].append(gemv(p, s, x, version=4, split_k=8))
+    torch.cuda.synchronize()
+    for i in range(2):
+        _check_against_oracle(outs[i][-1], cases[i][3], f"v4 stream {i}")
+        assert all(torch.equal(o, refs[i]) for o in outs[i]), f"stream {i} differs from serial"
+
+
+def test_graph_replays_match_eager():
+    # Every product path, the MLP step and the device quantizer captured in
+    # one HIP graph; three replays with eager work between them, each checked
+    # bit for bit against the eager results.
+    from decode_kernel import _cuda, gemv, mlp_decode, quantize_and_pack
+
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    w = torch.randn(1024, 2048, device="cuda", generator=gen) * 0.02
+    p, s = quantize_and_pack(w)
+    up, us = quantize_and_pack(torch.randn(1024, 2048, device="cuda", generator=gen) * 0.02)
+    dp, ds = quantize_and_pack(torch.randn(2048, 1024, device="cuda", generator=gen) * 0.02)
+    x = torch.randn(3, 2048, device="cuda", generator=gen).half()
+
+    def work():
+        outs = [gemv(p, s, x, **kw) for _, kw in PATHS]
+        outs.append(mlp_decode(x, p, s, up, us, dp, ds))
+        outs.extend(_cuda.quantize_and_pack(w))
+        return outs
+
+    eager = work()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = work()
+    for rep in range(3):
+        torch.cuda.synchronize()
+        # Eager work between replays, on the same memory the graph reads.
+        gemv(p, s, x, version=4, split_k=4)
+        graph.replay()
+        torch.cuda.synchronize()
+        for k, (a, b) in enumerate(zip(captured, eager)):
+            assert torch.equal(a, b), f"replay {rep}: output {k} differs from eager"
