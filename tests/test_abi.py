@@ -202,3 +202,52 @@ def test_extension_rejects_cpu_tensors():
     x = torch.zeros(1, 128, dtype=torch.float16)
     with pytest.raises(RuntimeError, match="must be CUDA tensors"):
         gemv(packed, scales, x)
+
+
+CPP_PROGRAM = r"""
+#include "decode_kernel/gemv_w4a16.hpp"
+#include <cstdio>
+int main() {
+  using namespace decode_kernel;
+  GemvLaunchConfig cfg;  // the reference's defaults (gemv_w4a16.h:22-27)
+  if (cfg.version != KernelVersion::V5 || cfg.split_k != 4 || cfg.reuse_weights ||
+      cfg.warps_per_row != 1 || kGroupSize != 128 || kNibblesPerWord != 8 || kWeightsPerInt4 != 32)
+    return 2;
+  w4a16_gemv(nullptr, nullptr, nullptr, nullptr, 0, 128, 1, cfg, nullptr, nullptr);  // no-op
+  try {
+    w4a16_gemv(reinterpret_cast<const uint32_t*>(0x10000), reinterpret_cast<const __half*>(0x10000),
+               reinterpret_cast<const __half*>(0x10000), reinterpret_cast<__half*>(0x10000), 4, 200,
+               1, cfg, nullptr, nullptr);
+    return 3;
+  } catch (const std::runtime_error& e) {
+    std::printf("threw: %s\n", e.what());
+  }
+  GemvLaunchConfig v4;
+  v4.version = KernelVersion::V4;
+  std::printf("ws %zu %zu\n", workspace_bytes(4096, 4096, 2, v4), workspace_bytes(4096, 4096, 2, cfg));
+  return 0;
+}
+"""
+
+
+def test_cpp_namespace_wrapper_compiles_and_validates(tmp_path):
+    # include/decode_kernel/gemv_w4a16.hpp mirrors the reference's C++ API
+    # (include/decode_kernel/gemv_w4a16.h) over the C ABI; a plain g++ build
+    # against it must work, and argument errors must surface as exceptions.
+    import shutil
+    import subprocess
+
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+    src = tmp_path / "t.cpp"
+    src.write_text(CPP_PROGRAM)
+    exe = tmp_path / "t"
+    libdir = _abi.LIB_PATH.parent
+    subprocess.run(["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", f"-I{REPO / 'include'}",
+                    "-I/opt/rocm/include", str(src), f"-L{libdir}", "-ldk_hip",
+                    f"-Wl,-rpath,{libdir}", "-L/opt/rocm/lib", "-lamdhip64", "-o", str(exe)],
+                   check=True, capture_output=True, text=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, (out.returncode, out.stdout, out.stderr)
+    assert "threw: w4a16_gemv: K must be divisible by group size 128" in out.stdout
+    assert f"ws {4 * 2 * 4096 * 4 + 1024 * 4} 0" in out.stdout
