@@ -83,6 +83,8 @@ def parse_args():
     ap.add_argument("--no-quantizer", action="store_true",
                     help="skip the device quantizer measurement")
     ap.add_argument("--no-mlp", action="store_true", help="skip the MLP decode step measurement")
+    ap.add_argument("--no-fp16-baseline", action="store_true",
+                    help="skip the cross-precision torch fp16 F.linear rows")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="budget of the CPU baseline sample")
     ap.add_argument("--out", type=Path, default=None, help="also write the full JSON here")
@@ -148,6 +150,28 @@ def bench_variant(ext, copies, x, variant, steps, y_ref=None, call_level_flush=N
                       flush=call_level_flush)
         row["call_events"] = {k2: ev[k2] for k2 in ("median_us", "iqr_us", "mean_us", "iters")}
     return row
+
+
+def bench_torch_fp16(pd, sd, x, steps):
+    """Cross-precision baseline (labelled as such, as the reference's bench
+    does, bench/bench.py:1-9): torch F.linear on the dequantized weights in
+    fp16 (hipBLASLt/rocBLAS), back-to-back over weight copies totalling
+    > 640 MB. It moves 4x the weight bytes of the W4A16 kernel."""
+    import torch
+
+    from decode_kernel import dequantize
+    from dk_bench.common import bytes_moved_fp16, time_graph_steps
+
+    w16 = dequantize(pd, sd, dtype=torch.float16)
+    n = max(2, (640 << 20) // (w16.numel() * 2) + 1)
+    ws = [w16] + [w16.clone() for _ in range(n - 1)]
+    st, graph = time_graph_steps(lambda i: torch.nn.functional.linear(x, ws[i % n]), steps=steps)
+    del graph, ws, w16
+    m, k, b = pd.shape[0], pd.shape[1] * 8, x.shape[0]
+    moved = bytes_moved_fp16(m, k, b)
+    return {"impl": "torch_fp16_linear", "precision": "fp16 weights (cross-precision)",
+            "bytes_moved": moved, "gbps": moved / (st["median_us"] * 1e3), "weight_copies": n,
+            **st}
 
 
 def torch_equal(a, b) -> bool:
@@ -380,6 +404,13 @@ def main():
                 entry["kernels"].append(r)
                 log(f"   {v:8s} {r['median_us']:8.2f} us/step  {r['gbps']:8.1f} GB/s  "
                     f"{r['pct_of_read_roof']:5.1f}% of read roof")
+            if b == 1 and not args.no_fp16_baseline:
+                r16 = bench_torch_fp16(copies[0][0], copies[1][0], xd, args.other_steps)
+                v5row = next(r for r in entry["kernels"] if r["impl"] == "v5")
+                entry["torch_fp16"] = {"p50_us": r16["median_us"], "gbps": r16["gbps"],
+                                       "w4a16_v5_speedup": r16["median_us"] / v5row["median_us"]}
+                log(f"   torch fp16 F.linear {r16['median_us']:8.2f} us/step (cross-precision; "
+                    f"v5 is {entry['torch_fp16']['w4a16_v5_speedup']:.2f}x faster)")
             results[f"{name}_B{b}"] = entry
             if name == "c0":
                 headline = next(r for r in entry["kernels"] if r["impl"] == "v5")
@@ -453,6 +484,7 @@ def main():
             key: {"M": r["M"], "K": r["K"], "batch": r["batch"],
                   "same_size_read_gbps": (round(r["same_size_read"]["gbps"], 1)
                                           if "same_size_read" in r else None),
+                  "torch_fp16_linear": r.get("torch_fp16"),
                   "kernels": {row["impl"]: {"p50_us": round(row["median_us"], 3),
                                             "iqr_us": round(row["iqr_us"], 3),
                                             "gbps": round(row["gbps"], 1),

@@ -43,6 +43,11 @@ def bytes_moved_fp16(m: int, k: int, batch: int) -> int:
     return m * k * 2 + batch * k * 2 + batch * m * 2
 
 
+def arithmetic_intensity_w4(m: int, k: int, batch: int) -> float:
+    """FLOP per algorithmic byte (bench/common.py:128-129)."""
+    return flop_gemv(m, k, batch) / bytes_moved_w4(m, k, batch)
+
+
 def flop_gemv(m: int, k: int, batch: int) -> int:
     return 2 * m * k * batch
 
