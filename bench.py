@@ -198,6 +198,18 @@ def cpu_baseline(packed, scales, x, budget_s):
         times.append((time.perf_counter_ns() - t0) / 1e3)
     times.sort()
     med = times[len(times) // 2]
+    # The GEMM alone with W already dequantized (fp32), labelled separately:
+    # what the CPU path costs once dequantization is paid for.
+    w32 = oracle.dequantize(p, s, dtype=np.float32)
+    x32 = np.asarray(xv, dtype=np.float32).reshape(-1, w32.shape[1])
+    mm = []
+    t_end = time.perf_counter() + min(5.0, budget_s / 3)
+    while time.perf_counter() < t_end and len(mm) < 500:
+        t0 = time.perf_counter_ns()
+        _ = x32 @ w32.T
+        mm.append((time.perf_counter_ns() - t0) / 1e3)
+    mm.sort()
+    del w32
     try:
         from threadpoolctl import threadpool_info
 
@@ -221,6 +233,8 @@ def cpu_baseline(packed, scales, x, budget_s):
                    f"{blas_threads} threads), median of ~{budget_s:.0f} s"),
         "p50_us": med, "iqr_us": times[(3 * len(times)) // 4] - times[len(times) // 4],
         "calls": len(times), "host_cpus": len(os.sched_getaffinity(0)), "cpu_model": cpu_model,
+        "matmul_only": {"p50_us": mm[len(mm) // 2], "calls": len(mm),
+                        "note": "fp32 x @ W^T with W pre-dequantized (not the reference path)"},
     }
 
 
