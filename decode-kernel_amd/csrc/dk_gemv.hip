@@ -84,18 +84,19 @@ struct Launch {
 };
 
 // v5 stage shapes (R rows per wave, U 16-byte chunks per lane per stage),
-// from a sweep on MI355X of back-to-back
-// launches over cold weights, B = 1 (us per launch; R rows, U chunks):
-//   M = 4096,  K = 4096:  R2 U2 3.92 (double-buffered 4.03; R4 U1 4.61)
-//   M = 11008, K = 4096:  R2 U2 6.73 (R4 U1 7.39)
-//   M = 4096,  K = 11008: R2 U2 7.22 (R4 U1 9.77)
-//   M = 28672, K = 8192:  R4 U1 24.66 (R2 U2 27.14)
-//   M = 8192,  K = 28672: R4 U1 23.36 (double-buffered 24.22; R2 U2 28.55)
-//   M = 8192,  K = 3584:  R4 U1 5.35, R2 U2 5.35; M = 3584, K = 8192: R2 U2 5.56
-// Double-buffered stages (the next stage's loads issued before this stage's
-// math) measured slower everywhere once the decode is 13 ops per word: the
-// other waves on the SIMD hide the load latency instead.
-// B > 1, M = K = 4096 (us per launch; NB activation rows per tile):
+// timed on MI355X as the bench times them: a HIP graph of 1000 back-to-back
+// steps over torch-allocated weight copies (> 640 MB, cold), B = 1, us:
+//   M = K = 4096:        R2 U2 3.68; double-buffered 3.76; R2 U1 3.80;
+//                        R1 U2 4.18; R4 U1 4.38; R2 U3 4.38; 1 / 4 / 8 waves
+//                        per workgroup 3.82 / 3.73 / 3.89; no XCD renumbering 3.76
+//   M = 11008, K = 4096: R2 U2 6.33 (1 wave per workgroup 6.20); R4 U1 6.83
+//   M = 4096, K = 11008: R2 U2 6.82; R2 U3 7.57; double-buffered 8.25; R4 U1 9.34
+//   M = 8192, K = 3584:  R2 U2 5.21; R3 U2 5.50; R2 U3 6.22
+// and, from an earlier per-launch sweep, R4 U1 for the 70B shapes
+// (M = 28672, K = 8192: 24.66 vs R2 U2 27.14; M = 8192, K = 28672: 23.36 vs
+// 28.55). Splitting K across the waves of a workgroup was slower in every
+// case above (3.79 at M = K = 4096, 7.48 at M = 4096, K = 11008).
+// B > 1, M = K = 4096 (earlier per-launch sweep):
 //   B = 2:  R2 U1 NB2 4.81 (R4 U1 NB2 5.47; R2 U1 NB4 6.17)
 //   B = 4:  R4 U1 NB2 6.05 (R2 U1 NB4 6.81); B = 8: R4 U1 NB2 9.68 (11.71)
 //   B = 16: R4 U1 NB2 16.82 (21.73); M = 8192, K = 28672, B = 4: 56.0 (69.0)
@@ -103,8 +104,8 @@ struct Launch {
 // stage keep two weight loads in flight per row; more than that measured
 // slower on this memory system. With a batch, more rows per wave pay for
 // the extra activation registers; tiles of four batch rows were slower.
-// Two waves per workgroup: measured 2-4% faster than four with the XCD
-// renumbering (finer-grained blocks of rows per XCD).
+// Two waves per workgroup with the XCD renumbering (finer-grained blocks of
+// rows per XCD).
 constexpr int kV5WavesPerBlock = dk::kStreamWaves;
 
 template <int R, int U, int NB, typename Layout>

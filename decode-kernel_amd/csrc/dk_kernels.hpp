@@ -1,7 +1,6 @@
 // Every W4A16 GEMV kernel for gfx950, as templates and __global__ functions.
 // Included by exactly one translation unit of the library (dk_gemv.hip),
-// which owns the __device__ globals defined here (dispatch stamp and split-K
-// tickets).
+// which owns the one __device__ global defined here (the dispatch stamp).
 //
 // Layout in HBM (the reference format, no repacking):
 //   packed uint32 [M, K/8]: row m is K/2 bytes; 16-byte chunk c of a row holds
@@ -187,7 +186,8 @@ __global__ __launch_bounds__(256) void gemv_v23(const uint4* __restrict__ packed
 // the scales, then the weights with the non-temporal hint (read-once data).
 // Activations are paired once per stage and reused for all R rows. Load
 // latency is hidden by the other waves on the SIMD, not by double buffering
-// inside a wave (which measured slower once the decode was 13 ops per word).
+// inside a wave (2% slower at M = K = 4096 and 20% at M = 4096, K = 11008
+// once the decode was 13 ops per word).
 // grid.y covers the batch in tiles of NB rows; workgroup ids are renumbered
 // so each XCD streams one contiguous block of rows (measured 2-5% faster).
 // Reference: csrc/gemv_w4a16.cu:318-357.
@@ -302,9 +302,10 @@ __device__ __forceinline__ void v5_compute(const V5Stage<R, U, NB>& st, float (&
 
 template <int R, int U, int NB, typename Layout = LayoutLogical>
 __global__ __launch_bounds__(kStreamWaves * 64) void gemv_v5(const uint4* __restrict__ packed,
-                                               const uint16_t* __restrict__ scales,
-                                               const uint4* __restrict__ x4,
-                                               uint16_t* __restrict__ y, int M, int K, int B) {
+                                                             const uint16_t* __restrict__ scales,
+                                                             const uint4* __restrict__ x4,
+                                                             uint16_t* __restrict__ y, int M, int K,
+                                                             int B) {
   write_stamp(Layout::kStamp);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -334,9 +335,10 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemv_v5(const uint4* __rest
   for (int c0 = 0; c0 < nck; c0 += kStep) {
     v5_load(st, rw, rs, rx, c0, nck, G, K, b0, B, lane);
     // With the paired layout's shorter math the scheduler interleaves it
-    // between the stage's loads, which cuts the loads in flight per wave;
-    // the barrier keeps them back to back (measured 1-3.5% faster at the
-    // large shapes there, and 1.5-3% slower for the logical layout at c0-c2).
+    // between the stage's loads, which cuts the loads in flight per wave (it
+    // made that layout 23% slower at M = 8192, K = 28672); the barrier keeps
+    // them back to back. For the logical layout it changes nothing beyond
+    // +-2%, so it is a trait of the layout.
     if constexpr (Layout::kLoadsFirst) __builtin_amdgcn_sched_barrier(0);
     v5_compute<R, U, NB, Layout>(st, acc);
   }
