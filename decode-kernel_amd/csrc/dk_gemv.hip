@@ -108,26 +108,26 @@ struct Launch {
 // rows per XCD).
 constexpr int kV5WavesPerBlock = dk::kStreamWaves;
 
-template <int R, int U, int NB, typename Layout>
+template <int R, int U, int NB, typename Layout, int kStamp>
 int launch_v5_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                 int M, int K, int B) {
   const int rows_per_block = kV5WavesPerBlock * R;
   dim3 grid((M + rows_per_block - 1) / rows_per_block, (B + NB - 1) / NB);
-  return L("v5 launch", dk::gemv_v5<R, U, NB, Layout>, grid, dim3(kV5WavesPerBlock * 64), 0, p, s,
-           x, y, M, K, B);
+  return L("v5 launch", dk::gemv_v5<R, U, NB, Layout, kStamp>, grid, dim3(kV5WavesPerBlock * 64), 0,
+           p, s, x, y, M, K, B);
 }
 
-template <typename Layout = dk::LayoutLogical>
+template <typename Layout = dk::LayoutLogical, int kStamp = Layout::kStamp>
 int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y, int M,
               int K, int B) {
   if (B == 1) {
     // Four rows per wave once both dimensions are large: still >= 2048 waves,
     // and half the activation loads and pairing per weight.
-    if (M >= 8192 && K >= 8192) return launch_v5_t<4, 1, 1, Layout>(L, p, s, x, y, M, K, B);
-    return launch_v5_t<2, 2, 1, Layout>(L, p, s, x, y, M, K, B);
+    if (M >= 8192 && K >= 8192) return launch_v5_t<4, 1, 1, Layout, kStamp>(L, p, s, x, y, M, K, B);
+    return launch_v5_t<2, 2, 1, Layout, kStamp>(L, p, s, x, y, M, K, B);
   }
-  if (B == 2) return launch_v5_t<2, 1, 2, Layout>(L, p, s, x, y, M, K, B);
-  return launch_v5_t<4, 1, 2, Layout>(L, p, s, x, y, M, K, B);
+  if (B == 2) return launch_v5_t<2, 1, 2, Layout, kStamp>(L, p, s, x, y, M, K, B);
+  return launch_v5_t<4, 1, 2, Layout, kStamp>(L, p, s, x, y, M, K, B);
 }
 
 // Fused gate/up (R rows of each matrix per wave, U chunks per stage, NB
@@ -159,29 +159,38 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 // Reuse-path shapes (waves per 16-row tile, groups per stage, scales staged
 // in LDS or loaded directly), measured on MI355X back-to-back over cold
 // weights (us per launch):
-//   M = K = 4096:  B = 1: direct KS16 UG2 4.86 (staged KS16 5.20)
-//                  B = 4: direct KS16 UG2 5.48 (staged KS16 5.84)
-//                  B = 16: direct KS8 UG1 7.34 (staged KS8 7.76)
-//   M = 11008, K = 4096, B = 16: direct KS8 17.60, staged KS8 17.47
-//   M = 28672, K = 8192, B = 1: staged KS8 36.0 (direct KS8 38.3)
-//   M = 8192, K = 28672: B = 1 staged KS8 35.7 (direct 42.3); B = 16 staged KS8 72.2
+//   M = K = 4096:  B = 1: streaming 3.68 (direct KS8 UG2 4.78, KS16 UG2 4.84)
+//                  B = 2: streaming 4.57 (direct KS8 UG2 4.87, KS16 UG2 5.02)
+//                  B = 3: direct KS8 UG2 4.99 (KS16 UG2 5.22; streaming 5.41)
+//                  B = 4: direct KS8 UG2 5.19 (KS16 UG2 5.43; streaming 5.75)
+//                  B = 8: direct KS8 UG1 5.71 (KS8 UG2 5.70, KS16 UG2 5.91)
+//                  B = 16: direct KS8 UG1 6.99 (KS8 UG2 7.25, KS16 UG2 7.09)
+//   M = 11008, K = 4096: B = 1: streaming 6.33 (direct KS8 UG1 9.40)
+//                        B = 2: streaming 8.94 (direct KS8 UG1 9.58)
+//                        B = 16: direct KS8 17.07, staged KS8 17.47
+//   M = 28672, K = 8192, B = 1: streaming 22.7 (staged KS8 36.0, direct KS8 38.3)
+//   M = 8192, K = 28672: B = 1: streaming 21.7 (staged KS8 34.0, direct 40.2)
+//                        B = 2: staged KS8 34.9 (streaming 38.3)
+//                        B = 16: staged KS8 70.4 (direct 73.1)
 // Staged scales win once rows are long (the LDS copy is amortised over many
 // groups; direct scale loads add four loads per group); with 512 or more
-// tiles (M >= 8192) 8 waves per tile are enough.
-enum class ReuseShape { kDirect16x2, kDirect8x1, kStaged16, kStaged8 };
+// tiles (M >= 8192) 8 waves per tile with one group per stage are enough.
+enum class ReuseShape { kStream, kDirect8x2, kDirect8x1, kStaged16, kStaged8 };
 
 ReuseShape reuse_shape(int M, int K, int B) {
+  if (B == 1 || (B == 2 && K <= 4096)) return ReuseShape::kStream;
   const int tiles = (M + 15) / 16;
   // Rows too long for the staged copy in LDS take the direct path too.
   const bool fits = dk::reuse_lds_bytes_for(16, K, true) <= (size_t)lds_limit_bytes();
   if (K <= 4096 || !fits)
-    return (B <= 4 && tiles < 512) ? ReuseShape::kDirect16x2 : ReuseShape::kDirect8x1;
+    return (B <= 4 && tiles < 512) ? ReuseShape::kDirect8x2 : ReuseShape::kDirect8x1;
   return (tiles >= 512 || B > 4) ? ReuseShape::kStaged8 : ReuseShape::kStaged16;
 }
 
 size_t reuse_lds_bytes(int M, int K, int B) {
   switch (reuse_shape(M, K, B)) {
-    case ReuseShape::kDirect16x2: return dk::reuse_lds_bytes_for(16, K, false);
+    case ReuseShape::kStream: return 0;
+    case ReuseShape::kDirect8x2:
     case ReuseShape::kDirect8x1: return dk::reuse_lds_bytes_for(8, K, false);
     case ReuseShape::kStaged16: return dk::reuse_lds_bytes_for(16, K, true);
     default: return dk::reuse_lds_bytes_for(8, K, true);
@@ -229,8 +238,10 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
     dim3 grid((M + 15) / 16, (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
     const size_t lds = reuse_lds_bytes(M, K, B);
     switch (reuse_shape(M, K, B)) {
-      case ReuseShape::kDirect16x2:
-        return L("reuse launch", dk::gemv_reuse<16, 2, false>, grid, dim3(16 * 64), lds, p4, scales,
+      case ReuseShape::kStream:
+        return launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B);
+      case ReuseShape::kDirect8x2:
+        return L("reuse launch", dk::gemv_reuse<8, 2, false>, grid, dim3(8 * 64), lds, p4, scales,
                  x4, y, M, K, B);
       case ReuseShape::kDirect8x1:
         return L("reuse launch", dk::gemv_reuse<8, 1, false>, grid, dim3(8 * 64), lds, p4, scales,

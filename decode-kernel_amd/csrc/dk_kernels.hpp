@@ -300,13 +300,15 @@ __device__ __forceinline__ void v5_compute(const V5Stage<R, U, NB>& st, float (&
   }
 }
 
-template <int R, int U, int NB, typename Layout = LayoutLogical>
+// kStamp is the layout's stamp, or the reuse path's when that path runs this
+// kernel for one or two batch rows.
+template <int R, int U, int NB, typename Layout = LayoutLogical, int kStamp = Layout::kStamp>
 __global__ __launch_bounds__(kStreamWaves * 64) void gemv_v5(const uint4* __restrict__ packed,
                                                              const uint16_t* __restrict__ scales,
                                                              const uint4* __restrict__ x4,
                                                              uint16_t* __restrict__ y, int M, int K,
                                                              int B) {
-  write_stamp(Layout::kStamp);
+  write_stamp(kStamp);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // The grid size follows from M (it is the launch's), so no hidden argument
@@ -467,6 +469,10 @@ __global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
 //   * direct: no staging round trip before the first weight load; each lane
 //     loads the four scales of its D rows with the activations and weights,
 //     UG groups per stage (best for K <= 4096: 3-6% at M = K = 4096).
+// For one or two batch rows the reuse path runs the streaming kernel above
+// with NB = B instead (each decoded weight still serves every batch row):
+// 16 batch columns of MFMA operands cost more activation traffic than they
+// save there.
 // ---------------------------------------------------------------------------
 constexpr int kReuseBatch = 16;
 
@@ -542,6 +548,11 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ 
       const int g = g0 + u * KS;
       w[u] = buffer_load16<kLoadNonTemporal>(rw, g < G ? wbase + g * 64 : kOutOfRange);
     }
+    // Direct path: every load of the stage is issued before the first MFMA.
+    // Left to itself the scheduler moves the second group's activation loads
+    // behind the first group's MFMAs, which makes them wait for its weights
+    // (4.87 vs 5.48 us for 8 waves x 2 groups at M = K = 4096, B = 2).
+    if constexpr (!kStaged) __builtin_amdgcn_sched_barrier(0);
     if (kStaged) {
       const uint2 s4 = *reinterpret_cast<const uint2*>(sT + g0 * 16 + 4 * kq);
       sc[0][0] = h2f((uint16_t)(s4.x & 0xFFFFu));

@@ -190,6 +190,25 @@ def test_fp16_conversion_matches_ieee_on_edges():
     assert np.array_equal(got, ref)
 
 
+def test_fp16_rounding_and_doubling():
+    # The GPU linearity checks compare y(2x) with 2 y(x): rounding an fp32
+    # value t to fp16 commutes with doubling when fp16(t) is normal, and in
+    # the subnormal range the two differ by at most 2**-23. Both facts on
+    # every fp32 value around the subnormal/normal boundary and a random
+    # sample across the range.
+    rng = np.random.Generator(np.random.PCG64(9))
+    edge = np.arange(0, 3 << 20, 7, dtype=np.uint32) + np.uint32(0x33000000)  # ~2**-25 .. 2**-13
+    t = np.concatenate([edge.view(np.float32),
+                        rng.standard_normal(200000).astype(np.float32) * np.float32(3.0)])
+    t = np.concatenate([t, -t])
+    y1 = t.astype(np.float16)
+    y2 = (t * np.float32(2)).astype(np.float16)
+    normal = np.abs(y1.astype(np.float32)) >= 2.0 ** -14
+    assert np.array_equal(y2[normal].view(np.uint16), (y1[normal] * np.float16(2)).view(np.uint16))
+    diff = np.abs(y2[~normal].astype(np.float64) - 2 * y1[~normal].astype(np.float64))
+    assert diff.max() <= 2.0 ** -23 and (diff > 0).any()  # the exception is real
+
+
 # ------------------------------------------------ GEMV closed forms ---
 def test_gemv_one_hot_picks_single_weights():
     w, _ = oracle.make_case(6, 256, 1, 21, 0.05)
