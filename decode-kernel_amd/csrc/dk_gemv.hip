@@ -83,29 +83,54 @@ struct Launch {
   }
 };
 
-// v5 stage shapes (R rows per wave, U 16-byte chunks per lane per stage),
-// timed on MI355X as the bench times them: a HIP graph of 1000 back-to-back
-// steps over torch-allocated weight copies (> 640 MB, cold), B = 1, us:
-//   M = K = 4096:        R2 U2 3.68; double-buffered 3.76; R2 U1 3.80;
-//                        R1 U2 4.18; R4 U1 4.38; R2 U3 4.38; 1 / 4 / 8 waves
-//                        per workgroup 3.82 / 3.73 / 3.89; no XCD renumbering 3.76
-//   M = 11008, K = 4096: R2 U2 6.33 (1 wave per workgroup 6.20); R4 U1 6.83
-//   M = 4096, K = 11008: R2 U2 6.82; R2 U3 7.57; double-buffered 8.25; R4 U1 9.34
-//   M = 8192, K = 3584:  R2 U2 5.21; R3 U2 5.50; R2 U3 6.22
-// and, from an earlier per-launch sweep, R4 U1 for the 70B shapes
-// (M = 28672, K = 8192: 24.66 vs R2 U2 27.14; M = 8192, K = 28672: 23.36 vs
-// 28.55). Splitting K across the waves of a workgroup was slower in every
-// case above (3.79 at M = K = 4096, 7.48 at M = 4096, K = 11008).
-// B > 1, M = K = 4096 (earlier per-launch sweep):
+// One activation row: the streaming kernel with activations shared through
+// LDS (R rows per wave, U 16-byte chunks per lane per stage, W waves per
+// workgroup, next stage prefetched or not). Timed on MI355X as the bench
+// times it: a HIP graph of back-to-back steps over torch-allocated weight
+// copies (> 640 MB, cold), us per step, against gemv_v5 with activations in
+// registers (R2 U2, or R4 U1 at the 70B shapes, two waves per workgroup):
+//   M = K = 4096:         R1 U2 W8 prefetch 3.59 (R2 U2 W4 3.69; registers 3.73)
+//   M = 11008, K = 4096:  R2 U2 W4 5.83 (W8 5.72, prefetch 5.75; registers 6.32)
+//   M = 4096, K = 11008:  R1 U2 W16 prefetch 6.07 (no prefetch 6.49; registers 7.08)
+//   M = 28672, K = 8192:  R2 U2 W4 20.73 (prefetch 22.60; registers 23.04)
+//   M = 8192, K = 28672:  R2 U1 W16 prefetch 20.17 (no prefetch 19.79; registers 22.24)
+//   M = 8192, K = 3584:   R1 U2 W8 prefetch 4.40 (registers 5.23)
+//   M = 8192, K = 8192:   R2 U1 W16 prefetch 7.73 (R1 U2 W8 prefetch 8.15; registers 8.47)
+//   M = 4096, K = 2048:   R1 U1 W16 prefetch 2.72 (R1 U2 W8 prefetch 3.27; registers 3.46)
+//   M = K = 28672:        R2 U1 W8 64.65 (registers 75.82)
+// Over 19 shapes (M and K from 2048 to 28672) the choice below is within 1%
+// of the best of 18 variants on average and 6.5% at worst. Prefetching pays
+// when rows are few (few waves per SIMD to hide a stage's latency) and costs
+// occupancy when they are many; 16-wave workgroups share each activation
+// load among more rows when stages are many.
+template <int R, int U, int W, bool kPrefetch, typename Layout, int kStamp>
+int launch_lds_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
+                 int M, int K) {
+  dim3 grid((M + W * R - 1) / (W * R));
+  return L("v5 launch", dk::gemv_v5_lds<R, U, W, kPrefetch, Layout, kStamp>, grid, dim3(W * 64), 0,
+           p, s, x, y, M, K);
+}
+
+template <typename Layout, int kStamp>
+int launch_lds(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
+               int M, int K) {
+  if (K <= 2048) return launch_lds_t<1, 1, 16, true, Layout, kStamp>(L, p, s, x, y, M, K);
+  if (M > 8192) {
+    if (K <= 8192) return launch_lds_t<2, 2, 4, false, Layout, kStamp>(L, p, s, x, y, M, K);
+    return launch_lds_t<2, 1, 8, false, Layout, kStamp>(L, p, s, x, y, M, K);
+  }
+  if (K > 8192 && M <= 4096) return launch_lds_t<1, 2, 16, true, Layout, kStamp>(L, p, s, x, y, M, K);
+  if (K >= 8192 && M > 4096) return launch_lds_t<2, 1, 16, true, Layout, kStamp>(L, p, s, x, y, M, K);
+  return launch_lds_t<1, 2, 8, true, Layout, kStamp>(L, p, s, x, y, M, K);
+}
+
+// Batches: gemv_v5 with the activations of NB batch rows in registers, from
+// an earlier sweep (M = K = 4096, us per launch):
 //   B = 2:  R2 U1 NB2 4.81 (R4 U1 NB2 5.47; R2 U1 NB4 6.17)
 //   B = 4:  R4 U1 NB2 6.05 (R2 U1 NB4 6.81); B = 8: R4 U1 NB2 9.68 (11.71)
 //   B = 16: R4 U1 NB2 16.82 (21.73); M = 8192, K = 28672, B = 4: 56.0 (69.0)
-// Two rows per wave halve the activation loads and pairing; two chunks per
-// stage keep two weight loads in flight per row; more than that measured
-// slower on this memory system. With a batch, more rows per wave pay for
-// the extra activation registers; tiles of four batch rows were slower.
-// Two waves per workgroup with the XCD renumbering (finer-grained blocks of
-// rows per XCD).
+// More rows per wave pay for the extra activation registers; tiles of four
+// batch rows were slower. Two waves per workgroup with the XCD renumbering.
 constexpr int kV5WavesPerBlock = dk::kStreamWaves;
 
 template <int R, int U, int NB, typename Layout, int kStamp>
@@ -120,12 +145,7 @@ int launch_v5_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4*
 template <typename Layout = dk::LayoutLogical, int kStamp = Layout::kStamp>
 int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y, int M,
               int K, int B) {
-  if (B == 1) {
-    // Four rows per wave once both dimensions are large: still >= 2048 waves,
-    // and half the activation loads and pairing per weight.
-    if (M >= 8192 && K >= 8192) return launch_v5_t<4, 1, 1, Layout, kStamp>(L, p, s, x, y, M, K, B);
-    return launch_v5_t<2, 2, 1, Layout, kStamp>(L, p, s, x, y, M, K, B);
-  }
+  if (B == 1) return launch_lds<Layout, kStamp>(L, p, s, x, y, M, K);
   if (B == 2) return launch_v5_t<2, 1, 2, Layout, kStamp>(L, p, s, x, y, M, K, B);
   return launch_v5_t<4, 1, 2, Layout, kStamp>(L, p, s, x, y, M, K, B);
 }

@@ -355,6 +355,181 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemv_v5(const uint4* __rest
 }
 
 // ---------------------------------------------------------------------------
+// v5 for one activation row, with the activations shared through LDS (stamp 5,
+// or the layout's). A workgroup of W waves streams R rows per wave as gemv_v5
+// does, but each stage's activations (U * 4 KiB) are loaded once per
+// workgroup, one or two 16-byte loads per lane, paired once, and read by
+// every wave from LDS. gemv_v5 re-reads them per wave from L2, twice the
+// weight bytes at two rows per wave; that traffic and the pairing were the
+// largest cost left beside the weights (4-21% at the shapes measured).
+// Two LDS buffers alternate by stage, so one barrier per stage suffices: a
+// wave writes buffer b at stage s only after every wave has passed the
+// barrier of stage s-1, which each wave reaches after its reads of buffer b
+// (stage s-2). Waves past M still load activations and meet every barrier.
+// kPrefetch: the next stage's loads are issued before this stage's math, in
+// a second register set (the loop is unrolled by two so that no register
+// copy waits on a load, and the loads are unconditional, reading zeros past
+// the row end, so the wait counts stay exact). It pays when few waves share
+// a SIMD; with many rows the extra registers cost more occupancy than the
+// overlap gains.
+// ---------------------------------------------------------------------------
+template <int R, int U, int W>
+struct LdsStage {
+  static constexpr int kPieces = U * 4 * kWave;  // 16-byte activation pieces per stage
+  static constexpr int kPer = (kPieces + W * kWave - 1) / (W * kWave);
+  uint4 xv[kPer];
+  uint4 w[U][R];
+  uint32_t s[U][R];  // raw fp16 scale bits, converted where used
+};
+
+template <int R, int U, int W>
+__device__ __forceinline__ void lds_stage_load(LdsStage<R, U, W>& st, __amdgpu_buffer_rsrc_t rw,
+                                               __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rx,
+                                               int c0, int nck, int G, int tid, int lane) {
+  using S = LdsStage<R, U, W>;
+  // Activations of chunks [c0, c0 + 64U): piece p is bytes [16p, 16p + 16)
+  // of that range, so consecutive lanes read consecutive 16 bytes.
+#pragma unroll
+  for (int i = 0; i < S::kPer; ++i) {
+    const int piece = tid + i * W * kWave;
+    const int c = c0 + (piece >> 2);
+    st.xv[i] = buffer_load16<0>(
+        rx, (piece < S::kPieces && c < nck) ? (c0 * 4 + piece) * 16 : kOutOfRange);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int c = c0 + u * kWave + lane;
+    const bool ok = c < nck;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      st.s[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (r * G + (c >> 2)) * 2 : kOutOfRange,
+                                                        0, 0);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      st.w[u][r] = buffer_load16<kLoadNonTemporal>(rw, ok ? (r * nck + c) * 16 : kOutOfRange);
+  }
+}
+
+// Pairs this lane's activation pieces for the layout and stores them where
+// the lane that owns the chunk reads them: xs[u][j][l] holds the four pairs
+// of bytes [16j, 16j + 16) of chunk c0 + 64u + l.
+template <int R, int U, int W, typename Layout>
+__device__ __forceinline__ void lds_stage_publish(const LdsStage<R, U, W>& st,
+                                                  uint4 (&xs)[U][4][kWave], int tid) {
+  using S = LdsStage<R, U, W>;
+#pragma unroll
+  for (int i = 0; i < S::kPer; ++i) {
+    const int piece = tid + i * W * kWave;
+    if (S::kPieces % (W * kWave) == 0 || piece < S::kPieces) {
+      h2_t p[4];
+      Layout::pair(st.xv[i], p);
+      const int cr = piece >> 2;
+      xs[cr / kWave][piece & 3][cr % kWave] =
+          make_uint4(__builtin_bit_cast(uint32_t, p[0]), __builtin_bit_cast(uint32_t, p[1]),
+                     __builtin_bit_cast(uint32_t, p[2]), __builtin_bit_cast(uint32_t, p[3]));
+    }
+  }
+}
+
+template <int R, int U, int W, typename Layout>
+__device__ __forceinline__ void lds_stage_compute(const LdsStage<R, U, W>& st,
+                                                  const uint4 (&xs)[U][4][kWave], float (&acc)[R],
+                                                  int lane) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    h2_t xp[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 pv = xs[u][j][lane];
+      xp[j][0] = as_h2(pv.x);
+      xp[j][1] = as_h2(pv.y);
+      xp[j][2] = as_h2(pv.z);
+      xp[j][3] = as_h2(pv.w);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t words[4] = {st.w[u][r].x, st.w[u][r].y, st.w[u][r].z, st.w[u][r].w};
+      float part = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        h2_t q[4];
+        Layout::unpack(words[j], q);
+        part = __builtin_amdgcn_fdot2(q[0], xp[j][0], part, false);
+        part = __builtin_amdgcn_fdot2(q[1], xp[j][1], part, false);
+        part = __builtin_amdgcn_fdot2(q[2], xp[j][2], part, false);
+        part = __builtin_amdgcn_fdot2(q[3], xp[j][3], part, false);
+      }
+      acc[r] = __builtin_fmaf(part, h2f((uint16_t)st.s[u][r]), acc[r]);
+    }
+  }
+}
+
+template <int R, int U, int W, bool kPrefetch, typename Layout = LayoutLogical,
+          int kStamp = Layout::kStamp>
+__global__ __launch_bounds__(W * kWave) void gemv_v5_lds(const uint4* __restrict__ packed,
+                                                         const uint16_t* __restrict__ scales,
+                                                         const uint4* __restrict__ x4,
+                                                         uint16_t* __restrict__ y, int M, int K) {
+  write_stamp(kStamp);
+  __shared__ uint4 xs[2][U][4][kWave];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wg = xcd_contiguous_block(blockIdx.x, (M + W * R - 1) / (W * R));
+  const int row0 = (wg * W + wave) * R;
+  const bool active = row0 < M;  // wave-uniform
+  const int nck = K >> 5;
+  const int G = K >> 7;
+  // An inactive wave gets empty weight and scale descriptors: all its
+  // weight and scale loads read zero.
+  const int rows = active ? min(R, M - row0) : 0;
+  const int rbase = active ? row0 : 0;
+  const auto rw = buffer_rsrc(packed + (size_t)rbase * nck, (uint32_t)(rows * (K / 2)));
+  const auto rs = buffer_rsrc(scales + (size_t)rbase * G, (uint32_t)(rows * G * 2));
+  const auto rx = buffer_rsrc(x4, (uint32_t)K * 2);
+
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  constexpr int kStep = U * kWave;
+  if constexpr (kPrefetch) {
+    LdsStage<R, U, W> sa, sb;
+    lds_stage_load(sa, rw, rs, rx, 0, nck, G, tid, lane);
+    for (int c0 = 0;;) {
+      lds_stage_publish<R, U, W, Layout>(sa, xs[0], tid);
+      __syncthreads();
+      lds_stage_load(sb, rw, rs, rx, c0 + kStep, nck, G, tid, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      lds_stage_compute<R, U, W, Layout>(sa, xs[0], acc, lane);
+      c0 += kStep;
+      if (c0 >= nck) break;
+      lds_stage_publish<R, U, W, Layout>(sb, xs[1], tid);
+      __syncthreads();
+      lds_stage_load(sa, rw, rs, rx, c0 + kStep, nck, G, tid, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      lds_stage_compute<R, U, W, Layout>(sb, xs[1], acc, lane);
+      c0 += kStep;
+      if (c0 >= nck) break;
+    }
+  } else {
+    LdsStage<R, U, W> st;
+    int buf = 0;
+    for (int c0 = 0; c0 < nck; c0 += kStep, buf ^= 1) {
+      lds_stage_load(st, rw, rs, rx, c0, nck, G, tid, lane);
+      lds_stage_publish<R, U, W, Layout>(st, xs[buf], tid);
+      __syncthreads();
+      lds_stage_compute<R, U, W, Layout>(st, xs[buf], acc, lane);
+    }
+  }
+  if (!active) return;  // after the last barrier
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float t = wave_sum(acc[r]);
+    if (lane == 63 && row0 + r < M) y[row0 + r] = f2h(t);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // v4: split-K. grid = (row tiles of 4, S). Workgroup (tile, s) computes the
 // fp32 partial of its 4 rows over group slice s and stores it to
 // ws[s][b][row]; the last workgroup of a tile to finish adds the S partials
