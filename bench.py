@@ -61,7 +61,7 @@ VARIANTS = {
 }
 EXPECTED_STAMP = {"v0": 0, "v1": 1, "v1_wpr2": 12, "v1_wpr4": 14, "v2": 2, "v3": 3, "v4": 4,
                   "v5": 5, "reuse": 15, "v5_paired": 25}
-PROFILE_TRAFFIC = REPO / "profiles" / "traffic_c0_v5.json"
+PROFILE_TRAFFIC = REPO / "profiles" / "traffic_c0_gemv_v5_lds.json"
 
 
 def log(*a):
@@ -75,7 +75,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--configs", default="all",
                     help="comma list of c0,c1,c2,c3,c4a,c4b or 'all' (c0 is always run)")
-    ap.add_argument("--other-steps", type=int, default=200,
+    ap.add_argument("--other-steps", type=int, default=1000,
                     help="timed steps per variant outside the headline")
     ap.add_argument("--flush", choices=["read", "write", "none"], default="read")
     ap.add_argument("--flush-bytes", type=int, default=1 << 30)
@@ -488,7 +488,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": achieved, "peak": MI355X_HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": achieved / MI355X_HBM_PEAK_GBPS, "traffic": traffic,
-            "kernel": "dk::gemv_v5<2, 2, 1, dk::LayoutLogical>", "mean_us": headline["mean_us"],
+            "kernel": "dk::gemv_v5_lds<1, 2, 8, 1, true, dk::LayoutLogical, 5>", "mean_us": headline["mean_us"],
             "algorithmic_bytes": headline["bytes_moved"],
         },
         "cpu_baseline": cpu,

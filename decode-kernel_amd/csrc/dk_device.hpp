@@ -102,13 +102,11 @@ __device__ __forceinline__ h8_t pair_x8(const uint4& xv) {
 // eight activations are paired to match it.
 struct LayoutLogical {
   static constexpr int kStamp = 5;
-  static constexpr bool kLoadsFirst = false;
   static __device__ __forceinline__ void unpack(uint32_t w, h2_t (&q)[4]) { unpack_word(w, q); }
   static __device__ __forceinline__ void pair(const uint4& xv, h2_t (&p)[4]) { pair_x(xv, p); }
 };
 struct LayoutPaired {
   static constexpr int kStamp = 25;
-  static constexpr bool kLoadsFirst = true;
   static __device__ __forceinline__ void unpack(uint32_t w, h2_t (&q)[4]) { unpack_word(w, q); }
   static __device__ __forceinline__ void pair(const uint4& xv, h2_t (&p)[4]) {
     p[0] = as_h2(xv.x);  // (x0, x1)

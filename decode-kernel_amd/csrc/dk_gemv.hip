@@ -87,8 +87,9 @@ struct Launch {
 // LDS (R rows per wave, U 16-byte chunks per lane per stage, W waves per
 // workgroup, next stage prefetched or not). Timed on MI355X as the bench
 // times it: a HIP graph of back-to-back steps over torch-allocated weight
-// copies (> 640 MB, cold), us per step, against gemv_v5 with activations in
-// registers (R2 U2, or R4 U1 at the 70B shapes, two waves per workgroup):
+// copies (> 640 MB, cold), us per step, against the earlier form of the
+// kernel that loaded the activations per wave into registers ("registers":
+// R2 U2, or R4 U1 at the 70B shapes, two waves per workgroup):
 //   M = K = 4096:         R1 U2 W8 prefetch 3.59 (R2 U2 W4 3.69; registers 3.73)
 //   M = 11008, K = 4096:  R2 U2 W4 5.83 (W8 5.72, prefetch 5.75; registers 6.32)
 //   M = 4096, K = 11008:  R1 U2 W16 prefetch 6.07 (no prefetch 6.49; registers 7.08)
@@ -103,12 +104,12 @@ struct Launch {
 // when rows are few (few waves per SIMD to hide a stage's latency) and costs
 // occupancy when they are many; 16-wave workgroups share each activation
 // load among more rows when stages are many.
-template <int R, int U, int W, bool kPrefetch, typename Layout, int kStamp>
+template <int R, int U, int W, bool kPrefetch, typename Layout, int kStamp, int NB = 1>
 int launch_lds_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
-                 int M, int K) {
-  dim3 grid((M + W * R - 1) / (W * R));
-  return L("v5 launch", dk::gemv_v5_lds<R, U, W, kPrefetch, Layout, kStamp>, grid, dim3(W * 64), 0,
-           p, s, x, y, M, K);
+                 int M, int K, int B = 1) {
+  dim3 grid((M + W * R - 1) / (W * R), (B + NB - 1) / NB);
+  return L("v5 launch", dk::gemv_v5_lds<R, U, W, NB, kPrefetch, Layout, kStamp>, grid, dim3(W * 64),
+           0, p, s, x, y, M, K, B);
 }
 
 template <typename Layout, int kStamp>
@@ -124,56 +125,78 @@ int launch_lds(const Launch& L, const uint4* p, const uint16_t* s, const uint4* 
   return launch_lds_t<1, 2, 8, true, Layout, kStamp>(L, p, s, x, y, M, K);
 }
 
-// Batches: gemv_v5 with the activations of NB batch rows in registers, from
-// an earlier sweep (M = K = 4096, us per launch):
-//   B = 2:  R2 U1 NB2 4.81 (R4 U1 NB2 5.47; R2 U1 NB4 6.17)
-//   B = 4:  R4 U1 NB2 6.05 (R2 U1 NB4 6.81); B = 8: R4 U1 NB2 9.68 (11.71)
-//   B = 16: R4 U1 NB2 16.82 (21.73); M = 8192, K = 28672, B = 4: 56.0 (69.0)
-// More rows per wave pay for the extra activation registers; tiles of four
-// batch rows were slower. Two waves per workgroup with the XCD renumbering.
-constexpr int kV5WavesPerBlock = dk::kStreamWaves;
-
-template <int R, int U, int NB, typename Layout, int kStamp>
-int launch_v5_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
-                int M, int K, int B) {
-  const int rows_per_block = kV5WavesPerBlock * R;
-  dim3 grid((M + rows_per_block - 1) / rows_per_block, (B + NB - 1) / NB);
-  return L("v5 launch", dk::gemv_v5<R, U, NB, Layout, kStamp>, grid, dim3(kV5WavesPerBlock * 64), 0,
-           p, s, x, y, M, K, B);
-}
-
+// Batches: the same LDS kernel with NB batch rows per stage (grid.y covers
+// the batch in tiles of NB rows), us per launch:
+//   M = K = 4096:        B = 2: R1 U2 W8 NB2 prefetch 3.93 (registers 4.55)
+//                        B = 3: R1 U1 W8 NB3 prefetch 4.66 (registers 5.63)
+//                        B = 4: R2 U1 W4 NB4 prefetch 5.27 (registers 5.77)
+//                        B = 8: R2 U1 W8 NB4 7.57 (registers 9.50)
+//   M = 11008, K = 4096: B = 2: R2 U1 W8 NB2 prefetch 7.10 (registers 8.91)
+//                        B = 4: R2 U1 W8 NB4 9.68 (registers 12.66)
+//   M = 4096, K = 11008: B = 2: R1 U2 W8 NB2 prefetch 7.46 (registers 9.04)
+//                        B = 4: R2 U1 W4 NB4 prefetch 11.11 (registers 13.34)
+//   M = 28672, K = 8192: B = 2: R2 U1 W8 NB2 prefetch 26.4 (registers 37.5)
+//                        B = 4: R2 U1 W8 NB4 36.1 (registers 54.7)
+//   M = 8192, K = 28672: B = 2: R2 U1 W8 NB2 prefetch 25.5 (registers 38.2)
+//                        B = 4: R2 U1 W8 NB4 38.9 (registers 54.7)
+// (registers: activations per wave, R2 U1 NB2 for B = 2, R4 U1 NB2 tiles
+// otherwise.)
 template <typename Layout = dk::LayoutLogical, int kStamp = Layout::kStamp>
 int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y, int M,
               int K, int B) {
   if (B == 1) return launch_lds<Layout, kStamp>(L, p, s, x, y, M, K);
-  if (B == 2) return launch_v5_t<2, 1, 2, Layout, kStamp>(L, p, s, x, y, M, K, B);
-  return launch_v5_t<4, 1, 2, Layout, kStamp>(L, p, s, x, y, M, K, B);
+  if (M <= 4096) {
+    if (B == 2) return launch_lds_t<1, 2, 8, true, Layout, kStamp, 2>(L, p, s, x, y, M, K, B);
+    if (B == 3) return launch_lds_t<1, 1, 8, true, Layout, kStamp, 3>(L, p, s, x, y, M, K, B);
+    return launch_lds_t<2, 1, 4, true, Layout, kStamp, 4>(L, p, s, x, y, M, K, B);
+  }
+  if (B == 2) return launch_lds_t<2, 1, 8, true, Layout, kStamp, 2>(L, p, s, x, y, M, K, B);
+  return launch_lds_t<2, 1, 8, false, Layout, kStamp, 4>(L, p, s, x, y, M, K, B);
 }
 
-// Fused gate/up (R rows of each matrix per wave, U chunks per stage, NB
-// batch rows per tile), from a sweep on MI355X, back-to-back over cold
-// weights (us per launch for both matrices):
-//   I = 11008, H = 4096:  R2 U1 10.71 (R1 U2 10.84; two v5 GEMVs 13.6)
-//   I = 14336, H = 4096:  R2 U2 12.81, R2 U1 13.04 (R1 U2 13.34)
-//   I = 3584,  H = 8192:  R2 U1 8.16 (R1 U2 9.06; R4 U1 11.33)
-//   I = 28672, H = 8192:  R4 U1 41.37 (R2 U1 44.60; two v5 GEMVs 49.3)
-//   I = 11008, H = 4096, B = 4: R2 U1 NB2 22.14 (R1 U1 NB2 27.48)
-template <int R, int U, int NB>
-int launch_gate_up_t(const Launch& L, const uint4* g, const uint16_t* gs, const uint4* u,
-                     const uint16_t* us, const uint4* x, uint16_t* h, int I, int H, int B) {
-  const int rows_per_block = kV5WavesPerBlock * R;
-  dim3 grid((I + rows_per_block - 1) / rows_per_block, (B + NB - 1) / NB);
-  return L("gate/up launch", dk::gate_up_silu<R, U, NB>, grid, dim3(kV5WavesPerBlock * 64), 0, g,
+// Fused gate/up, R rows of each matrix per wave, on the LDS stage loop (U
+// chunks per stage, W waves per workgroup, next stage prefetched or not, NB
+// batch rows per stage). Timed on MI355X back-to-back over cold weights (us
+// per launch for both matrices), against the fused kernel with activations
+// in registers (two waves per workgroup, R2 U1, NB2 tiles for batches):
+//   I = 11008, H = 4096:  R1 U2 W4 9.17 (prefetch 9.57, W8 9.75; registers 10.25)
+//                         B = 2: R1 U2 W4 prefetch 12.44 (registers 13.71)
+//                         B = 4: R1 U1 W8 NB4 19.56 (registers 22.65)
+//   I = 14336, H = 4096:  R1 U2 W4 11.88 (prefetch 11.65; registers 12.43)
+//   I = 3584,  H = 8192:  R1 U1 W16 prefetch 7.37 (W8 7.45; registers 7.82)
+//                         B = 2: 8.82 (registers 9.89); B = 4: NB4 12.71 (registers 17.20)
+//   I = 14336, H = 8192:  R1 U2 W8 20.90 (W4 21.43; registers 23.27)
+//   I = 28672, H = 8192:  R1 U2 W8 38.91 (R2 U1 W8 38.82; registers 40.17)
+//                         B = 2: R2 U1 W4 48.56 (registers 55.51)
+//                         B = 4: R1 U1 W8 NB4 74.52 (registers 107.87)
+//   I = 4096,  H = 4096:  R1 U2 W4 prefetch 5.02 (registers 5.29)
+template <int R, int U, int W, bool kPrefetch, int NB = 1>
+int launch_gate_up_lds_t(const Launch& L, const uint4* g, const uint16_t* gs, const uint4* u,
+                         const uint16_t* us, const uint4* x, uint16_t* h, int I, int H, int B = 1) {
+  dim3 grid((I + W * R - 1) / (W * R), (B + NB - 1) / NB);
+  return L("gate/up launch", dk::gate_up_silu_lds<R, U, W, NB, kPrefetch>, grid, dim3(W * 64), 0, g,
            gs, u, us, x, I, H, B, h);
 }
 
 int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const uint4* u,
                    const uint16_t* us, const uint4* x, uint16_t* h, int I, int H, int B) {
-  if (B == 1) {
-    if (I >= 16384 && H >= 8192) return launch_gate_up_t<4, 1, 1>(L, g, gs, u, us, x, h, I, H, B);
-    return launch_gate_up_t<2, 1, 1>(L, g, gs, u, us, x, h, I, H, B);
+  if (I <= 4096) {
+    if (B == 1) {
+      if (H > 4096) return launch_gate_up_lds_t<1, 1, 16, true>(L, g, gs, u, us, x, h, I, H);
+      return launch_gate_up_lds_t<1, 2, 4, true>(L, g, gs, u, us, x, h, I, H);
+    }
+    if (B == 2) return launch_gate_up_lds_t<1, 1, 16, true, 2>(L, g, gs, u, us, x, h, I, H, B);
+    return launch_gate_up_lds_t<1, 1, 16, true, 4>(L, g, gs, u, us, x, h, I, H, B);
   }
-  return launch_gate_up_t<2, 1, 2>(L, g, gs, u, us, x, h, I, H, B);
+  if (B == 1) {
+    if (H <= 4096) return launch_gate_up_lds_t<1, 2, 4, false>(L, g, gs, u, us, x, h, I, H);
+    return launch_gate_up_lds_t<1, 2, 8, false>(L, g, gs, u, us, x, h, I, H);
+  }
+  if (B == 2) {
+    if (H <= 4096) return launch_gate_up_lds_t<1, 2, 4, true, 2>(L, g, gs, u, us, x, h, I, H, B);
+    return launch_gate_up_lds_t<2, 1, 4, false, 2>(L, g, gs, u, us, x, h, I, H, B);
+  }
+  return launch_gate_up_lds_t<1, 1, 8, false, 4>(L, g, gs, u, us, x, h, I, H, B);
 }
 
 // Reuse-path shapes (waves per 16-row tile, groups per stage, scales staged
@@ -198,7 +221,7 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 enum class ReuseShape { kStream, kDirect8x2, kDirect8x1, kStaged16, kStaged8 };
 
 ReuseShape reuse_shape(int M, int K, int B) {
-  if (B == 1 || (B == 2 && K <= 4096)) return ReuseShape::kStream;
+  if (B <= 2 || (B <= 4 && M >= 8192)) return ReuseShape::kStream;
   const int tiles = (M + 15) / 16;
   // Rows too long for the staged copy in LDS take the direct path too.
   const bool fits = dk::reuse_lds_bytes_for(16, K, true) <= (size_t)lds_limit_bytes();

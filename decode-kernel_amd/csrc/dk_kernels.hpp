@@ -177,26 +177,12 @@ __global__ __launch_bounds__(256) void gemv_v23(const uint4* __restrict__ packed
 }
 
 // ---------------------------------------------------------------------------
-// v5: the tuned streaming kernel. Each wave owns R consecutive rows; lane l
-// owns 16-byte chunks l, l+64, ... of each of them, U chunks per lane per
-// stage. All loads of a stage are raw buffer loads through SGPR resource
-// descriptors scoped to the wave's rows (a chunk past the row end, or a row
-// past M, is an out-of-range offset that reads 0, so tails need no branches
-// and the loads issue back to back): the NB activation chunks first, then
-// the scales, then the weights with the non-temporal hint (read-once data).
-// Activations are paired once per stage and reused for all R rows. Load
-// latency is hidden by the other waves on the SIMD, not by double buffering
-// inside a wave (2% slower at M = K = 4096 and 20% at M = 4096, K = 11008
-// once the decode was 13 ops per word).
-// grid.y covers the batch in tiles of NB rows; workgroup ids are renumbered
-// so each XCD streams one contiguous block of rows (measured 2-5% faster).
-// Reference: csrc/gemv_w4a16.cu:318-357.
+// Raw buffer loads for the streaming kernels: SGPR resource descriptors
+// scoped to a wave's rows, so a chunk past the row end or a row past M is an
+// out-of-range offset that reads 0 (tails need no branches and the loads
+// issue back to back).
 // ---------------------------------------------------------------------------
 constexpr int kOutOfRange = (int)0x80000000;  // beyond any descriptor's num_records
-// Waves per workgroup of the streaming kernels (v5 and the fused gate/up):
-// a compile-time constant, so no wave reads the dispatch packet's workgroup
-// size before issuing its first load.
-constexpr int kStreamWaves = 2;
 constexpr int kLoadNonTemporal = 2;            // buffer-load cache policy bit "nt"
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
@@ -212,70 +198,134 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, int off
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-template <int R, int U, int NB>
-struct V5Stage {
+// ---------------------------------------------------------------------------
+// v5: the streaming kernel (stamp 5, or the layout's). Each wave owns R
+// consecutive rows; lane l owns 16-byte chunks l, l+64, ... of each of them,
+// U chunks per lane per stage. A stage's loads are the activations, then
+// the scales, then the weights with the non-temporal hint (read-once data).
+// The activations of a stage (NB batch rows x U * 4 KiB) are loaded once per
+// workgroup of W waves, one or two 16-byte loads per lane, paired once for
+// the layout, and read by every wave from LDS. Loading them per wave instead
+// (an earlier form of this kernel) re-reads twice the weight bytes from L2
+// at two rows per wave and pairs them in every wave; that cost 4-21% at the
+// shapes measured for one batch row and more with a batch.
+// Workgroup ids are renumbered so each XCD streams one contiguous block of
+// rows (measured 2-5% faster). Reference: csrc/gemv_w4a16.cu:318-357.
+// Two LDS buffers alternate by stage, so one barrier per stage suffices: a
+// wave writes buffer b at stage s only after every wave has passed the
+// barrier of stage s-1, which each wave reaches after its reads of buffer b
+// (stage s-2). Waves past M still load activations and meet every barrier.
+// kPrefetch: the next stage's loads are issued before this stage's math, in
+// a second register set (the loop is unrolled by two so that no register
+// copy waits on a load, and the loads are unconditional, reading zeros past
+// the row end, so the wait counts stay exact). It pays when few waves share
+// a SIMD; with many rows the extra registers cost more occupancy than the
+// overlap gains.
+// grid.y covers the batch in tiles of NB rows.
+// ---------------------------------------------------------------------------
+template <int R, int U, int W, int NB>
+struct LdsStage {
+  static constexpr int kPiecesPerRow = U * 4 * kWave;  // 16-byte pieces of one batch row
+  static constexpr int kPieces = NB * kPiecesPerRow;
+  static constexpr int kPer = (kPieces + W * kWave - 1) / (W * kWave);
+  uint4 xv[kPer];
   uint4 w[U][R];
-  float s[U][R];
-  uint4 xv[U][NB][4];
+  uint32_t s[U][R];  // raw fp16 scale bits, converted where used
 };
 
-// Loads one stage: rows r < kSplit come from (rw, rs), rows r >= kSplit
-// from (rw2, rs2) as their row r - kSplit (the fused gate/up kernel streams
-// two matrices against one activation load; plain v5 has kSplit = R).
-template <int R, int U, int NB, int kSplit = R>
-__device__ __forceinline__ void v5_load(V5Stage<R, U, NB>& st, __amdgpu_buffer_rsrc_t rw,
-                                        __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rx,
-                                        int c0, int nck, int G, int K, int b0, int B, int lane,
-                                        __amdgpu_buffer_rsrc_t rw2, __amdgpu_buffer_rsrc_t rs2) {
-  int c[U];
-  bool ok[U];
+// One stage's activations in LDS: slot ((b * U + u) * 4 + j) * 64 + l holds
+// the pairs of bytes [16j, 16j + 16) of chunk c0 + 64u + l of batch row
+// b0 + b.
+template <int U, int W, int NB>
+struct LdsActsT {
+  static constexpr int kSlots = NB * U * 4 * kWave;
+  using type = uint4[2][kSlots];
+};
+template <int U, int W, int NB>
+using LdsActs = typename LdsActsT<U, W, NB>::type;
+
+// Rows r < kSplit come from (rw, rs), rows r >= kSplit from (rw2, rs2) as
+// their row r - kSplit (the fused gate/up kernel streams two matrices
+// against one activation stage; the GEMV has kSplit = R).
+template <int R, int U, int W, int NB, int kSplit>
+__device__ __forceinline__ void lds_stage_load(LdsStage<R, U, W, NB>& st, __amdgpu_buffer_rsrc_t rw,
+                                               __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rw2,
+                                               __amdgpu_buffer_rsrc_t rs2, __amdgpu_buffer_rsrc_t rx,
+                                               int c0, int nck, int G, int K, int b0, int B, int tid,
+                                               int lane) {
+  using S = LdsStage<R, U, W, NB>;
+  // Activations of chunks [c0, c0 + 64U) of batch row b0 + b: piece p of
+  // that row is bytes [16p, 16p + 16) of the range, so consecutive lanes
+  // read consecutive 16 bytes.
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    c[u] = c0 + u * kWave + lane;
-    ok[u] = c[u] < nck;
+  for (int i = 0; i < S::kPer; ++i) {
+    const int piece = tid + i * W * kWave;
+    const int b = piece / S::kPiecesPerRow;
+    const int p = piece % S::kPiecesPerRow;
+    const int c = c0 + (p >> 2);
+    const bool ok = piece < S::kPieces && c < nck && b0 + b < B;
+    st.xv[i] = buffer_load16<0>(rx, ok ? (b0 + b) * K * 2 + (c0 * 4 + p) * 16 : kOutOfRange);
   }
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int off = (ok[u] && b0 + b < B) ? (b0 + b) * K * 2 + c[u] * 64 : kOutOfRange;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) st.xv[u][b][j] = buffer_load16<0>(rx, off + 16 * j);
-    }
-#pragma unroll
-  for (int u = 0; u < U; ++u)
+  for (int u = 0; u < U; ++u) {
+    const int c = c0 + u * kWave + lane;
+    const bool ok = c < nck;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int rr = r < kSplit ? r : r - kSplit;
-      const int off = ok[u] ? (rr * G + (c[u] >> 2)) * 2 : kOutOfRange;
-      st.s[u][r] = h2f(__builtin_amdgcn_raw_buffer_load_b16(r < kSplit ? rs : rs2, off, 0, 0));
+      st.s[u][r] = __builtin_amdgcn_raw_buffer_load_b16(
+          r < kSplit ? rs : rs2, ok ? (rr * G + (c >> 2)) * 2 : kOutOfRange, 0, 0);
     }
-#pragma unroll
-  for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int rr = r < kSplit ? r : r - kSplit;
-      const int off = ok[u] ? (rr * nck + c[u]) * 16 : kOutOfRange;
-      st.w[u][r] = buffer_load16<kLoadNonTemporal>(r < kSplit ? rw : rw2, off);
+      st.w[u][r] = buffer_load16<kLoadNonTemporal>(r < kSplit ? rw : rw2,
+                                                   ok ? (rr * nck + c) * 16 : kOutOfRange);
     }
+  }
 }
 
-template <int R, int U, int NB>
-__device__ __forceinline__ void v5_load(V5Stage<R, U, NB>& st, __amdgpu_buffer_rsrc_t rw,
-                                        __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rx,
-                                        int c0, int nck, int G, int K, int b0, int B, int lane) {
-  v5_load<R, U, NB, R>(st, rw, rs, rx, c0, nck, G, K, b0, B, lane, rw, rs);
+// Pairs this lane's activation pieces for the layout and stores them where
+// the lane that owns the chunk reads them (slot layout above). Lanes past
+// the stage's pieces (workgroups of more than 4U * NB waves) have none; the
+// test is uniform per wave, so those waves skip the store.
+template <int R, int U, int W, int NB, typename Layout>
+__device__ __forceinline__ void lds_stage_publish(const LdsStage<R, U, W, NB>& st,
+                                                  uint4 (&xs)[LdsActsT<U, W, NB>::kSlots],
+                                                  int tid) {
+  using S = LdsStage<R, U, W, NB>;
+#pragma unroll
+  for (int i = 0; i < S::kPer; ++i) {
+    const int piece = tid + i * W * kWave;
+    if (S::kPieces % (W * kWave) == 0 || piece < S::kPieces) {
+      const int b = piece / S::kPiecesPerRow;
+      const int cr = (piece % S::kPiecesPerRow) >> 2;  // chunk within the stage: 64 u + l
+      h2_t p[4];
+      Layout::pair(st.xv[i], p);
+      xs[((b * U + cr / kWave) * 4 + (piece & 3)) * kWave + cr % kWave] =
+          make_uint4(__builtin_bit_cast(uint32_t, p[0]), __builtin_bit_cast(uint32_t, p[1]),
+                     __builtin_bit_cast(uint32_t, p[2]), __builtin_bit_cast(uint32_t, p[3]));
+    }
+  }
 }
 
-template <int R, int U, int NB, typename Layout = LayoutLogical>
-__device__ __forceinline__ void v5_compute(const V5Stage<R, U, NB>& st, float (&acc)[NB][R]) {
+template <int R, int U, int W, int NB, typename Layout>
+__device__ __forceinline__ void lds_stage_compute(const LdsStage<R, U, W, NB>& st,
+                                                  const uint4 (&xs)[LdsActsT<U, W, NB>::kSlots],
+                                                  float (&acc)[NB][R], int lane) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     h2_t xp[NB][4][4];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) Layout::pair(st.xv[u][b][j], xp[b][j]);
+      for (int j = 0; j < 4; ++j) {
+        const uint4 pv = xs[((b * U + u) * 4 + j) * kWave + lane];
+        xp[b][j][0] = as_h2(pv.x);
+        xp[b][j][1] = as_h2(pv.y);
+        xp[b][j][2] = as_h2(pv.z);
+        xp[b][j][3] = as_h2(pv.w);
+      }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const uint32_t words[4] = {st.w[u][r].x, st.w[u][r].y, st.w[u][r].z, st.w[u][r].w};
@@ -294,190 +344,98 @@ __device__ __forceinline__ void v5_compute(const V5Stage<R, U, NB>& st, float (&
           part[b] = __builtin_amdgcn_fdot2(q[3], xp[b][j][3], part[b], false);
         }
       }
+      const float sc = h2f((uint16_t)st.s[u][r]);
 #pragma unroll
-      for (int b = 0; b < NB; ++b) acc[b][r] = __builtin_fmaf(part[b], st.s[u][r], acc[b][r]);
+      for (int b = 0; b < NB; ++b) acc[b][r] = __builtin_fmaf(part[b], sc, acc[b][r]);
     }
   }
 }
 
-// kStamp is the layout's stamp, or the reuse path's when that path runs this
-// kernel for one or two batch rows.
-template <int R, int U, int NB, typename Layout = LayoutLogical, int kStamp = Layout::kStamp>
-__global__ __launch_bounds__(kStreamWaves * 64) void gemv_v5(const uint4* __restrict__ packed,
-                                                             const uint16_t* __restrict__ scales,
-                                                             const uint4* __restrict__ x4,
-                                                             uint16_t* __restrict__ y, int M, int K,
-                                                             int B) {
-  write_stamp(kStamp);
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // The grid size follows from M (it is the launch's), so no hidden argument
-  // is read before the first load.
-  const int wg = xcd_contiguous_block(blockIdx.x, (M + kStreamWaves * R - 1) / (kStreamWaves * R));
-  const int row0 = (wg * kStreamWaves + wave) * R;
-  if (row0 >= M) return;  // wave-uniform; no barriers in this kernel
-  const int b0 = blockIdx.y * NB;
-  const int nck = K >> 5;
-  const int G = K >> 7;
-  const int rows = min(R, M - row0);
-  // Descriptors cover only this wave's rows and the activations: every valid
-  // offset stays below 2^31 and rows past M read as zero.
-  const auto rw = buffer_rsrc(packed + (size_t)row0 * nck, (uint32_t)(rows * (K / 2)));
-  const auto rs = buffer_rsrc(scales + (size_t)row0 * G, (uint32_t)(rows * G * 2));
-  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
+// Workgroup barrier for the stage loop. The scheduling barriers keep ALU
+// work on either side of it: left alone, the scheduler hoists the weight
+// decode (pure ALU on loaded registers) above s_barrier, which makes the
+// wave wait for its weights before the barrier instead of after it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+}
 
-  float acc[NB][R];
+// The stage loop shared by the GEMV and the fused gate/up kernel: acc[b][r]
+// is row r's fp32 sum for batch row b0 + b over this lane's chunks of K.
+template <int R, int U, int W, int NB, bool kPrefetch, typename Layout, int kSplit>
+__device__ __forceinline__ void lds_stream(LdsActs<U, W, NB>& xs, float (&acc)[NB][R],
+                                           __amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs,
+                                           __amdgpu_buffer_rsrc_t rw2, __amdgpu_buffer_rsrc_t rs2,
+                                           __amdgpu_buffer_rsrc_t rx, int nck, int G, int K, int b0,
+                                           int B, int tid, int lane) {
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[b][r] = 0.f;
-
   constexpr int kStep = U * kWave;
-  V5Stage<R, U, NB> st;
-  for (int c0 = 0; c0 < nck; c0 += kStep) {
-    v5_load(st, rw, rs, rx, c0, nck, G, K, b0, B, lane);
-    // With the paired layout's shorter math the scheduler interleaves it
-    // between the stage's loads, which cuts the loads in flight per wave (it
-    // made that layout 23% slower at M = 8192, K = 28672); the barrier keeps
-    // them back to back. For the logical layout it changes nothing beyond
-    // +-2%, so it is a trait of the layout.
-    if constexpr (Layout::kLoadsFirst) __builtin_amdgcn_sched_barrier(0);
-    v5_compute<R, U, NB, Layout>(st, acc);
-  }
-
-#pragma unroll
-  for (int b = 0; b < NB; ++b)
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float t = wave_sum(acc[b][r]);
-      if (lane == 63 && row0 + r < M && b0 + b < B) y[(size_t)(b0 + b) * M + row0 + r] = f2h(t);
+  if constexpr (kPrefetch) {
+    // Two register sets, the loop unrolled by two so that no register copy
+    // waits on a load; the prefetch loads are unconditional (zeros past the
+    // row end) so the wait counts stay exact. The compiler sinks the first
+    // half's prefetch below the exit test, so only every other stage is
+    // prefetched before the math. Taking stages in pairs (every prefetch
+    // ahead of the math) measured 2-4% slower at 3-7 stages per row and 2%
+    // faster at 14 (M = 8192, K = 28672). Workgroups with more lanes than
+    // activation pieces keep the publish test: giving the spare lanes
+    // padding slots instead (so every lane loads and stores) cost 11-17%.
+    LdsStage<R, U, W, NB> sa, sb;
+    lds_stage_load<R, U, W, NB, kSplit>(sa, rw, rs, rw2, rs2, rx, 0, nck, G, K, b0, B, tid, lane);
+    for (int c0 = 0;;) {
+      lds_stage_publish<R, U, W, NB, Layout>(sa, xs[0], tid);
+      __syncthreads();
+      lds_stage_load<R, U, W, NB, kSplit>(sb, rw, rs, rw2, rs2, rx, c0 + kStep, nck, G, K, b0, B,
+                                          tid, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      lds_stage_compute<R, U, W, NB, Layout>(sa, xs[0], acc, lane);
+      c0 += kStep;
+      if (c0 >= nck) break;
+      lds_stage_publish<R, U, W, NB, Layout>(sb, xs[1], tid);
+      __syncthreads();
+      lds_stage_load<R, U, W, NB, kSplit>(sa, rw, rs, rw2, rs2, rx, c0 + kStep, nck, G, K, b0, B,
+                                          tid, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      lds_stage_compute<R, U, W, NB, Layout>(sb, xs[1], acc, lane);
+      c0 += kStep;
+      if (c0 >= nck) break;
     }
-}
-
-// ---------------------------------------------------------------------------
-// v5 for one activation row, with the activations shared through LDS (stamp 5,
-// or the layout's). A workgroup of W waves streams R rows per wave as gemv_v5
-// does, but each stage's activations (U * 4 KiB) are loaded once per
-// workgroup, one or two 16-byte loads per lane, paired once, and read by
-// every wave from LDS. gemv_v5 re-reads them per wave from L2, twice the
-// weight bytes at two rows per wave; that traffic and the pairing were the
-// largest cost left beside the weights (4-21% at the shapes measured).
-// Two LDS buffers alternate by stage, so one barrier per stage suffices: a
-// wave writes buffer b at stage s only after every wave has passed the
-// barrier of stage s-1, which each wave reaches after its reads of buffer b
-// (stage s-2). Waves past M still load activations and meet every barrier.
-// kPrefetch: the next stage's loads are issued before this stage's math, in
-// a second register set (the loop is unrolled by two so that no register
-// copy waits on a load, and the loads are unconditional, reading zeros past
-// the row end, so the wait counts stay exact). It pays when few waves share
-// a SIMD; with many rows the extra registers cost more occupancy than the
-// overlap gains.
-// ---------------------------------------------------------------------------
-template <int R, int U, int W>
-struct LdsStage {
-  static constexpr int kPieces = U * 4 * kWave;  // 16-byte activation pieces per stage
-  static constexpr int kPer = (kPieces + W * kWave - 1) / (W * kWave);
-  uint4 xv[kPer];
-  uint4 w[U][R];
-  uint32_t s[U][R];  // raw fp16 scale bits, converted where used
-};
-
-template <int R, int U, int W>
-__device__ __forceinline__ void lds_stage_load(LdsStage<R, U, W>& st, __amdgpu_buffer_rsrc_t rw,
-                                               __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rx,
-                                               int c0, int nck, int G, int tid, int lane) {
-  using S = LdsStage<R, U, W>;
-  // Activations of chunks [c0, c0 + 64U): piece p is bytes [16p, 16p + 16)
-  // of that range, so consecutive lanes read consecutive 16 bytes.
-#pragma unroll
-  for (int i = 0; i < S::kPer; ++i) {
-    const int piece = tid + i * W * kWave;
-    const int c = c0 + (piece >> 2);
-    st.xv[i] = buffer_load16<0>(
-        rx, (piece < S::kPieces && c < nck) ? (c0 * 4 + piece) * 16 : kOutOfRange);
-  }
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int c = c0 + u * kWave + lane;
-    const bool ok = c < nck;
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-      st.s[u][r] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (r * G + (c >> 2)) * 2 : kOutOfRange,
-                                                        0, 0);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-      st.w[u][r] = buffer_load16<kLoadNonTemporal>(rw, ok ? (r * nck + c) * 16 : kOutOfRange);
-  }
-}
-
-// Pairs this lane's activation pieces for the layout and stores them where
-// the lane that owns the chunk reads them: xs[u][j][l] holds the four pairs
-// of bytes [16j, 16j + 16) of chunk c0 + 64u + l.
-template <int R, int U, int W, typename Layout>
-__device__ __forceinline__ void lds_stage_publish(const LdsStage<R, U, W>& st,
-                                                  uint4 (&xs)[U][4][kWave], int tid) {
-  using S = LdsStage<R, U, W>;
-#pragma unroll
-  for (int i = 0; i < S::kPer; ++i) {
-    const int piece = tid + i * W * kWave;
-    if (S::kPieces % (W * kWave) == 0 || piece < S::kPieces) {
-      h2_t p[4];
-      Layout::pair(st.xv[i], p);
-      const int cr = piece >> 2;
-      xs[cr / kWave][piece & 3][cr % kWave] =
-          make_uint4(__builtin_bit_cast(uint32_t, p[0]), __builtin_bit_cast(uint32_t, p[1]),
-                     __builtin_bit_cast(uint32_t, p[2]), __builtin_bit_cast(uint32_t, p[3]));
+  } else {
+    LdsStage<R, U, W, NB> st;
+    int buf = 0;
+    for (int c0 = 0; c0 < nck; c0 += kStep, buf ^= 1) {
+      lds_stage_load<R, U, W, NB, kSplit>(st, rw, rs, rw2, rs2, rx, c0, nck, G, K, b0, B, tid, lane);
+      // Every load of the stage issues before the publish waits on the
+      // activation pieces (left alone, the scheduler can put that wait
+      // between the loads).
+      __builtin_amdgcn_sched_barrier(0);
+      lds_stage_publish<R, U, W, NB, Layout>(st, xs[buf], tid);
+      lds_barrier();
+      lds_stage_compute<R, U, W, NB, Layout>(st, xs[buf], acc, lane);
     }
   }
 }
 
-template <int R, int U, int W, typename Layout>
-__device__ __forceinline__ void lds_stage_compute(const LdsStage<R, U, W>& st,
-                                                  const uint4 (&xs)[U][4][kWave], float (&acc)[R],
-                                                  int lane) {
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    h2_t xp[4][4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint4 pv = xs[u][j][lane];
-      xp[j][0] = as_h2(pv.x);
-      xp[j][1] = as_h2(pv.y);
-      xp[j][2] = as_h2(pv.z);
-      xp[j][3] = as_h2(pv.w);
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const uint32_t words[4] = {st.w[u][r].x, st.w[u][r].y, st.w[u][r].z, st.w[u][r].w};
-      float part = 0.f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        h2_t q[4];
-        Layout::unpack(words[j], q);
-        part = __builtin_amdgcn_fdot2(q[0], xp[j][0], part, false);
-        part = __builtin_amdgcn_fdot2(q[1], xp[j][1], part, false);
-        part = __builtin_amdgcn_fdot2(q[2], xp[j][2], part, false);
-        part = __builtin_amdgcn_fdot2(q[3], xp[j][3], part, false);
-      }
-      acc[r] = __builtin_fmaf(part, h2f((uint16_t)st.s[u][r]), acc[r]);
-    }
-  }
-}
-
-template <int R, int U, int W, bool kPrefetch, typename Layout = LayoutLogical,
+template <int R, int U, int W, int NB, bool kPrefetch, typename Layout = LayoutLogical,
           int kStamp = Layout::kStamp>
 __global__ __launch_bounds__(W * kWave) void gemv_v5_lds(const uint4* __restrict__ packed,
                                                          const uint16_t* __restrict__ scales,
                                                          const uint4* __restrict__ x4,
-                                                         uint16_t* __restrict__ y, int M, int K) {
+                                                         uint16_t* __restrict__ y, int M, int K,
+                                                         int B) {
   write_stamp(kStamp);
-  __shared__ uint4 xs[2][U][4][kWave];
+  __shared__ LdsActs<U, W, NB> xs;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wg = xcd_contiguous_block(blockIdx.x, (M + W * R - 1) / (W * R));
   const int row0 = (wg * W + wave) * R;
   const bool active = row0 < M;  // wave-uniform
+  const int b0 = blockIdx.y * NB;
   const int nck = K >> 5;
   const int G = K >> 7;
   // An inactive wave gets empty weight and scale descriptors: all its
@@ -486,47 +444,19 @@ __global__ __launch_bounds__(W * kWave) void gemv_v5_lds(const uint4* __restrict
   const int rbase = active ? row0 : 0;
   const auto rw = buffer_rsrc(packed + (size_t)rbase * nck, (uint32_t)(rows * (K / 2)));
   const auto rs = buffer_rsrc(scales + (size_t)rbase * G, (uint32_t)(rows * G * 2));
-  const auto rx = buffer_rsrc(x4, (uint32_t)K * 2);
+  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
 
-  float acc[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.f;
-  constexpr int kStep = U * kWave;
-  if constexpr (kPrefetch) {
-    LdsStage<R, U, W> sa, sb;
-    lds_stage_load(sa, rw, rs, rx, 0, nck, G, tid, lane);
-    for (int c0 = 0;;) {
-      lds_stage_publish<R, U, W, Layout>(sa, xs[0], tid);
-      __syncthreads();
-      lds_stage_load(sb, rw, rs, rx, c0 + kStep, nck, G, tid, lane);
-      __builtin_amdgcn_sched_barrier(0);
-      lds_stage_compute<R, U, W, Layout>(sa, xs[0], acc, lane);
-      c0 += kStep;
-      if (c0 >= nck) break;
-      lds_stage_publish<R, U, W, Layout>(sb, xs[1], tid);
-      __syncthreads();
-      lds_stage_load(sa, rw, rs, rx, c0 + kStep, nck, G, tid, lane);
-      __builtin_amdgcn_sched_barrier(0);
-      lds_stage_compute<R, U, W, Layout>(sb, xs[1], acc, lane);
-      c0 += kStep;
-      if (c0 >= nck) break;
-    }
-  } else {
-    LdsStage<R, U, W> st;
-    int buf = 0;
-    for (int c0 = 0; c0 < nck; c0 += kStep, buf ^= 1) {
-      lds_stage_load(st, rw, rs, rx, c0, nck, G, tid, lane);
-      lds_stage_publish<R, U, W, Layout>(st, xs[buf], tid);
-      __syncthreads();
-      lds_stage_compute<R, U, W, Layout>(st, xs[buf], acc, lane);
-    }
-  }
+  float acc[NB][R];
+  lds_stream<R, U, W, NB, kPrefetch, Layout, R>(xs, acc, rw, rs, rw, rs, rx, nck, G, K, b0, B, tid,
+                                                lane);
   if (!active) return;  // after the last barrier
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const float t = wave_sum(acc[r]);
-    if (lane == 63 && row0 + r < M) y[row0 + r] = f2h(t);
-  }
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float t = wave_sum(acc[b][r]);
+      if (lane == 63 && row0 + r < M && b0 + b < B) y[(size_t)(b0 + b) * M + row0 + r] = f2h(t);
+    }
 }
 
 // ---------------------------------------------------------------------------

@@ -17,7 +17,8 @@
 // SiLU*mul epilogue costs no extra launch or round trip of g and u.
 //
 // Mapping: the v5 streaming kernel with 2R rows per wave, rows 0..R-1 of the
-// stage taken from Wg and rows R..2R-1 from Wu at the same row indices.
+// stage taken from Wg and rows R..2R-1 from Wu at the same row indices, so
+// each activation stage in LDS serves both matrices.
 #pragma once
 
 #include "dk_kernels.hpp"
@@ -28,46 +29,36 @@ constexpr int kStampGateUp = 20;
 
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + expf(-v)); }
 
-template <int R, int U, int NB>
-__global__ __launch_bounds__(kStreamWaves * 64) void gate_up_silu(const uint4* __restrict__ gate,
-                                                    const uint16_t* __restrict__ gate_scales,
-                                                    const uint4* __restrict__ up,
-                                                    const uint16_t* __restrict__ up_scales,
-                                                    const uint4* __restrict__ x4, int I, int H,
-                                                    int B, uint16_t* __restrict__ h) {
-  // h is the last argument: with 15 argument dwords not all fit the preload
-  // registers, and h is only needed after the sums.
+// The stage loop of gemv_v5_lds with NB batch rows per stage (grid.y covers
+// the batch).
+template <int R, int U, int W, int NB, bool kPrefetch>
+__global__ __launch_bounds__(W * kWave) void gate_up_silu_lds(
+    const uint4* __restrict__ gate, const uint16_t* __restrict__ gate_scales,
+    const uint4* __restrict__ up, const uint16_t* __restrict__ up_scales,
+    const uint4* __restrict__ x4, int I, int H, int B, uint16_t* __restrict__ h) {
   write_stamp(kStampGateUp);
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // The grid size follows from I (it is the launch's), so no hidden argument
-  // is read before the first load.
-  const int wg = xcd_contiguous_block(blockIdx.x, (I + kStreamWaves * R - 1) / (kStreamWaves * R));
-  const int row0 = (wg * kStreamWaves + wave) * R;
-  if (row0 >= I) return;  // wave-uniform; no barriers in this kernel
-  const int b0 = blockIdx.y * NB;
+  __shared__ LdsActs<U, W, NB> xs;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wg = xcd_contiguous_block(blockIdx.x, (I + W * R - 1) / (W * R));
+  const int row0 = (wg * W + wave) * R;
+  const bool active = row0 < I;  // wave-uniform; inactive waves still meet every barrier
   const int nck = H >> 5;
   const int G = H >> 7;
-  const int rows = min(R, I - row0);
-  const auto rwg = buffer_rsrc(gate + (size_t)row0 * nck, (uint32_t)(rows * (H / 2)));
-  const auto rsg = buffer_rsrc(gate_scales + (size_t)row0 * G, (uint32_t)(rows * G * 2));
-  const auto rwu = buffer_rsrc(up + (size_t)row0 * nck, (uint32_t)(rows * (H / 2)));
-  const auto rsu = buffer_rsrc(up_scales + (size_t)row0 * G, (uint32_t)(rows * G * 2));
+  const int rows = active ? min(R, I - row0) : 0;
+  const int rbase = active ? row0 : 0;
+  const auto rwg = buffer_rsrc(gate + (size_t)rbase * nck, (uint32_t)(rows * (H / 2)));
+  const auto rsg = buffer_rsrc(gate_scales + (size_t)rbase * G, (uint32_t)(rows * G * 2));
+  const auto rwu = buffer_rsrc(up + (size_t)rbase * nck, (uint32_t)(rows * (H / 2)));
+  const auto rsu = buffer_rsrc(up_scales + (size_t)rbase * G, (uint32_t)(rows * G * 2));
   const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * H * 2));
+  const int b0 = blockIdx.y * NB;
 
   float acc[NB][2 * R];
-#pragma unroll
-  for (int b = 0; b < NB; ++b)
-#pragma unroll
-    for (int r = 0; r < 2 * R; ++r) acc[b][r] = 0.f;
-
-  constexpr int kStep = U * kWave;
-  V5Stage<2 * R, U, NB> st;
-  for (int c0 = 0; c0 < nck; c0 += kStep) {
-    v5_load<2 * R, U, NB, R>(st, rwg, rsg, rx, c0, nck, G, H, b0, B, lane, rwu, rsu);
-    v5_compute(st, acc);
-  }
-
+  lds_stream<2 * R, U, W, NB, kPrefetch, LayoutLogical, R>(xs, acc, rwg, rsg, rwu, rsu, rx, nck, G,
+                                                            H, b0, B, tid, lane);
+  if (!active) return;  // after the last barrier
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
