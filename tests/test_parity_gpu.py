@@ -131,27 +131,29 @@ def test_batch_sweep_c3(batch):
 
 
 def test_reuse_small_batches_run_the_streaming_kernel():
-    # One batch row, or two with K <= 4096: the reuse path runs the streaming
-    # kernel with every batch row per tile (stamp 15), so its output is the
-    # v5 output bit for bit. Two rows with longer K take the MFMA tile kernel.
+    # One or two batch rows, or up to four with M >= 8192: the reuse path runs
+    # the streaming kernel with every batch row in each stage (stamp 15), so
+    # its output is the v5 output bit for bit. Three rows with M < 8192 take
+    # the MFMA tile kernel, which still meets the oracle's bound.
     from decode_kernel import _cuda
 
-    for (m, k, b) in [(4096, 4096, 1), (4096, 4096, 2), (11008, 4096, 2), (300, 8192, 1)]:
+    for (m, k, b) in [(4096, 4096, 1), (4096, 4096, 2), (11008, 4096, 2), (300, 8192, 1),
+                      (512, 8192, 2), (8192, 4096, 3), (9000, 8192, 4)]:
         w, x = oracle.make_case(m, k, b, seed=m + k + b)
         _, _, pd, sd, xd = _upload(w, x)
         y_reuse = _gemv(pd, sd, xd, version=5, reuse_weights=True)
         assert int(_cuda.last_kernel_stamp()) == 15
         y_v5 = _gemv(pd, sd, xd, version=5)
         assert torch.equal(y_reuse, y_v5), (m, k, b)
-    w, x = oracle.make_case(512, 8192, 2, seed=5)
+    w, x = oracle.make_case(512, 8192, 3, seed=5)
     packed, scales, pd, sd, xd = _upload(w, x)
     y = _gemv(pd, sd, xd, reuse_weights=True)
     assert int(_cuda.last_kernel_stamp()) == 15
-    _check_against_oracle(y, oracle.linear_f64(x, packed, scales), "reuse 512x8192 B=2")
+    _check_against_oracle(y, oracle.linear_f64(x, packed, scales), "reuse 512x8192 B=3")
 
 
 @pytest.mark.parametrize("m,k,b", [(4096, 4096, 3), (4096, 4096, 8), (4096, 11008, 3),
-                                   (8192, 28672, 3), (11008, 4096, 16)])
+                                   (8192, 28672, 8), (11008, 4096, 16)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
     # The MFMA tile shapes (direct 8x2, direct 8x1, staged 16, staged 8): a
     # one-hot batch row selects single scaled weights bit for bit, scaling x
@@ -217,6 +219,47 @@ def test_edge_shapes_all_paths(m, k, batch):
         assert y.shape == (batch, m)
         err = oracle.max_abs_err(y.float().cpu().numpy(), y_ref)
         assert err < MAX_ABS, (label, m, k, batch, err)
+
+
+# One shape per kernel the streaming path can choose (rows per wave, chunks
+# per stage, waves per workgroup, prefetch, batch rows per stage), each with M
+# not a multiple of the workgroup's rows so the last workgroup has idle waves:
+#   K <= 2048                      -> R1 U1 W16 prefetch
+#   M > 8192, K <= 8192            -> R2 U2 W4
+#   M > 8192, K > 8192             -> R2 U1 W8
+#   M <= 4096, K > 8192            -> R1 U2 W16 prefetch
+#   4096 < M <= 8192, K >= 8192    -> R2 U1 W16 prefetch
+#   otherwise                      -> R1 U2 W8 prefetch
+# and batches of 2, 3, 4 and 6 rows (tiles of 2, 3 or 4 rows per stage, a
+# partial tile at 6) on both sides of M = 4096.
+DISPATCH_SHAPES = [(5000, 1920), (9001, 4224), (8197, 8320), (3000, 8320), (6001, 8320),
+                   (2500, 4224)]
+
+
+@pytest.mark.parametrize("m,k", DISPATCH_SHAPES)
+def test_every_dispatch_class(m, k):
+    from decode_kernel import _cuda, gemv_paired, repack_paired
+
+    w, _ = oracle.make_case(m, k, 1, seed=m + k, w_std=0.05)
+    packed, scales = oracle.quantize_and_pack(w)
+    pd, sd = torch.from_numpy(packed).cuda(), torch.from_numpy(scales).cuda()
+    paired = repack_paired(pd)
+    rng = np.random.Generator(np.random.PCG64(k))
+    for b in (1, 2, 3, 4, 6):
+        x = rng.standard_normal((b, k), dtype=np.float32).astype(np.float16)
+        xd = torch.from_numpy(x).cuda()
+        y_ref = oracle.linear_f64(x, packed, scales)
+        y = _gemv(pd, sd, xd, version=5)
+        assert int(_cuda.last_kernel_stamp()) == 5
+        _check_against_oracle(y, y_ref, f"v5 {m}x{k} B={b}")
+        yp = gemv_paired(paired, sd, xd)
+        _check_against_oracle(yp, y_ref, f"paired {m}x{k} B={b}")
+        yr = _gemv(pd, sd, xd, reuse_weights=True)
+        assert int(_cuda.last_kernel_stamp()) == 15
+        _check_against_oracle(yr, y_ref, f"reuse {m}x{k} B={b}")
+        # Batch rows are independent of their position in the batch: the
+        # reversed batch gives the reversed outputs bit for bit.
+        assert torch.equal(_gemv(pd, sd, xd.flip(0).contiguous(), version=5), y.flip(0))
 
 
 def test_empty_dimensions():
