@@ -204,7 +204,7 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, int off
 // U chunks per lane per stage. A stage's loads are the activations, then
 // the scales, then the weights with the non-temporal hint (read-once data).
 // The activations of a stage (NB batch rows x U * 4 KiB) are loaded once per
-// workgroup of W waves, one or two 16-byte loads per lane, paired once for
+// workgroup of W waves, one to four 16-byte loads per lane, paired once for
 // the layout, and read by every wave from LDS. Loading them per wave instead
 // (an earlier form of this kernel) re-reads twice the weight bytes from L2
 // at two rows per wave and pairs them in every wave; that cost 4-21% at the
@@ -236,13 +236,13 @@ struct LdsStage {
 // One stage's activations in LDS: slot ((b * U + u) * 4 + j) * 64 + l holds
 // the pairs of bytes [16j, 16j + 16) of chunk c0 + 64u + l of batch row
 // b0 + b.
-template <int U, int W, int NB>
+template <int U, int NB>
 struct LdsActsT {
   static constexpr int kSlots = NB * U * 4 * kWave;
   using type = uint4[2][kSlots];
 };
-template <int U, int W, int NB>
-using LdsActs = typename LdsActsT<U, W, NB>::type;
+template <int U, int NB>
+using LdsActs = typename LdsActsT<U, NB>::type;
 
 // Rows r < kSplit come from (rw, rs), rows r >= kSplit from (rw2, rs2) as
 // their row r - kSplit (the fused gate/up kernel streams two matrices
@@ -291,7 +291,7 @@ __device__ __forceinline__ void lds_stage_load(LdsStage<R, U, W, NB>& st, __amdg
 // test is uniform per wave, so those waves skip the store.
 template <int R, int U, int W, int NB, typename Layout>
 __device__ __forceinline__ void lds_stage_publish(const LdsStage<R, U, W, NB>& st,
-                                                  uint4 (&xs)[LdsActsT<U, W, NB>::kSlots],
+                                                  uint4 (&xs)[LdsActsT<U, NB>::kSlots],
                                                   int tid) {
   using S = LdsStage<R, U, W, NB>;
 #pragma unroll
@@ -311,7 +311,7 @@ __device__ __forceinline__ void lds_stage_publish(const LdsStage<R, U, W, NB>& s
 
 template <int R, int U, int W, int NB, typename Layout>
 __device__ __forceinline__ void lds_stage_compute(const LdsStage<R, U, W, NB>& st,
-                                                  const uint4 (&xs)[LdsActsT<U, W, NB>::kSlots],
+                                                  const uint4 (&xs)[LdsActsT<U, NB>::kSlots],
                                                   float (&acc)[NB][R], int lane) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -364,7 +364,7 @@ __device__ __forceinline__ void lds_barrier() {
 // The stage loop shared by the GEMV and the fused gate/up kernel: acc[b][r]
 // is row r's fp32 sum for batch row b0 + b over this lane's chunks of K.
 template <int R, int U, int W, int NB, bool kPrefetch, typename Layout, int kSplit>
-__device__ __forceinline__ void lds_stream(LdsActs<U, W, NB>& xs, float (&acc)[NB][R],
+__device__ __forceinline__ void lds_stream(LdsActs<U, NB>& xs, float (&acc)[NB][R],
                                            __amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs,
                                            __amdgpu_buffer_rsrc_t rw2, __amdgpu_buffer_rsrc_t rs2,
                                            __amdgpu_buffer_rsrc_t rx, int nck, int G, int K, int b0,
@@ -428,7 +428,7 @@ __global__ __launch_bounds__(W * kWave) void gemv_v5_lds(const uint4* __restrict
                                                          uint16_t* __restrict__ y, int M, int K,
                                                          int B) {
   write_stamp(kStamp);
-  __shared__ LdsActs<U, W, NB> xs;
+  __shared__ LdsActs<U, NB> xs;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);

@@ -37,7 +37,7 @@ __global__ __launch_bounds__(W * kWave) void gate_up_silu_lds(
     const uint4* __restrict__ up, const uint16_t* __restrict__ up_scales,
     const uint4* __restrict__ x4, int I, int H, int B, uint16_t* __restrict__ h) {
   write_stamp(kStampGateUp);
-  __shared__ LdsActs<U, W, NB> xs;
+  __shared__ LdsActs<U, NB> xs;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
