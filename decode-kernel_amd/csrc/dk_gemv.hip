@@ -201,19 +201,26 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 
 // Reuse-path shapes (waves per 16-row tile, groups per stage, scales staged
 // in LDS or loaded directly), measured on MI355X back-to-back over cold
-// weights (us per launch):
-//   M = K = 4096:  B = 1: streaming 3.68 (direct KS8 UG2 4.78, KS16 UG2 4.84)
-//                  B = 2: streaming 4.57 (direct KS8 UG2 4.87, KS16 UG2 5.02)
-//                  B = 3: direct KS8 UG2 4.99 (KS16 UG2 5.22; streaming 5.41)
-//                  B = 4: direct KS8 UG2 5.19 (KS16 UG2 5.43; streaming 5.75)
+// weights (us per launch; "streaming" is the v5 kernel with every batch row
+// in each stage):
+//   M = K = 4096:  B = 1: streaming 3.55 (direct KS8 UG2 4.78, KS16 UG2 4.84)
+//                  B = 2: streaming 3.93 (direct KS8 UG2 4.87, KS16 UG2 5.02)
+//                  B = 3: streaming 4.69 (direct KS8 UG2 5.00)
+//                  B = 4: streaming 5.19 (direct KS8 UG2 5.19, KS16 UG2 5.43)
+//                  B = 5: direct KS8 UG1 5.46 (streaming 8.52)
 //                  B = 8: direct KS8 UG1 5.71 (KS8 UG2 5.70, KS16 UG2 5.91)
 //                  B = 16: direct KS8 UG1 6.99 (KS8 UG2 7.25, KS16 UG2 7.09)
-//   M = 11008, K = 4096: B = 1: streaming 6.33 (direct KS8 UG1 9.40)
-//                        B = 2: streaming 8.94 (direct KS8 UG1 9.58)
+//   M = 2048, K = 4096: B = 4: streaming 4.31 (direct 5.00)
+//   M = 4096, K = 8192: B = 3: streaming 7.53 (staged KS16 8.00); B = 4: 8.32 (8.40)
+//   M = 4096, K = 11008: B = 3: staged KS16 9.66 (streaming 9.90); B = 4: 10.36 (11.12)
+//   M = 4096, K = 28672: B = 4: staged KS16 21.74 (streaming 23.00)
+//   M = 11008, K = 4096: B = 1: streaming 5.75 (direct KS8 UG1 9.40)
+//                        B = 2: streaming 7.08 (direct KS8 UG1 9.58)
 //                        B = 16: direct KS8 17.07, staged KS8 17.47
-//   M = 28672, K = 8192, B = 1: streaming 22.7 (staged KS8 36.0, direct KS8 38.3)
-//   M = 8192, K = 28672: B = 1: streaming 21.7 (staged KS8 34.0, direct 40.2)
-//                        B = 2: staged KS8 34.9 (streaming 38.3)
+//   M = 28672, K = 8192: B = 1: streaming 20.4 (staged KS8 36.0, direct KS8 38.3)
+//                        B = 4: streaming 34.4 (staged KS8 39.4)
+//   M = 8192, K = 28672: B = 1: streaming 19.6 (staged KS8 34.0, direct 40.2)
+//                        B = 2: streaming 25.5 (staged KS8 34.9)
 //                        B = 16: staged KS8 70.4 (direct 73.1)
 // Staged scales win once rows are long (the LDS copy is amortised over many
 // groups; direct scale loads add four loads per group); with 512 or more
@@ -221,7 +228,7 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 enum class ReuseShape { kStream, kDirect8x2, kDirect8x1, kStaged16, kStaged8 };
 
 ReuseShape reuse_shape(int M, int K, int B) {
-  if (B <= 2 || (B <= 4 && M >= 8192)) return ReuseShape::kStream;
+  if (B <= 2 || (B <= 4 && (M >= 8192 || K <= 8192))) return ReuseShape::kStream;
   const int tiles = (M + 15) / 16;
   // Rows too long for the staged copy in LDS take the direct path too.
   const bool fits = dk::reuse_lds_bytes_for(16, K, true) <= (size_t)lds_limit_bytes();
