@@ -126,33 +126,71 @@ int launch_lds(const Launch& L, const uint4* p, const uint16_t* s, const uint4* 
 }
 
 // Batches: the same LDS kernel with NB batch rows per stage (grid.y covers
-// the batch in tiles of NB rows), us per launch:
-//   M = K = 4096:        B = 2: R1 U2 W8 NB2 prefetch 3.93 (registers 4.55)
-//                        B = 3: R1 U1 W8 NB3 prefetch 4.66 (registers 5.63)
-//                        B = 4: R2 U1 W4 NB4 prefetch 5.27 (registers 5.77)
-//                        B = 8: R2 U1 W8 NB4 7.57 (registers 9.50)
-//   M = 11008, K = 4096: B = 2: R2 U1 W8 NB2 prefetch 7.10 (registers 8.91)
-//                        B = 4: R2 U1 W8 NB4 9.68 (registers 12.66)
-//   M = 4096, K = 11008: B = 2: R1 U2 W8 NB2 prefetch 7.46 (registers 9.04)
-//                        B = 4: R2 U1 W4 NB4 prefetch 11.11 (registers 13.34)
-//   M = 28672, K = 8192: B = 2: R2 U1 W8 NB2 prefetch 26.4 (registers 37.5)
-//                        B = 4: R2 U1 W8 NB4 36.1 (registers 54.7)
-//   M = 8192, K = 28672: B = 2: R2 U1 W8 NB2 prefetch 25.5 (registers 38.2)
-//                        B = 4: R2 U1 W8 NB4 38.9 (registers 54.7)
-// (registers: activations per wave, R2 U1 NB2 for B = 2, R4 U1 NB2 tiles
-// otherwise.)
+// the batch in tiles of NB rows). Timed as above, us per launch, the choice
+// below against the previous rule (NB = 2 tiles for B = 2, NB = 4 tiles
+// otherwise, one shape per M range):
+//                        B = 2           B = 3           B = 4
+//   M = 512, K = 8320:   4.38 (5.12)     4.40 (5.79)     4.41 (7.39)
+//   M = 1024, K = 11008: 4.58 (5.29)     5.22 (5.95)     5.31 (7.50)
+//   M = 2048, K = 16384: 7.12 (7.11)     7.86 (7.89)     8.64 (10.11)
+//   M = K = 4096:        3.94 (3.93)     4.45 (4.71)     4.95 (5.19)
+//   M = 4096, K = 11008: 7.49 (7.42)     8.62 (9.93)     10.00 (11.12)
+//   M = 4096, K = 28672: 14.64 (15.47)   17.61 (19.09)   20.61 (23.75)
+//   M = 6144, K = 8192:  8.23 (8.69)     10.01 (12.05)   11.65 (12.18)
+//   M = 11008, K = 4096: 6.80 (7.20)     8.51 (9.23)     9.44 (9.52)
+//   M = 8192, K = 28672: 24.30 (25.75)   30.00 (36.80)   34.20 (37.99)
+//   M = 28672, K = 8192: 25.65 (26.32)   32.26 (34.13)   35.62 (35.47)
+// B = 5 and 6 run two tiles of three rows (the previous rule's four-row
+// tiles left three rows of the second empty at B = 5): M = 1024, K = 11008
+// 5.97 (7.52); M = 4096, K = 14336 14.52 (26.59). Over 18 shapes (M from 512
+// to 28672, K from 3584 to 28672) the choice is 2-3% from the best of 72
+// variants (R, U, W, prefetch, NB) per batch size on average and 8-17% at
+// worst. What decides is the number of workgroups: one per CU (256) with as
+// many rows and batch rows in each as that allows shares every activation
+// load most widely, so small M takes narrow workgroups and splits the batch
+// into more tiles (NB = 2 at B = 4 for M <= 1024: 4.41 against 7.39 us at
+// M = 512), and large M takes wide ones with every batch row in one tile.
+#define DK_BATCH(R, U, W, PF, NB) \
+  launch_lds_t<R, U, W, PF, Layout, kStamp, NB>(L, p, s, x, y, M, K, B)
 template <typename Layout = dk::LayoutLogical, int kStamp = Layout::kStamp>
 int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y, int M,
               int K, int B) {
   if (B == 1) return launch_lds<Layout, kStamp>(L, p, s, x, y, M, K);
-  if (M <= 4096) {
-    if (B == 2) return launch_lds_t<1, 2, 8, true, Layout, kStamp, 2>(L, p, s, x, y, M, K, B);
-    if (B == 3) return launch_lds_t<1, 1, 8, true, Layout, kStamp, 3>(L, p, s, x, y, M, K, B);
-    return launch_lds_t<2, 1, 4, true, Layout, kStamp, 4>(L, p, s, x, y, M, K, B);
+  const bool long_rows = K > 8192;
+  if (B == 2) {
+    if (M <= 1024) return DK_BATCH(1, 2, 4, true, 2);
+    if (M <= 2048 || (M <= 4096 && K <= 12288)) return DK_BATCH(1, 2, 8, true, 2);
+    if (M <= 4096) return DK_BATCH(2, 2, 8, true, 2);
+    if (M > 8192) return DK_BATCH(2, 2, 8, false, 2);
+    return K <= 4096 ? DK_BATCH(2, 2, 4, true, 2) : DK_BATCH(2, 1, 16, false, 2);
   }
-  if (B == 2) return launch_lds_t<2, 1, 8, true, Layout, kStamp, 2>(L, p, s, x, y, M, K, B);
-  return launch_lds_t<2, 1, 8, false, Layout, kStamp, 4>(L, p, s, x, y, M, K, B);
+  if (B == 3) {
+    if (M <= 512) return DK_BATCH(1, 2, 4, true, 2);
+    if (M <= 1024) return DK_BATCH(1, 2, 4, true, 3);
+    if (M <= 2048) return DK_BATCH(1, 2, 8, true, 3);
+    if (M <= 4096) return long_rows ? DK_BATCH(1, 2, 16, true, 3) : DK_BATCH(1, 2, 8, true, 3);
+    return DK_BATCH(2, 2, 8, false, 3);
+  }
+  if (B == 4) {
+    if (M <= 512) return DK_BATCH(1, 2, 4, true, 2);
+    if (M <= 1024) return DK_BATCH(1, 2, 8, true, 2);
+    if (M <= 2048) return DK_BATCH(2, 2, 8, true, 2);
+    if (M <= 4096) return long_rows ? DK_BATCH(2, 2, 8, true, 4) : DK_BATCH(1, 2, 8, true, 4);
+    return M > 8192 ? DK_BATCH(2, 1, 8, false, 4) : DK_BATCH(2, 2, 8, false, 4);
+  }
+  if (B <= 6) {
+    if (M <= 512) return DK_BATCH(1, 2, 4, true, 3);
+    if (M <= 1024) return DK_BATCH(1, 2, 8, true, 3);
+    if (M <= 2048) return DK_BATCH(2, 2, 8, true, 3);
+    if (M <= 4096 || K > 4096) return DK_BATCH(2, 1, 16, true, 3);
+    return DK_BATCH(2, 2, 8, false, 3);
+  }
+  if (M <= 1024) return DK_BATCH(1, 2, 8, true, 2);
+  if (M <= 2048) return DK_BATCH(2, 2, 8, true, 4);
+  if (M <= 4096) return DK_BATCH(2, 1, 16, true, 4);
+  return M > 8192 ? DK_BATCH(2, 1, 8, false, 4) : DK_BATCH(2, 2, 8, false, 4);
 }
+#undef DK_BATCH
 
 // Fused gate/up, R rows of each matrix per wave, on the LDS stage loop (U
 // chunks per stage, W waves per workgroup, next stage prefetched or not, NB
@@ -199,50 +237,40 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
   return launch_gate_up_lds_t<1, 1, 8, false, 4>(L, g, gs, u, us, x, h, I, H, B);
 }
 
-// Reuse-path shapes (waves per 16-row tile, groups per stage, scales staged
-// in LDS or loaded directly), measured on MI355X back-to-back over cold
-// weights (us per launch; "streaming" is the v5 kernel with every batch row
-// in each stage):
-//   M = K = 4096:  B = 1: streaming 3.55 (direct KS8 UG2 4.78, KS16 UG2 4.84)
-//                  B = 2: streaming 3.93 (direct KS8 UG2 4.87, KS16 UG2 5.02)
-//                  B = 3: streaming 4.69 (direct KS8 UG2 5.00)
-//                  B = 4: streaming 5.19 (direct KS8 UG2 5.19, KS16 UG2 5.43)
-//                  B = 5: direct KS8 UG1 5.46 (streaming 8.52)
-//                  B = 8: direct KS8 UG1 5.71 (KS8 UG2 5.70, KS16 UG2 5.91)
-//                  B = 16: direct KS8 UG1 6.99 (KS8 UG2 7.25, KS16 UG2 7.09)
-//   M = 2048, K = 4096: B = 4: streaming 4.31 (direct 5.00)
-//   M = 4096, K = 8192: B = 3: streaming 7.53 (staged KS16 8.00); B = 4: 8.32 (8.40)
-//   M = 4096, K = 11008: B = 3: staged KS16 9.66 (streaming 9.90); B = 4: 10.36 (11.12)
-//   M = 4096, K = 28672: B = 4: staged KS16 21.74 (streaming 23.00)
-//   M = 11008, K = 4096: B = 1: streaming 5.75 (direct KS8 UG1 9.40)
-//                        B = 2: streaming 7.08 (direct KS8 UG1 9.58)
-//                        B = 16: direct KS8 17.07, staged KS8 17.47
-//   M = 28672, K = 8192: B = 1: streaming 20.4 (staged KS8 36.0, direct KS8 38.3)
-//                        B = 4: streaming 34.4 (staged KS8 39.4)
-//   M = 8192, K = 28672: B = 1: streaming 19.6 (staged KS8 34.0, direct 40.2)
-//                        B = 2: streaming 25.5 (staged KS8 34.9)
-//                        B = 16: staged KS8 70.4 (direct 73.1)
-// Staged scales win once rows are long (the LDS copy is amortised over many
-// groups; direct scale loads add four loads per group); with 512 or more
-// tiles (M >= 8192) 8 waves per tile with one group per stage are enough.
-enum class ReuseShape { kStream, kDirect8x2, kDirect8x1, kStaged16, kStaged8 };
+// Reuse path: the MFMA tile kernel (8 waves per 16-row tile, one group per
+// iteration, scales staged in LDS or loaded directly) against the streaming
+// kernel with its batch tiles, measured on MI355X back-to-back over cold
+// weights (us per launch, chosen first):
+//   M = K = 4096:        B = 4: streaming 4.96 (tiles 5.19)
+//                        B = 5: tiles 5.48 (streaming 6.20)
+//                        B = 8: tiles 5.74 (streaming 7.51); B = 16: 7.00 (13.49)
+//   M = 4096, K = 11008: B = 4: streaming 10.00 (tiles 10.36)
+//                        B = 5: tiles 11.35 (streaming 12.92)
+//   M = 8192, K = 28672: B = 4: streaming 35.5; B = 5: tiles 42.0 (streaming 57.5)
+//   M = 3072, K = 12288: B = 5: tiles 12.00 (streaming 12.70)
+//   M = 2048, K = 16384: B = 8: streaming 12.10 (tiles 15.64)
+//                        B = 12: tiles 18.14 (streaming 22.54)
+//   M = 1024, K = 11008: B = 8: streaming 6.82 (tiles 11.67)
+//                        B = 16: streaming 12.15 (tiles 15.43)
+//   M = 512, K = 8320:   B = 16: streaming 6.69 (tiles 11.61)
+// The tiles need B >= 5 to pay for 16 MFMA batch columns, and M / 16 tiles
+// leave most CUs idle at small M, where the streaming kernel splits the batch
+// over more workgroups instead. Staged scales win once rows are long (the
+// LDS copy is amortised over many groups; direct scale loads add four loads
+// per group).
+enum class ReuseShape { kStream, kDirect, kStaged };
 
 ReuseShape reuse_shape(int M, int K, int B) {
-  if (B <= 2 || (B <= 4 && (M >= 8192 || K <= 8192))) return ReuseShape::kStream;
-  const int tiles = (M + 15) / 16;
+  if (B <= 4 || (B <= 8 && M <= 2048) || (B <= 16 && M <= 1024)) return ReuseShape::kStream;
   // Rows too long for the staged copy in LDS take the direct path too.
-  const bool fits = dk::reuse_lds_bytes_for(16, K, true) <= (size_t)lds_limit_bytes();
-  if (K <= 4096 || !fits)
-    return (B <= 4 && tiles < 512) ? ReuseShape::kDirect8x2 : ReuseShape::kDirect8x1;
-  return (tiles >= 512 || B > 4) ? ReuseShape::kStaged8 : ReuseShape::kStaged16;
+  const bool fits = dk::reuse_lds_bytes_for(8, K, true) <= (size_t)lds_limit_bytes();
+  return (K <= 4096 || !fits) ? ReuseShape::kDirect : ReuseShape::kStaged;
 }
 
 size_t reuse_lds_bytes(int M, int K, int B) {
   switch (reuse_shape(M, K, B)) {
     case ReuseShape::kStream: return 0;
-    case ReuseShape::kDirect8x2:
-    case ReuseShape::kDirect8x1: return dk::reuse_lds_bytes_for(8, K, false);
-    case ReuseShape::kStaged16: return dk::reuse_lds_bytes_for(16, K, true);
+    case ReuseShape::kDirect: return dk::reuse_lds_bytes_for(8, K, false);
     default: return dk::reuse_lds_bytes_for(8, K, true);
   }
 }
@@ -290,14 +318,8 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
     switch (reuse_shape(M, K, B)) {
       case ReuseShape::kStream:
         return launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B);
-      case ReuseShape::kDirect8x2:
-        return L("reuse launch", dk::gemv_reuse<8, 2, false>, grid, dim3(8 * 64), lds, p4, scales,
-                 x4, y, M, K, B);
-      case ReuseShape::kDirect8x1:
+      case ReuseShape::kDirect:
         return L("reuse launch", dk::gemv_reuse<8, 1, false>, grid, dim3(8 * 64), lds, p4, scales,
-                 x4, y, M, K, B);
-      case ReuseShape::kStaged16:
-        return L("reuse launch", dk::gemv_reuse<16, 1, true>, grid, dim3(16 * 64), lds, p4, scales,
                  x4, y, M, K, B);
       default:
         return L("reuse launch", dk::gemv_reuse<8, 1, true>, grid, dim3(8 * 64), lds, p4, scales,

@@ -574,10 +574,11 @@ __global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
 //   * direct: no staging round trip before the first weight load; each lane
 //     loads the four scales of its D rows with the activations and weights,
 //     UG groups per stage (best for K <= 4096: 3-6% at M = K = 4096).
-// For one or two batch rows the reuse path runs the streaming kernel above
-// with NB = B instead (each decoded weight still serves every batch row):
-// 16 batch columns of MFMA operands cost more activation traffic than they
-// save there.
+// For up to four batch rows, and up to eight when M <= 2048, the reuse path
+// runs the streaming kernel above instead (each decoded weight still serves
+// every batch row of its tile): 16 MFMA batch columns cost more activation
+// traffic than they save at small batches, and M / 16 tiles leave most CUs
+// idle at small M.
 // ---------------------------------------------------------------------------
 constexpr int kReuseBatch = 16;
 

@@ -131,39 +131,39 @@ def test_batch_sweep_c3(batch):
 
 
 def test_reuse_small_batches_run_the_streaming_kernel():
-    # One or two batch rows, or up to four with M >= 8192 or K <= 8192: the
-    # reuse path runs the streaming kernel with every batch row in each stage
-    # (stamp 15), so its output is the v5 output bit for bit. Three rows with
-    # M < 8192 and K > 8192 take the MFMA tile kernel, which still meets the
-    # oracle's bound.
+    # Up to four batch rows, up to eight with M <= 2048 and up to 16 with
+    # M <= 1024: the reuse path runs the streaming kernel with its batch tiles
+    # (stamp 15), so its output is the v5 output bit for bit. Five rows with
+    # M > 2048 take the MFMA tile kernel, which still meets the oracle's bound.
     from decode_kernel import _cuda
 
     for (m, k, b) in [(4096, 4096, 1), (4096, 4096, 2), (11008, 4096, 2), (300, 8192, 1),
                       (512, 8192, 2), (8192, 4096, 3), (9000, 8192, 4), (4096, 4096, 3),
-                      (2000, 8192, 4)]:
+                      (2000, 8192, 4), (512, 8320, 3), (4096, 11008, 4), (1024, 11008, 6),
+                      (2048, 4224, 8), (40, 197632, 3), (1000, 4224, 16)]:
         w, x = oracle.make_case(m, k, b, seed=m + k + b)
         _, _, pd, sd, xd = _upload(w, x)
         y_reuse = _gemv(pd, sd, xd, version=5, reuse_weights=True)
         assert int(_cuda.last_kernel_stamp()) == 15
         y_v5 = _gemv(pd, sd, xd, version=5)
         assert torch.equal(y_reuse, y_v5), (m, k, b)
-    w, x = oracle.make_case(512, 8320, 3, seed=5)
+    w, x = oracle.make_case(3000, 8320, 5, seed=5)
     packed, scales, pd, sd, xd = _upload(w, x)
     y = _gemv(pd, sd, xd, reuse_weights=True)
     assert int(_cuda.last_kernel_stamp()) == 15
-    _check_against_oracle(y, oracle.linear_f64(x, packed, scales), "reuse 512x8320 B=3")
+    _check_against_oracle(y, oracle.linear_f64(x, packed, scales), "reuse 3000x8320 B=5")
 
 
-@pytest.mark.parametrize("m,k,b", [(40, 197632, 3), (4096, 4096, 8), (4096, 11008, 3),
-                                   (8192, 28672, 8), (11008, 4096, 16)])
+@pytest.mark.parametrize("m,k,b", [(40, 230400, 9), (4096, 4096, 8), (4096, 11008, 5),
+                                   (8192, 28672, 8), (11008, 4096, 16), (2048, 4096, 12)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
-    # The MFMA tile shapes (direct 8x2: rows too long for the staged scales,
-    # 1544 groups; direct 8x1; staged 16; staged 8): a
+    # The MFMA tile shapes (direct: rows too long for the staged scales, 1800
+    # groups, or K <= 4096; staged scales otherwise): a
     # one-hot batch row selects single scaled weights bit for bit, scaling x
     # by 2 or -1 scales y exactly (2 up to fp16 subnormal rounding), and rows
     # of a batch do not mix.
     # |y| grows as sqrt(K): keep it below ~16 so the fp16 output step stays
-    # inside the absolute gate (at K = 197632 and W ~ N(0, 0.05), |y| reaches
+    # inside the absolute gate (at K ~ 200000 and W ~ N(0, 0.05), |y| reaches
     # 64 and one fp16 step there is 0.06).
     w_std = 0.05 if k <= 28672 else 0.005
     w, x = oracle.make_case(m, k, b, seed=7 + b, w_std=w_std)
@@ -239,8 +239,11 @@ def test_edge_shapes_all_paths(m, k, batch):
 #   otherwise                      -> R1 U2 W8 prefetch
 # and batches of 2, 3, 4 and 6 rows (tiles of 2, 3 or 4 rows per stage, a
 # partial tile at 6) on both sides of M = 4096.
+# Ragged shapes in every M range (<= 512, 1024, 2048, 4096, 8192, above) and
+# K range (<= 2048, 4096, 8192, 12288, above) the streaming dispatch tells
+# apart, run at batches that cover every tile size (NB = 1, 2, 3, 4).
 DISPATCH_SHAPES = [(5000, 1920), (9001, 4224), (8197, 8320), (3000, 8320), (6001, 8320),
-                   (2500, 4224)]
+                   (2500, 4224), (500, 8320), (1000, 4224), (2000, 12416), (4000, 12416)]
 
 
 @pytest.mark.parametrize("m,k", DISPATCH_SHAPES)
@@ -252,7 +255,7 @@ def test_every_dispatch_class(m, k):
     pd, sd = torch.from_numpy(packed).cuda(), torch.from_numpy(scales).cuda()
     paired = repack_paired(pd)
     rng = np.random.Generator(np.random.PCG64(k))
-    for b in (1, 2, 3, 4, 6):
+    for b in (1, 2, 3, 4, 5, 6, 8):
         x = rng.standard_normal((b, k), dtype=np.float32).astype(np.float16)
         xd = torch.from_numpy(x).cuda()
         y_ref = oracle.linear_f64(x, packed, scales)
