@@ -216,26 +216,43 @@ int launch_gate_up_lds_t(const Launch& L, const uint4* g, const uint16_t* gs, co
            gs, u, us, x, I, H, B, h);
 }
 
+// Batches: tiles of two batch rows at B = 2, three at B = 3, 5 and 6, four
+// otherwise, as for the GEMV. Timed as above (us per launch), against the
+// previous rule (NB = 4 tiles from B = 3 on, no separate small-I case):
+//                        B = 2           B = 3           B = 4
+//   I = 1376, H = 4096:  4.09 (5.40)     4.70 (7.82)     5.26 (8.09)
+//   I = 1792, H = 8192:  6.13 (8.15)     7.11 (11.86)    8.30 (12.21)
+//   I = 3584, H = 8192:  8.78 (8.94)     10.65 (12.43)   12.70 (12.75)
+//   I = 11008, H = 4096: 12.04 (12.30)   14.95 (17.25)   17.88 (18.64)
+//   I = 14336, H = 4096: 15.00 (15.61)   17.33 (20.29)   20.45 (21.06)
+//   I = 28672, H = 8192: 47.02 (47.29)   58.23 (66.36)   66.48 (69.62)
+// Within 2.5% of the best of 72 variants (R, U, W, prefetch, NB) at every
+// one of these shapes but I = 1376, B = 4 (8%: two tiles of two rows do
+// better there). Small I takes narrow workgroups (W = 4) so that the grid
+// still covers the chip.
+#define DK_GATE_UP(R, U, W, PF, NB) \
+  launch_gate_up_lds_t<R, U, W, PF, NB>(L, g, gs, u, us, x, h, I, H, B)
 int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const uint4* u,
                    const uint16_t* us, const uint4* x, uint16_t* h, int I, int H, int B) {
-  if (I <= 4096) {
-    if (B == 1) {
-      if (H > 4096) return launch_gate_up_lds_t<1, 1, 16, true>(L, g, gs, u, us, x, h, I, H);
-      return launch_gate_up_lds_t<1, 2, 4, true>(L, g, gs, u, us, x, h, I, H);
-    }
-    if (B == 2) return launch_gate_up_lds_t<1, 1, 16, true, 2>(L, g, gs, u, us, x, h, I, H, B);
-    return launch_gate_up_lds_t<1, 1, 16, true, 4>(L, g, gs, u, us, x, h, I, H, B);
-  }
   if (B == 1) {
-    if (H <= 4096) return launch_gate_up_lds_t<1, 2, 4, false>(L, g, gs, u, us, x, h, I, H);
-    return launch_gate_up_lds_t<1, 2, 8, false>(L, g, gs, u, us, x, h, I, H);
+    if (I <= 4096) return H > 4096 ? DK_GATE_UP(1, 1, 16, true, 1) : DK_GATE_UP(1, 2, 4, true, 1);
+    return H <= 4096 ? DK_GATE_UP(1, 2, 4, false, 1) : DK_GATE_UP(1, 2, 8, false, 1);
   }
   if (B == 2) {
-    if (H <= 4096) return launch_gate_up_lds_t<1, 2, 4, true, 2>(L, g, gs, u, us, x, h, I, H, B);
-    return launch_gate_up_lds_t<2, 1, 4, false, 2>(L, g, gs, u, us, x, h, I, H, B);
+    if (I <= 2048) return DK_GATE_UP(1, 2, 4, true, 2);
+    if (I <= 4096) return DK_GATE_UP(1, 1, 16, true, 2);
+    return H <= 4096 ? DK_GATE_UP(1, 2, 8, false, 2) : DK_GATE_UP(2, 1, 4, false, 2);
   }
-  return launch_gate_up_lds_t<1, 1, 8, false, 4>(L, g, gs, u, us, x, h, I, H, B);
+  if (B == 3 || B == 5 || B == 6) {
+    if (I <= 2048) return DK_GATE_UP(1, 2, 4, true, 3);
+    if (I <= 4096) return DK_GATE_UP(1, 1, 16, true, 3);
+    return DK_GATE_UP(2, 2, 4, false, 3);
+  }
+  if (I <= 2048) return DK_GATE_UP(1, 2, 4, true, 4);
+  if (I <= 4096) return DK_GATE_UP(1, 1, 16, true, 4);
+  return DK_GATE_UP(2, 1, 4, false, 4);
 }
+#undef DK_GATE_UP
 
 // Reuse path: the MFMA tile kernel (8 waves per 16-row tile, one group per
 // iteration, scales staged in LDS or loaded directly) against the streaming

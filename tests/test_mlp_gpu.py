@@ -7,7 +7,8 @@ oracle.linear_f64 of the kernel's own h with the GEMV's bound, and end to end
 against oracle.mlp_decode_f64 with the reference's 1e-2 gate. Shapes: the
 Llama-7B MLP (I = 11008, H = 4096), the per-GPU Llama-70B shard at TP = 8
 (I = 3584, H = 8192), the full Llama-70B MLP (I = 28672, H = 8192, sampled
-rows), small ragged shapes, batches 1-5, and empty dimensions.
+rows), ragged shapes in every dispatch range, batches 1-8, and empty
+dimensions.
 """
 
 from __future__ import annotations
@@ -86,6 +87,29 @@ def test_mlp_step_matches_oracle(i, h, b):
     from decode_kernel import gemv
 
     assert torch.equal(y, gemv(dp, ds, hk))
+
+
+# Ragged shapes in every I range (<= 2048, 4096, above) and H range (<= 4096,
+# above) the gate/up dispatch tells apart.
+GATE_UP_SHAPES = [(1000, 4224), (2000, 8320), (3000, 4224), (3000, 8320), (5000, 4224),
+                  (4500, 8320)]
+
+
+@pytest.mark.parametrize("i,h", GATE_UP_SHAPES)
+def test_gate_up_every_dispatch_class(i, h):
+    # Batches 1-8 cover every tile size (one row, and tiles of 2, 3 and 4
+    # rows, the last one partly empty at B = 5 and 7). Each output row
+    # depends on its own activation row only, so the first b rows of one
+    # 8-row case give the reference for every b.
+    from decode_kernel import _cuda, gate_up_silu
+
+    (gp, gs, up, us, _, _), (ngp, ngs, nup, nus, _, _) = _weights(i, h, seed=i + h)
+    x8 = _x(8, h, seed=i)
+    h_ref = oracle.gate_up_silu_f64(x8.cpu().numpy(), ngp, ngs, nup, nus)
+    for b in (1, 2, 3, 4, 5, 6, 7, 8):
+        hk = gate_up_silu(x8[:b].contiguous(), gp, gs, up, us)
+        assert int(_cuda.last_kernel_stamp()) == 20
+        _check_tight(hk.float().cpu().numpy(), h_ref[:b], f"h {i}x{h} B={b}")
 
 
 def test_llama70b_full_mlp_sampled_rows():
