@@ -104,6 +104,21 @@ struct Launch {
 // when rows are few (few waves per SIMD to hide a stage's latency) and costs
 // occupancy when they are many; 16-wave workgroups share each activation
 // load among more rows when stages are many.
+// Up to 3072 rows (tensor-parallel shards) the grid is the limit: four-wave
+// workgroups, and stages of U = 4 or 6 chunks per lane so that a row of up
+// to 12288 weights is one stage (each wave waits for one round of loads),
+// against the rule for larger M (one row per wave, U = 2 or 1, W = 8 or 16):
+//   M = 512,  K = 8320:  R1 U6 W4 prefetch 3.03 (5.09)
+//   M = 1024, K = 8192:  R1 U4 W4 prefetch 2.82 (3.83)
+//   M = 1280, K = 8192:  R1 U4 W4 prefetch 3.20 (3.92)
+//   M = 2048, K = 11008: R1 U6 W4 prefetch 4.34 (5.37)
+//   M = 3072, K = 8192:  R1 U4 W4 prefetch 4.23 (4.74)
+//   M = 2048, K = 16384: R1 U4 W8 prefetch 5.63 (6.79)
+//   M = 1024, K = 28672: R1 U4 W4 prefetch 6.50 (9.53)
+//   M = 512,  K = 4096:  R1 U2 W4 prefetch 2.28 (2.56)
+// (best of 48 variants, U from 2 to 6, at each but the last two: 2-3% off).
+// At M = 4096 the wide stages lose (M = 4096, K = 11008: R1 U6 W4 7.26
+// against R1 U2 W16 prefetch 6.04).
 template <int R, int U, int W, bool kPrefetch, typename Layout, int kStamp, int NB = 1>
 int launch_lds_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                  int M, int K, int B = 1) {
@@ -116,6 +131,13 @@ template <typename Layout, int kStamp>
 int launch_lds(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                int M, int K) {
   if (K <= 2048) return launch_lds_t<1, 1, 16, true, Layout, kStamp>(L, p, s, x, y, M, K);
+  if (M <= 3072) {
+    if (K <= 4096) return launch_lds_t<1, 2, 4, true, Layout, kStamp>(L, p, s, x, y, M, K);
+    if (K <= 8192) return launch_lds_t<1, 4, 4, true, Layout, kStamp>(L, p, s, x, y, M, K);
+    if (K <= 12288) return launch_lds_t<1, 6, 4, true, Layout, kStamp>(L, p, s, x, y, M, K);
+    if (M <= 1024) return launch_lds_t<1, 4, 4, true, Layout, kStamp>(L, p, s, x, y, M, K);
+    return launch_lds_t<1, 4, 8, true, Layout, kStamp>(L, p, s, x, y, M, K);
+  }
   if (M > 8192) {
     if (K <= 8192) return launch_lds_t<2, 2, 4, false, Layout, kStamp>(L, p, s, x, y, M, K);
     return launch_lds_t<2, 1, 8, false, Layout, kStamp>(L, p, s, x, y, M, K);
@@ -150,6 +172,10 @@ int launch_lds(const Launch& L, const uint4* p, const uint16_t* s, const uint4* 
 // load most widely, so small M takes narrow workgroups and splits the batch
 // into more tiles (NB = 2 at B = 4 for M <= 1024: 4.41 against 7.39 us at
 // M = 512), and large M takes wide ones with every batch row in one tile.
+// Up to 2048 rows of 4097-8192 weights, stages of U = 4 (one per row) in
+// two-row tiles: M = 1024, K = 8192: B = 2 3.19 (3.98), B = 3 3.72 (4.45),
+// B = 4 3.80 (4.56); M = 2048, K = 8192, B = 2: 4.15 (4.91); M = 768,
+// K = 8192, B = 3: 3.61 (4.37); M = 512, K = 8192, B = 4: 3.12 (3.85).
 #define DK_BATCH(R, U, W, PF, NB) \
   launch_lds_t<R, U, W, PF, Layout, kStamp, NB>(L, p, s, x, y, M, K, B)
 template <typename Layout = dk::LayoutLogical, int kStamp = Layout::kStamp>
@@ -157,13 +183,19 @@ int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x
               int K, int B) {
   if (B == 1) return launch_lds<Layout, kStamp>(L, p, s, x, y, M, K);
   const bool long_rows = K > 8192;
+  // Few rows with one-stage rows of up to 8192 weights (U = 4).
+  const bool one_wide_stage = K > 4096 && K <= 8192;
   if (B == 2) {
+    if (one_wide_stage && M <= 1024) return DK_BATCH(1, 4, 4, true, 2);
+    if (one_wide_stage && M <= 2048) return DK_BATCH(2, 4, 4, true, 2);
     if (M <= 1024) return DK_BATCH(1, 2, 4, true, 2);
     if (M <= 2048 || (M <= 4096 && K <= 12288)) return DK_BATCH(1, 2, 8, true, 2);
     if (M <= 4096) return DK_BATCH(2, 2, 8, true, 2);
     if (M > 8192) return DK_BATCH(2, 2, 8, false, 2);
     return K <= 4096 ? DK_BATCH(2, 2, 4, true, 2) : DK_BATCH(2, 1, 16, false, 2);
   }
+  if ((B == 3 || B == 4) && one_wide_stage && M <= 1024)
+    return M <= 512 ? DK_BATCH(1, 4, 4, true, 2) : DK_BATCH(1, 4, 8, true, 2);
   if (B == 3) {
     if (M <= 512) return DK_BATCH(1, 2, 4, true, 2);
     if (M <= 1024) return DK_BATCH(1, 2, 4, true, 3);

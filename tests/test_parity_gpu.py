@@ -239,11 +239,13 @@ def test_edge_shapes_all_paths(m, k, batch):
 #   otherwise                      -> R1 U2 W8 prefetch
 # and batches of 2, 3, 4 and 6 rows (tiles of 2, 3 or 4 rows per stage, a
 # partial tile at 6) on both sides of M = 4096.
-# Ragged shapes in every M range (<= 512, 1024, 2048, 4096, 8192, above) and
-# K range (<= 2048, 4096, 8192, 12288, above) the streaming dispatch tells
-# apart, run at batches that cover every tile size (NB = 1, 2, 3, 4).
+# Ragged shapes in every M range (<= 512, 1024, 2048, 3072, 4096, 8192,
+# above) and K range (<= 2048, 4096, 8192, 12288, above) the streaming
+# dispatch tells apart, run at batches that cover every tile size (NB = 1, 2,
+# 3, 4).
 DISPATCH_SHAPES = [(5000, 1920), (9001, 4224), (8197, 8320), (3000, 8320), (6001, 8320),
-                   (2500, 4224), (500, 8320), (1000, 4224), (2000, 12416), (4000, 12416)]
+                   (2500, 4224), (500, 8320), (1000, 4224), (2000, 12416), (4000, 12416),
+                   (700, 3968), (1500, 6144), (900, 16512), (3072, 2048), (400, 5120)]
 
 
 @pytest.mark.parametrize("m,k", DISPATCH_SHAPES)
