@@ -261,12 +261,17 @@ int launch_gate_up_lds_t(const Launch& L, const uint4* g, const uint16_t* gs, co
 // Within 2.5% of the best of 72 variants (R, U, W, prefetch, NB) at every
 // one of these shapes but I = 1376, B = 4 (8%: two tiles of two rows do
 // better there). Small I takes narrow workgroups (W = 4) so that the grid
-// still covers the chip.
+// still covers the chip. One batch row with I <= 2048 and H of 4097-8192
+// takes one stage of U = 4 per row: I = 1024, H = 8192: 3.72 (6.12);
+// I = 1792: 4.87 (6.40); I = 2048: 5.05 (6.47); at I = 3584 it is no better
+// than R1 U1 W16 (7.73 against 7.51).
 #define DK_GATE_UP(R, U, W, PF, NB) \
   launch_gate_up_lds_t<R, U, W, PF, NB>(L, g, gs, u, us, x, h, I, H, B)
 int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const uint4* u,
                    const uint16_t* us, const uint4* x, uint16_t* h, int I, int H, int B) {
   if (B == 1) {
+    // Few rows of up to 8192 weights: one stage of U = 4 per row.
+    if (I <= 2048 && H > 4096 && H <= 8192) return DK_GATE_UP(1, 4, 4, true, 1);
     if (I <= 4096) return H > 4096 ? DK_GATE_UP(1, 1, 16, true, 1) : DK_GATE_UP(1, 2, 4, true, 1);
     return H <= 4096 ? DK_GATE_UP(1, 2, 4, false, 1) : DK_GATE_UP(1, 2, 8, false, 1);
   }
