@@ -291,10 +291,12 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 }
 #undef DK_GATE_UP
 
-// Reuse path: the MFMA tile kernel (8 waves per 16-row tile, one group per
-// iteration, scales staged in LDS or loaded directly) against the streaming
-// kernel with its batch tiles, measured on MI355X back-to-back over cold
-// weights (us per launch, chosen first):
+// Reuse path: the MFMA tile kernel (8 waves per 16-row tile, blocks of four
+// groups, weights through wave-private LDS) against the streaming kernel
+// with its batch tiles, measured on MI355X back-to-back over cold weights
+// (us per launch, chosen first; the tile figures are from the earlier tile
+// kernel, which loaded the weights straight into the MFMA layout and is
+// 3-20% slower than the one here):
 //   M = K = 4096:        B = 4: streaming 4.96 (tiles 5.19)
 //                        B = 5: tiles 5.48 (streaming 6.20)
 //                        B = 8: tiles 5.74 (streaming 7.51); B = 16: 7.00 (13.49)
@@ -309,24 +311,18 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 //   M = 512, K = 8320:   B = 16: streaming 6.69 (tiles 11.61)
 // The tiles need B >= 5 to pay for 16 MFMA batch columns, and M / 16 tiles
 // leave most CUs idle at small M, where the streaming kernel splits the batch
-// over more workgroups instead. Staged scales win once rows are long (the
-// LDS copy is amortised over many groups; direct scale loads add four loads
-// per group).
-enum class ReuseShape { kStream, kDirect, kStaged };
+// over more workgroups instead. The tile kernel with weights through LDS
+// (us, against the direct-load tile kernel):
+//   M = K = 4096:        B = 5 5.02 (5.46), B = 8 5.56 (5.76), B = 16 6.82 (7.03)
+//   M = 11008, K = 4096: B = 5 9.57 (10.55), B = 8 11.03 (12.63), B = 16 15.40 (17.30)
+//   M = 8192, K = 28672: B = 5 36.7 (42.4), B = 8 42.4 (52.8), B = 16 62.1 (70.8)
+//   M = 28672, K = 8192: B = 5 37.1 (40.6), B = 8 43.6 (48.4), B = 16 62.9 (68.1)
+enum class ReuseShape { kStream, kTiles };
 
 ReuseShape reuse_shape(int M, int K, int B) {
+  (void)K;
   if (B <= 4 || (B <= 8 && M <= 2048) || (B <= 16 && M <= 1024)) return ReuseShape::kStream;
-  // Rows too long for the staged copy in LDS take the direct path too.
-  const bool fits = dk::reuse_lds_bytes_for(8, K, true) <= (size_t)lds_limit_bytes();
-  return (K <= 4096 || !fits) ? ReuseShape::kDirect : ReuseShape::kStaged;
-}
-
-size_t reuse_lds_bytes(int M, int K, int B) {
-  switch (reuse_shape(M, K, B)) {
-    case ReuseShape::kStream: return 0;
-    case ReuseShape::kDirect: return dk::reuse_lds_bytes_for(8, K, false);
-    default: return dk::reuse_lds_bytes_for(8, K, true);
-  }
+  return ReuseShape::kTiles;
 }
 
 size_t v3_lds_bytes(int K) { return (size_t)kWavesPerBlock * (K / DK_GROUP_SIZE) * sizeof(uint16_t); }
@@ -367,18 +363,11 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
   const uint4* x4 = reinterpret_cast<const uint4*>(x);
 
   if (cfg->reuse_weights) {
-    dim3 grid((M + 15) / 16, (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
-    const size_t lds = reuse_lds_bytes(M, K, B);
-    switch (reuse_shape(M, K, B)) {
-      case ReuseShape::kStream:
-        return launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B);
-      case ReuseShape::kDirect:
-        return L("reuse launch", dk::gemv_reuse<8, 1, false>, grid, dim3(8 * 64), lds, p4, scales,
-                 x4, y, M, K, B);
-      default:
-        return L("reuse launch", dk::gemv_reuse<8, 1, true>, grid, dim3(8 * 64), lds, p4, scales,
-                 x4, y, M, K, B);
-    }
+    if (reuse_shape(M, K, B) == ReuseShape::kStream)
+      return launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B);
+    const dim3 grid((M + 15) / 16, (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
+    return L("reuse launch", dk::gemv_reuse<dk::kReuseWaves>, grid, dim3(dk::kReuseWaves * 64), 0,
+             p4, scales, x4, y, M, K, B);
   }
   const dim3 block4(kWavesPerBlock * 64);
   const dim3 rows4((M + kWavesPerBlock - 1) / kWavesPerBlock);
@@ -440,11 +429,7 @@ int dk_gemv_validate(int M, int K, int B, const dk_gemv_config* cfg) {
   // v5 addresses activations through one buffer descriptor with 32-bit offsets.
   if ((long long)B * K * 2 > 0x7fffffffLL)
     return fail(DK_ERR_UNSUPPORTED, "B*K=%lld activation elements exceed 2^30", (long long)B * K);
-  if (cfg->reuse_weights) {
-    if (reuse_lds_bytes(M, K, B) > (size_t)lds_limit_bytes())
-      return fail(DK_ERR_UNSUPPORTED, "K=%d needs %zu B of LDS on the reuse path (limit %d)", K,
-                  reuse_lds_bytes(M, K, B), lds_limit_bytes());
-  } else if (cfg->version == DK_V3) {
+  if (!cfg->reuse_weights && cfg->version == DK_V3) {
     if (v3_lds_bytes(K) > (size_t)lds_limit_bytes())
       return fail(DK_ERR_UNSUPPORTED, "K=%d needs %zu B of LDS on v3 (limit %d)", K, v3_lds_bytes(K),
                   lds_limit_bytes());

@@ -557,23 +557,24 @@ __global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
 // Weight-reuse path (stamp 15): each decoded weight is used for up to 16
 // batch rows at once by v_mfma_f32_16x16x32_f16, so latency is nearly flat
 // in B instead of the reference's O(B) re-decode (csrc/gemv_w4a16.cu:364-413).
-// A workgroup of KS waves owns one 16-row tile; wave w takes groups w, w+KS,
-// ... (adjacent groups stream side by side). Lane l loads row l%16, bytes
-// [64g + 16(l/16), +16) of group g: four words = four MFMA k-steps that
-// together cover exactly group g, so the fp32 tile result of a group is
-// scaled once and accumulated. The KS wave partials are added in LDS in wave
-// order. Loads are raw buffer loads; rows past M and batch rows past B read
-// zero through out-of-range offsets.
+// A workgroup of KS waves owns one 16-row tile; wave w takes the blocks of
+// four consecutive groups w, w + KS, ... The MFMA operands:
 //   A (16x32, weights): lane l -> row l%16, 8 k-slots of lane group l/16
 //   B (32x16, x):       lane l -> batch l%16, same 8 k-slots
 //   D (16x16):          lane l -> rows 4(l/16)+v, batch l%16
-// Scales, two ways (kStaged):
-//   * staged: the tile's scales are copied transposed into LDS first, then
-//     one group per iteration (best for long rows, where the copy is
-//     amortised over many groups);
-//   * direct: no staging round trip before the first weight load; each lane
-//     loads the four scales of its D rows with the activations and weights,
-//     UG groups per stage (best for K <= 4096: 3-6% at M = K = 4096).
+// Lane l's A operand for group g is row l%16, bytes [64g + 16(l/16), +16):
+// four words = four MFMA k-steps that together cover exactly group g, so
+// the fp32 tile result of a group is scaled once and accumulated. Loading
+// those 16 bytes directly (one instruction reads 64 bytes from each of 16
+// rows) is slow at long rows; instead each block's weights come in four
+// instructions of 4 rows x 256 contiguous bytes, go through a wave-private
+// LDS buffer (one pad slot per row against bank conflicts) and are read back
+// in the A layout. Measured against the direct loads on MI355X: 8-20%
+// faster at M = 11008 or K = 28672 and 3-8% at M = K = 4096 for 5-16 batch
+// rows. Each lane loads the scales of its four D rows directly. The KS wave
+// partials are added in LDS in wave order. Loads are raw buffer loads; rows
+// past M, groups past G and batch rows past B read zero through out-of-range
+// offsets.
 // For up to four batch rows, and up to eight when M <= 2048, the reuse path
 // runs the streaming kernel above instead (each decoded weight still serves
 // every batch row of its tile): 16 MFMA batch columns cost more activation
@@ -581,41 +582,32 @@ __global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
 // idle at small M.
 // ---------------------------------------------------------------------------
 constexpr int kReuseBatch = 16;
+constexpr int kReuseWaves = 8;
+constexpr int kReuseRowSlots = 17;  // a row's four groups (16 x 16 bytes) and one pad slot
 
-__host__ __device__ constexpr size_t reuse_lds_bytes_for(int ks, int K, bool staged) {
-  return (size_t)ks * 256 * sizeof(float) +
-         (staged ? (size_t)16 * (K / kGroupSize) * sizeof(uint16_t) : 0);
+// The wave's own LDS traffic is ordered by these fences (no workgroup barrier:
+// every buffer is private to one wave).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int KS, int UG, bool kStaged>
+template <int KS>
 __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ packed,
                                                       const uint16_t* __restrict__ scales,
                                                       const uint4* __restrict__ x4,
                                                       uint16_t* __restrict__ y, int M, int K,
                                                       int B) {
-  static_assert(!kStaged || UG == 1, "the staged variant takes one group per iteration");
   write_stamp(DK_STAMP_REUSE);
-  extern __shared__ float lds_reuse[];
+  __shared__ uint4 wst[KS][16 * kReuseRowSlots];
+  __shared__ float red[KS * 256];
   const int G = K >> 7;
   const int nck = K >> 5;
-  float* red = lds_reuse;                                             // [KS][64][4]
-  uint16_t* sT = reinterpret_cast<uint16_t*>(lds_reuse + KS * 256);   // [G][16], staged only
-
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row0 = blockIdx.x * 16;
   const int b0 = blockIdx.y * kReuseBatch;
-
-  if (kStaged) {
-    // sT[g][r] = scales[row0 + r][g].
-    for (int e = threadIdx.x; e < 16 * G; e += blockDim.x) {
-      const int r = e / G, g = e - r * G;
-      const int row = min(row0 + r, M - 1);
-      sT[g * 16 + r] = scales[(size_t)row * G + g];
-    }
-    __syncthreads();
-  }
-
   const int r_lane = lane & 15;  // A row / B batch column
   const int kq = lane >> 4;      // lane group: 16-byte quarter of a group
   const int b = b0 + r_lane;
@@ -624,61 +616,55 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ 
   const auto rs = buffer_rsrc(scales + (size_t)row0 * G, (uint32_t)(rows * G * 2));
   const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
   const int xbase = b < B ? b * K * 2 + kq * 64 : kOutOfRange;
-  const int wbase = (r_lane * nck + kq) * 16;
+  uint4* wbuf = wst[wave];
 
   f4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int g0 = wave; g0 < G; g0 += KS * UG) {
-    uint4 xv[UG][4];
-    uint4 w[UG];
-    float sc[UG][4];
+  for (int g0 = 4 * wave; g0 < G; g0 += 4 * KS) {
+    // Weights of groups g0..g0+3: instruction i reads rows 4i + kq, lane
+    // r_lane taking bytes [16 r_lane, +16) of the row's 256-byte run.
+    const int run = g0 * 64 + r_lane * 16;
+    uint4 wl[4];
 #pragma unroll
-    for (int u = 0; u < UG; ++u) {
-      const int g = g0 + u * KS;
+    for (int i = 0; i < 4; ++i)
+      wl[i] = buffer_load16<kLoadNonTemporal>(
+          rw, run < nck * 16 ? (4 * i + kq) * nck * 16 + run : kOutOfRange);
+    uint4 xv[4][4];
+    float sc[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int g = g0 + u;
       const int xo = (b < B && g < G) ? xbase + g * 256 : kOutOfRange;
 #pragma unroll
       for (int j = 0; j < 4; ++j) xv[u][j] = buffer_load16<0>(rx, xo + 16 * j);
     }
-    if (!kStaged) {
 #pragma unroll
-      for (int u = 0; u < UG; ++u) {
-        const int g = g0 + u * KS;
+    for (int u = 0; u < 4; ++u) {
+      const int g = g0 + u;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int off = g < G ? ((4 * kq + v) * G + g) * 2 : kOutOfRange;
-          sc[u][v] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0));
-        }
+      for (int v = 0; v < 4; ++v) {
+        const int off = g < G ? ((4 * kq + v) * G + g) * 2 : kOutOfRange;
+        sc[u][v] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0));
       }
     }
+    // Every load of the block issues before the first wait.
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < UG; ++u) {
-      const int g = g0 + u * KS;
-      w[u] = buffer_load16<kLoadNonTemporal>(rw, g < G ? wbase + g * 64 : kOutOfRange);
-    }
-    // Direct path: every load of the stage is issued before the first MFMA.
-    // Left to itself the scheduler moves the second group's activation loads
-    // behind the first group's MFMAs, which makes them wait for its weights
-    // (4.87 vs 5.48 us for 8 waves x 2 groups at M = K = 4096, B = 2).
-    if constexpr (!kStaged) __builtin_amdgcn_sched_barrier(0);
-    if (kStaged) {
-      const uint2 s4 = *reinterpret_cast<const uint2*>(sT + g0 * 16 + 4 * kq);
-      sc[0][0] = h2f((uint16_t)(s4.x & 0xFFFFu));
-      sc[0][1] = h2f((uint16_t)(s4.x >> 16));
-      sc[0][2] = h2f((uint16_t)(s4.y & 0xFFFFu));
-      sc[0][3] = h2f((uint16_t)(s4.y >> 16));
-    }
+    for (int i = 0; i < 4; ++i) wbuf[(4 * i + kq) * kReuseRowSlots + r_lane] = wl[i];
+    wave_lds_sync();
 #pragma unroll
-    for (int u = 0; u < UG; ++u) {
-      const uint32_t words[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+    for (int u = 0; u < 4; ++u) {
+      const uint4 wv = wbuf[r_lane * kReuseRowSlots + 4 * u + kq];
+      const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
       f4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_word_h8(words[j]), pair_x8(xv[u][j]), c,
                                                    0, 0, 0);
-      // A group past G loaded zeros (weights, and scales on the direct path),
-      // so it adds nothing.
+      // A group past G loaded zero weights and scales, so it adds nothing.
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(c[v], sc[u][v], acc[v]);
     }
+    wave_lds_sync();  // the reads above complete before the next block's writes
   }
 
   // Cross-wave reduction of the 16x16 tile, in wave order.

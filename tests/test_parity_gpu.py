@@ -157,8 +157,8 @@ def test_reuse_small_batches_run_the_streaming_kernel():
 @pytest.mark.parametrize("m,k,b", [(40, 230400, 9), (4096, 4096, 8), (4096, 11008, 5),
                                    (8192, 28672, 8), (11008, 4096, 16), (2048, 4096, 12)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
-    # The MFMA tile shapes (direct: rows too long for the staged scales, 1800
-    # groups, or K <= 4096; staged scales otherwise): a
+    # The MFMA tile kernel (long rows of 1800 groups, K = 4096 and K > 4096,
+    # ragged groups per wave, one and two tiles of batch rows): a
     # one-hot batch row selects single scaled weights bit for bit, scaling x
     # by 2 or -1 scales y exactly (2 up to fp16 subnormal rounding), and rows
     # of a batch do not mix.
