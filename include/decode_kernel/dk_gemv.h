@@ -51,7 +51,9 @@ typedef enum dk_kernel_version {
 typedef struct dk_gemv_config {
   int version;       /* dk_kernel_version, 0..5 */
   int split_k;       /* v4 only, 1..32; ignored otherwise */
-  int reuse_weights; /* nonzero: weight-reuse path (MFMA), ignores version */
+  int reuse_weights; /* nonzero: weight-reuse path, ignores version: MFMA tiles
+                        from 5 batch rows (9 at M <= 2048, 17 at M <= 1024),
+                        the v5 kernel with batch tiles below that (stamp 15) */
   int warps_per_row; /* v1 only, 1..8: wave64s sharing one row's K */
 } dk_gemv_config;
 
