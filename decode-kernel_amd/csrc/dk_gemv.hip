@@ -312,11 +312,35 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 // The tiles need B >= 5 to pay for 16 MFMA batch columns, and M / 16 tiles
 // leave most CUs idle at small M, where the streaming kernel splits the batch
 // over more workgroups instead. The tile kernel with weights through LDS
-// (us, against the direct-load tile kernel):
+// (us; 8 waves, one tile per wave, blocks of four groups), against the
+// direct-load tile kernel:
 //   M = K = 4096:        B = 5 5.02 (5.46), B = 8 5.56 (5.76), B = 16 6.82 (7.03)
 //   M = 11008, K = 4096: B = 5 9.57 (10.55), B = 8 11.03 (12.63), B = 16 15.40 (17.30)
 //   M = 8192, K = 28672: B = 5 36.7 (42.4), B = 8 42.4 (52.8), B = 16 62.1 (70.8)
 //   M = 28672, K = 8192: B = 5 37.1 (40.6), B = 8 43.6 (48.4), B = 16 62.9 (68.1)
+// At 5-16 batch rows the activations (16 columns of x for every tile) are
+// 1.3-4x the weight bytes through each CU's L1; with them nearly free (a
+// timing probe) B = 16 ran 31-39% faster. Two tiles per wave share each
+// activation load, which pays once there are enough tiles for the chip
+// (M >= 8192; at M = 4096 half the CUs would idle); blocks of two groups
+// keep the two tiles' LDS within 64 KiB. Chosen (us), against one tile per
+// wave with blocks of four groups:
+//   M = 8192, K = 8192:   B = 5 11.02 (13.69), B = 8 11.44 (15.53), B = 16 15.21 (20.56)
+//   M = 11008, K = 4096:  B = 5 9.56 (9.69), B = 8 10.18 (11.03), B = 16 13.22 (15.44)
+//   M = 8192, K = 28672:  B = 5 28.45 (36.66), B = 8 32.60 (42.26), B = 16 42.82 (61.91)
+//   M = 28672, K = 8192:  B = 5 30.57 (36.42), B = 8 34.56 (43.67), B = 16 45.15 (62.83)
+//   M = 4096, K = 4096 (one tile per wave, blocks of two up to 8 rows):
+//                         B = 5 4.79 (5.04), B = 8 5.17 (5.60), B = 16 6.85
+//   M = 4096, K = 14336:  B = 5 10.87 (11.79), B = 8 12.26 (13.04), B = 16 17.96
+// Within 6% of the best of 8 shapes (waves 4-16, tiles per wave 1-4, blocks
+// of 2 or 4 groups) at these shapes.
+template <int KS, int RT, int SG>
+int launch_reuse(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
+                 int M, int K, int B) {
+  const dim3 grid((M + 16 * RT - 1) / (16 * RT), (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
+  return L("reuse launch", dk::gemv_reuse<KS, RT, SG>, grid, dim3(KS * 64), 0, p, s, x, y, M, K, B);
+}
+
 enum class ReuseShape { kStream, kTiles };
 
 ReuseShape reuse_shape(int M, int K, int B) {
@@ -365,9 +389,9 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
   if (cfg->reuse_weights) {
     if (reuse_shape(M, K, B) == ReuseShape::kStream)
       return launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B);
-    const dim3 grid((M + 15) / 16, (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
-    return L("reuse launch", dk::gemv_reuse<dk::kReuseWaves>, grid, dim3(dk::kReuseWaves * 64), 0,
-             p4, scales, x4, y, M, K, B);
+    if (M >= 8192) return launch_reuse<8, 2, 2>(L, p4, scales, x4, y, M, K, B);
+    return B <= 8 ? launch_reuse<8, 1, 2>(L, p4, scales, x4, y, M, K, B)
+                  : launch_reuse<8, 1, 4>(L, p4, scales, x4, y, M, K, B);
   }
   const dim3 block4(kWavesPerBlock * 64);
   const dim3 rows4((M + kWavesPerBlock - 1) / kWavesPerBlock);

@@ -582,8 +582,6 @@ __global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
 // idle at small M.
 // ---------------------------------------------------------------------------
 constexpr int kReuseBatch = 16;
-constexpr int kReuseWaves = 8;
-constexpr int kReuseRowSlots = 17;  // a row's four groups (16 x 16 bytes) and one pad slot
 
 // The wave's own LDS traffic is ordered by these fences (no workgroup barrier:
 // every buffer is private to one wave).
@@ -593,94 +591,116 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int KS>
+// KS waves per workgroup, RT 16-row tiles per wave (sharing each activation
+// load), SG consecutive groups per block.
+template <int KS, int RT, int SG>
 __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ packed,
                                                       const uint16_t* __restrict__ scales,
                                                       const uint4* __restrict__ x4,
                                                       uint16_t* __restrict__ y, int M, int K,
                                                       int B) {
+  static_assert(SG == 2 || SG == 4, "a block is two or four groups");
+  constexpr int kRows = 16 * RT;             // rows per workgroup
+  constexpr int kSlots = SG * 4 + 1;         // 16-byte slots per staged row, one of them padding
+  constexpr int kLanesPerRow = SG * 4;       // lanes loading one row's block
+  constexpr int kRowsPerLoad = 64 / kLanesPerRow;
+  constexpr int kLoads = kRows / kRowsPerLoad;
   write_stamp(DK_STAMP_REUSE);
-  __shared__ uint4 wst[KS][16 * kReuseRowSlots];
-  __shared__ float red[KS * 256];
+  __shared__ uint4 wst[KS][kRows * kSlots];
+  __shared__ float red[KS * 256 * RT];
   const int G = K >> 7;
   const int nck = K >> 5;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int row0 = blockIdx.x * 16;
+  const int row0 = blockIdx.x * kRows;
   const int b0 = blockIdx.y * kReuseBatch;
   const int r_lane = lane & 15;  // A row / B batch column
   const int kq = lane >> 4;      // lane group: 16-byte quarter of a group
   const int b = b0 + r_lane;
-  const int rows = min(16, M - row0);
+  const int rows = min(kRows, M - row0);
   const auto rw = buffer_rsrc(packed + (size_t)row0 * nck, (uint32_t)(rows * (K / 2)));
   const auto rs = buffer_rsrc(scales + (size_t)row0 * G, (uint32_t)(rows * G * 2));
   const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
   const int xbase = b < B ? b * K * 2 + kq * 64 : kOutOfRange;
+  const int lrow = lane / kLanesPerRow;  // row within one staging load
+  const int lcol = lane % kLanesPerRow;  // 16-byte slot within the row's block
   uint4* wbuf = wst[wave];
 
-  f4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int g0 = 4 * wave; g0 < G; g0 += 4 * KS) {
-    // Weights of groups g0..g0+3: instruction i reads rows 4i + kq, lane
-    // r_lane taking bytes [16 r_lane, +16) of the row's 256-byte run.
-    const int run = g0 * 64 + r_lane * 16;
-    uint4 wl[4];
+  f4_t acc[RT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+  for (int t = 0; t < RT; ++t) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+  for (int g0 = SG * wave; g0 < G; g0 += SG * KS) {
+    // Weights of groups g0..g0+SG-1: load i reads rows kRowsPerLoad * i +
+    // lrow, lane lcol taking bytes [16 lcol, +16) of the row's block.
+    const int run = g0 * 64 + lcol * 16;
+    uint4 wl[kLoads];
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i)
       wl[i] = buffer_load16<kLoadNonTemporal>(
-          rw, run < nck * 16 ? (4 * i + kq) * nck * 16 + run : kOutOfRange);
-    uint4 xv[4][4];
-    float sc[4][4];
+          rw, run < nck * 16 ? (kRowsPerLoad * i + lrow) * nck * 16 + run : kOutOfRange);
+    uint4 xv[SG][4];
+    float sc[RT][SG][4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < SG; ++u) {
       const int g = g0 + u;
       const int xo = (b < B && g < G) ? xbase + g * 256 : kOutOfRange;
 #pragma unroll
       for (int j = 0; j < 4; ++j) xv[u][j] = buffer_load16<0>(rx, xo + 16 * j);
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int g = g0 + u;
+    for (int t = 0; t < RT; ++t)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int off = g < G ? ((4 * kq + v) * G + g) * 2 : kOutOfRange;
-        sc[u][v] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0));
+      for (int u = 0; u < SG; ++u) {
+        const int g = g0 + u;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int off = g < G ? ((16 * t + 4 * kq + v) * G + g) * 2 : kOutOfRange;
+          sc[t][u][v] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0));
+        }
       }
-    }
     // Every load of the block issues before the first wait.
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wbuf[(4 * i + kq) * kReuseRowSlots + r_lane] = wl[i];
+    for (int i = 0; i < kLoads; ++i) wbuf[(kRowsPerLoad * i + lrow) * kSlots + lcol] = wl[i];
     wave_lds_sync();
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const uint4 wv = wbuf[r_lane * kReuseRowSlots + 4 * u + kq];
-      const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
-      f4_t c = {0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < SG; ++u) {
+      h8_t xp[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_word_h8(words[j]), pair_x8(xv[u][j]), c,
-                                                   0, 0, 0);
-      // A group past G loaded zero weights and scales, so it adds nothing.
+      for (int j = 0; j < 4; ++j) xp[j] = pair_x8(xv[u][j]);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(c[v], sc[u][v], acc[v]);
+      for (int t = 0; t < RT; ++t) {
+        const uint4 wv = wbuf[(16 * t + r_lane) * kSlots + 4 * u + kq];
+        const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+        f4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_word_h8(words[j]), xp[j], c, 0, 0, 0);
+        // A group past G loaded zero weights and scales, so it adds nothing.
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(c[v], sc[t][u][v], acc[t][v]);
+      }
     }
     wave_lds_sync();  // the reads above complete before the next block's writes
   }
 
-  // Cross-wave reduction of the 16x16 tile, in wave order.
+  // Cross-wave reduction of each 16x16 tile, in wave order.
 #pragma unroll
-  for (int v = 0; v < 4; ++v) red[(wave * 64 + lane) * 4 + v] = acc[v];
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[((t * KS + wave) * 64 + lane) * 4 + v] = acc[t][v];
   __syncthreads();
-  if (wave == 0) {
-    f4_t t = {0.f, 0.f, 0.f, 0.f};
+  if (wave < RT) {
+    const int t = wave;
+    f4_t sum = {0.f, 0.f, 0.f, 0.f};
     for (int w2 = 0; w2 < KS; ++w2)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) t[v] += red[(w2 * 64 + lane) * 4 + v];
+      for (int v = 0; v < 4; ++v) sum[v] += red[((t * KS + w2) * 64 + lane) * 4 + v];
     if (b < B) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int orow = row0 + 4 * kq + v;
-        if (orow < M) y[(size_t)b * M + orow] = f2h(t[v]);
+        const int orow = row0 + 16 * t + 4 * kq + v;
+        if (orow < M) y[(size_t)b * M + orow] = f2h(sum[v]);
       }
     }
   }

@@ -155,10 +155,13 @@ def test_reuse_small_batches_run_the_streaming_kernel():
 
 
 @pytest.mark.parametrize("m,k,b", [(40, 230400, 9), (4096, 4096, 8), (4096, 11008, 5),
-                                   (8192, 28672, 8), (11008, 4096, 16), (2048, 4096, 12)])
+                                   (8192, 28672, 8), (11008, 4096, 16), (2048, 4096, 12),
+                                   (8216, 4224, 6), (4096, 4096, 16)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
-    # The MFMA tile kernel (long rows of 1800 groups, K = 4096 and K > 4096,
-    # ragged groups per wave, one and two tiles of batch rows): a
+    # The MFMA tile kernel in each of its shapes (one tile per wave with blocks
+    # of two or four groups, two tiles per wave from M = 8192, the second of
+    # them partly past M at M = 8216), long rows of 1800 groups, K = 4096 and
+    # K > 4096, one and two tiles of batch rows: a
     # one-hot batch row selects single scaled weights bit for bit, scaling x
     # by 2 or -1 scales y exactly (2 up to fp16 subnormal rounding), and rows
     # of a batch do not mix.
