@@ -116,7 +116,8 @@ struct Launch {
 //   M = 2048, K = 16384: R1 U4 W8 prefetch 5.63 (6.79)
 //   M = 1024, K = 28672: R1 U4 W4 prefetch 6.50 (9.53)
 //   M = 512,  K = 4096:  R1 U2 W4 prefetch 2.28 (2.56)
-// (best of 48 variants, U from 2 to 6, at each but the last two: 2-3% off).
+// (the best of 48 variants, U from 2 to 6, at each of these shapes but
+// M = 1024, K = 28672, where R1 U3 W4 is 0.3% faster).
 // At M = 4096 the wide stages lose (M = 4096, K = 11008: R1 U6 W4 7.26
 // against R1 U2 W16 prefetch 6.04).
 template <int R, int U, int W, bool kPrefetch, typename Layout, int kStamp, int NB = 1>
