@@ -231,21 +231,41 @@ def test_edge_shapes_all_paths(m, k, batch):
         assert err < MAX_ABS, (label, m, k, batch, err)
 
 
+@pytest.mark.parametrize("batch", [64, 257])
+def test_large_batches_all_paths(batch):
+    # Many batch tiles on every path: 17 tiles of 16 rows on the MFMA path,
+    # 65-129 tiles of 2-4 rows on the streaming path.
+    m, k = 300, 1152
+    w, x = oracle.make_case(m, k, batch, seed=batch, w_std=0.05)
+    packed, scales, pd, sd, xd = _upload(w, x)
+    y_ref = oracle.linear_f64(x, packed, scales)
+    for label, kw in PATHS:
+        y = _gemv(pd, sd, xd, **kw)
+        err = oracle.max_abs_err(y.float().cpu().numpy(), y_ref)
+        assert err < MAX_ABS, (label, batch, err)
+    # Batch rows do not mix: the reversed batch gives the reversed outputs.
+    for label, kw in FAST_PATHS:
+        y = _gemv(pd, sd, xd, **kw)
+        assert torch.equal(_gemv(pd, sd, xd.flip(0).contiguous(), **kw), y.flip(0)), label
+
+
 # One shape per kernel the streaming path can choose (rows per wave, chunks
 # per stage, waves per workgroup, prefetch, batch rows per stage), each with M
-# not a multiple of the workgroup's rows so the last workgroup has idle waves:
-#   K <= 2048                      -> R1 U1 W16 prefetch
-#   M > 8192, K <= 8192            -> R2 U2 W4
-#   M > 8192, K > 8192             -> R2 U1 W8
-#   M <= 4096, K > 8192            -> R1 U2 W16 prefetch
-#   4096 < M <= 8192, K >= 8192    -> R2 U1 W16 prefetch
-#   otherwise                      -> R1 U2 W8 prefetch
-# and batches of 2, 3, 4 and 6 rows (tiles of 2, 3 or 4 rows per stage, a
-# partial tile at 6) on both sides of M = 4096.
-# Ragged shapes in every M range (<= 512, 1024, 2048, 3072, 4096, 8192,
-# above) and K range (<= 2048, 4096, 8192, 12288, above) the streaming
-# dispatch tells apart, run at batches that cover every tile size (NB = 1, 2,
-# 3, 4).
+# not a multiple of the workgroup's rows so the last workgroup has idle waves.
+# For one batch row:
+#   K <= 2048                              -> R1 U1 W16 prefetch
+#   M <= 3072: K <= 4096 / 8192 / 12288    -> R1 U2 / U4 / U6 W4 prefetch
+#              longer rows                 -> R1 U4 W4 (M <= 1024) or W8
+#   M > 8192, K <= 8192                    -> R2 U2 W4
+#   M > 8192, K > 8192                     -> R2 U1 W8
+#   M <= 4096, K > 8192                    -> R1 U2 W16 prefetch
+#   4096 < M <= 8192, K >= 8192            -> R2 U1 W16 prefetch
+#   otherwise                              -> R1 U2 W8 prefetch
+# and batches of 2-8 rows: tiles of 2, 3 or 4 rows per stage, the tile
+# choice depending on M and K ranges (the dispatch comments in dk_gemv.hip).
+# The shapes are ragged and fall in every M range (<= 512, 1024, 2048, 3072,
+# 4096, 8192, above) and K range (<= 2048, 4096, 8192, 12288, above) the
+# dispatch tells apart.
 DISPATCH_SHAPES = [(5000, 1920), (9001, 4224), (8197, 8320), (3000, 8320), (6001, 8320),
                    (2500, 4224), (500, 8320), (1000, 4224), (2000, 12416), (4000, 12416),
                    (700, 3968), (1500, 6144), (900, 16512), (3072, 2048), (400, 5120)]
