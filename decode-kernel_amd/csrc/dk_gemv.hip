@@ -225,6 +225,19 @@ int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x
 }
 #undef DK_BATCH
 
+// Batches that the MFMA tiles take on the fused gate/up step: the thresholds
+// of the GEMV's reuse path, with I rows per matrix. Against the streaming
+// kernel's batch tiles (us per launch, both matrices; 8 waves, blocks of two
+// groups, chosen over 4 waves with blocks of two or four):
+//                        B = 5           B = 8           B = 16
+//   I = 11008, H = 4096: 13.78 (24.31)   14.62 (31.51)   18.72 (58.31)
+//   I = 3584,  H = 8192: 11.39 (18.88)   11.96 (23.55)   13.89 (45.13)
+//   I = 28672, H = 8192: 52.96 (108.97)  59.11 (129.76)  76.80 (256.50)
+//   I = 2752,  H = 4096: 6.75 (11.62)    7.20 (15.39)    8.26 (22.66)
+bool gate_up_tiles(int I, int B) {
+  return !(B <= 4 || (B <= 8 && I <= 2048) || (B <= 16 && I <= 1024));
+}
+
 // Fused gate/up, R rows of each matrix per wave, on the LDS stage loop (U
 // chunks per stage, W waves per workgroup, next stage prefetched or not, NB
 // batch rows per stage). Timed on MI355X back-to-back over cold weights (us
@@ -270,6 +283,11 @@ int launch_gate_up_lds_t(const Launch& L, const uint4* g, const uint16_t* gs, co
   launch_gate_up_lds_t<R, U, W, PF, NB>(L, g, gs, u, us, x, h, I, H, B)
 int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const uint4* u,
                    const uint16_t* us, const uint4* x, uint16_t* h, int I, int H, int B) {
+  if (gate_up_tiles(I, B)) {
+    const dim3 grid((I + 15) / 16, (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
+    return L("gate/up launch", dk::gate_up_silu_tiles<8, 2>, grid, dim3(8 * 64), 0, g, gs, u, us,
+             x, I, H, B, h);
+  }
   if (B == 1) {
     // Few rows of up to 8192 weights: one stage of U = 4 per row.
     if (I <= 2048 && H > 4096 && H <= 8192) return DK_GATE_UP(1, 4, 4, true, 1);
@@ -553,6 +571,10 @@ int dk_mlp_decode(const uint32_t* gate_packed, const uint16_t* gate_scales,
   if (!aligned(workspace, 16)) return fail(DK_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   dk_gemv_config cfg;
   dk_gemv_config_default(&cfg);
+  // The down projection takes the weight-reuse path for a batch, as
+  // w4a16_linear does (python/decode_kernel/__init__.py:71-74): the v5
+  // kernel up to a few rows, the MFMA tiles beyond.
+  cfg.reuse_weights = B > 1 ? 1 : 0;
   // Validate the down projection before anything is launched.
   int rc = dk_gemv_validate(H, I, B, &cfg);
   if (rc != DK_OK) return rc;

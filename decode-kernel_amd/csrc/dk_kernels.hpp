@@ -591,59 +591,47 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// KS waves per workgroup, RT 16-row tiles per wave (sharing each activation
-// load), SG consecutive groups per block.
+// The block loop of the tile kernels: KS waves per workgroup, RT 16-row
+// tiles per wave sharing each activation load (tile t's weights and scales
+// through descriptors rw[t], rs[t], rows 0..15 relative to them), SG
+// consecutive groups per block. acc[t] is this lane's part of tile t's fp32
+// 16x16 result over the wave's blocks.
 template <int KS, int RT, int SG>
-__global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ packed,
-                                                      const uint16_t* __restrict__ scales,
-                                                      const uint4* __restrict__ x4,
-                                                      uint16_t* __restrict__ y, int M, int K,
-                                                      int B) {
+__device__ __forceinline__ void reuse_tile_loop(f4_t (&acc)[RT], uint4* wbuf,
+                                                const __amdgpu_buffer_rsrc_t (&rw)[RT],
+                                                const __amdgpu_buffer_rsrc_t (&rs)[RT],
+                                                __amdgpu_buffer_rsrc_t rx, int xbase, int G,
+                                                int nck, int lane, int wave, bool batch_ok) {
   static_assert(SG == 2 || SG == 4, "a block is two or four groups");
-  constexpr int kRows = 16 * RT;             // rows per workgroup
-  constexpr int kSlots = SG * 4 + 1;         // 16-byte slots per staged row, one of them padding
-  constexpr int kLanesPerRow = SG * 4;       // lanes loading one row's block
+  constexpr int kSlots = SG * 4 + 1;    // 16-byte slots per staged row, one of them padding
+  constexpr int kLanesPerRow = SG * 4;  // lanes loading one row's block
   constexpr int kRowsPerLoad = 64 / kLanesPerRow;
-  constexpr int kLoads = kRows / kRowsPerLoad;
-  write_stamp(DK_STAMP_REUSE);
-  __shared__ uint4 wst[KS][kRows * kSlots];
-  __shared__ float red[KS * 256 * RT];
-  const int G = K >> 7;
-  const int nck = K >> 5;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int row0 = blockIdx.x * kRows;
-  const int b0 = blockIdx.y * kReuseBatch;
-  const int r_lane = lane & 15;  // A row / B batch column
-  const int kq = lane >> 4;      // lane group: 16-byte quarter of a group
-  const int b = b0 + r_lane;
-  const int rows = min(kRows, M - row0);
-  const auto rw = buffer_rsrc(packed + (size_t)row0 * nck, (uint32_t)(rows * (K / 2)));
-  const auto rs = buffer_rsrc(scales + (size_t)row0 * G, (uint32_t)(rows * G * 2));
-  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
-  const int xbase = b < B ? b * K * 2 + kq * 64 : kOutOfRange;
+  constexpr int kLoads = 16 * RT / kRowsPerLoad;
+  constexpr int kLoadsPerTile = 16 / kRowsPerLoad;
+  const int r_lane = lane & 15;
+  const int kq = lane >> 4;
   const int lrow = lane / kLanesPerRow;  // row within one staging load
   const int lcol = lane % kLanesPerRow;  // 16-byte slot within the row's block
-  uint4* wbuf = wst[wave];
-
-  f4_t acc[RT];
 #pragma unroll
   for (int t = 0; t < RT; ++t) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
   for (int g0 = SG * wave; g0 < G; g0 += SG * KS) {
     // Weights of groups g0..g0+SG-1: load i reads rows kRowsPerLoad * i +
-    // lrow, lane lcol taking bytes [16 lcol, +16) of the row's block.
+    // lrow of the workgroup's 16 RT rows (tile i / kLoadsPerTile), lane lcol
+    // taking bytes [16 lcol, +16) of the row's block.
     const int run = g0 * 64 + lcol * 16;
     uint4 wl[kLoads];
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i)
-      wl[i] = buffer_load16<kLoadNonTemporal>(
-          rw, run < nck * 16 ? (kRowsPerLoad * i + lrow) * nck * 16 + run : kOutOfRange);
+    for (int i = 0; i < kLoads; ++i) {
+      const int r = (i % kLoadsPerTile) * kRowsPerLoad + lrow;
+      wl[i] = buffer_load16<kLoadNonTemporal>(rw[i / kLoadsPerTile],
+                                              run < nck * 16 ? r * nck * 16 + run : kOutOfRange);
+    }
     uint4 xv[SG][4];
     float sc[RT][SG][4];
 #pragma unroll
     for (int u = 0; u < SG; ++u) {
       const int g = g0 + u;
-      const int xo = (b < B && g < G) ? xbase + g * 256 : kOutOfRange;
+      const int xo = (batch_ok && g < G) ? xbase + g * 256 : kOutOfRange;
 #pragma unroll
       for (int j = 0; j < 4; ++j) xv[u][j] = buffer_load16<0>(rx, xo + 16 * j);
     }
@@ -654,8 +642,8 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ 
         const int g = g0 + u;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const int off = g < G ? ((16 * t + 4 * kq + v) * G + g) * 2 : kOutOfRange;
-          sc[t][u][v] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0));
+          const int off = g < G ? ((4 * kq + v) * G + g) * 2 : kOutOfRange;
+          sc[t][u][v] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs[t], off, 0, 0));
         }
       }
     // Every load of the block issues before the first wait.
@@ -683,23 +671,72 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ 
     }
     wave_lds_sync();  // the reads above complete before the next block's writes
   }
+}
 
-  // Cross-wave reduction of each 16x16 tile, in wave order.
+// LDS of the tile kernels: the wave-private staging buffers and the
+// cross-wave reduction.
+template <int KS, int RT, int SG>
+struct ReuseLds {
+  uint4 wst[KS][16 * RT * (SG * 4 + 1)];
+  float red[KS * 256 * RT];
+};
+
+// Adds tile t's KS wave partials in wave order (red after the barrier).
+template <int KS, int RT>
+__device__ __forceinline__ f4_t reuse_tile_sum(const float* red, int t, int lane) {
+  f4_t sum = {0.f, 0.f, 0.f, 0.f};
+  for (int w2 = 0; w2 < KS; ++w2)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) sum[v] += red[((t * KS + w2) * 64 + lane) * 4 + v];
+  return sum;
+}
+
+template <int KS, int RT>
+__device__ __forceinline__ void reuse_tile_publish(float* red, const f4_t (&acc)[RT], int wave,
+                                                   int lane) {
 #pragma unroll
   for (int t = 0; t < RT; ++t)
 #pragma unroll
     for (int v = 0; v < 4; ++v) red[((t * KS + wave) * 64 + lane) * 4 + v] = acc[t][v];
+}
+
+// GEMV: tile t of a workgroup is rows row0 + 16 t .. + 15.
+template <int KS, int RT, int SG>
+__global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ packed,
+                                                      const uint16_t* __restrict__ scales,
+                                                      const uint4* __restrict__ x4,
+                                                      uint16_t* __restrict__ y, int M, int K,
+                                                      int B) {
+  write_stamp(DK_STAMP_REUSE);
+  __shared__ ReuseLds<KS, RT, SG> lds;
+  const int G = K >> 7;
+  const int nck = K >> 5;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = blockIdx.x * 16 * RT;
+  const int b = blockIdx.y * kReuseBatch + (lane & 15);  // this lane's batch column
+  const int kq = lane >> 4;
+  __amdgpu_buffer_rsrc_t rw[RT], rs[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    // A tile wholly past M gets empty descriptors: its loads read zero.
+    const int rows = max(0, min(16, M - row0 - 16 * t));
+    const int rbase = rows > 0 ? row0 + 16 * t : 0;
+    rw[t] = buffer_rsrc(packed + (size_t)rbase * nck, (uint32_t)(rows * (K / 2)));
+    rs[t] = buffer_rsrc(scales + (size_t)rbase * G, (uint32_t)(rows * G * 2));
+  }
+  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
+  const int xbase = b < B ? b * K * 2 + kq * 64 : kOutOfRange;
+  f4_t acc[RT];
+  reuse_tile_loop<KS, RT, SG>(acc, lds.wst[wave], rw, rs, rx, xbase, G, nck, lane, wave, b < B);
+  reuse_tile_publish<KS, RT>(lds.red, acc, wave, lane);
   __syncthreads();
   if (wave < RT) {
-    const int t = wave;
-    f4_t sum = {0.f, 0.f, 0.f, 0.f};
-    for (int w2 = 0; w2 < KS; ++w2)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) sum[v] += red[((t * KS + w2) * 64 + lane) * 4 + v];
+    const f4_t sum = reuse_tile_sum<KS, RT>(lds.red, wave, lane);
     if (b < B) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int orow = row0 + 16 * t + 4 * kq + v;
+        const int orow = row0 + 16 * wave + 4 * kq + v;
         if (orow < M) y[(size_t)b * M + orow] = f2h(sum[v]);
       }
     }

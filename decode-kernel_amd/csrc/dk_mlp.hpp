@@ -7,8 +7,8 @@
 // with Wg and Wu in the W4A16 format of the GEMV (int4, group 128, fp16
 // scales), g and u accumulated in fp32 exactly as the v5 GEMV accumulates a
 // row, and the SiLU and product evaluated in fp32 before the one rounding to
-// fp16. The down projection that follows is the v5 GEMV with h as its
-// activations.
+// fp16. The down projection that follows is the GEMV with h as its
+// activations (the weight-reuse path for a batch).
 //
 // No counterpart in the reference, which times one GEMV at a time: this is
 // the step either side of its gemv() (python/decode_kernel/__init__.py:32-83)
@@ -18,7 +18,9 @@
 //
 // Mapping: the v5 streaming kernel with 2R rows per wave, rows 0..R-1 of the
 // stage taken from Wg and rows R..2R-1 from Wu at the same row indices, so
-// each activation stage in LDS serves both matrices.
+// each activation stage in LDS serves both matrices; from 5 batch rows (9 at
+// I <= 2048, 17 at I <= 1024) the MFMA tiles of the reuse path, one tile of
+// Wg and one of Wu per wave.
 #pragma once
 
 #include "dk_kernels.hpp"
@@ -68,6 +70,51 @@ __global__ __launch_bounds__(W * kWave) void gate_up_silu_lds(
       if (lane == 63 && row0 + r < I && b0 + b < B)
         h[(size_t)(b0 + b) * I + row0 + r] = f2h(silu_f32(g) * u);
     }
+}
+
+// Batches of several rows: the MFMA tile loop of the GEMV's reuse path with
+// its two tiles the same 16 rows of Wg and of Wu, so one activation load
+// serves both matrices and each decoded weight serves up to 16 batch rows.
+// The epilogue adds each tile's wave partials in wave order and forms h from
+// the two fp32 sums, as the streaming kernel above does.
+template <int KS, int SG>
+__global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles(
+    const uint4* __restrict__ gate, const uint16_t* __restrict__ gate_scales,
+    const uint4* __restrict__ up, const uint16_t* __restrict__ up_scales,
+    const uint4* __restrict__ x4, int I, int H, int B, uint16_t* __restrict__ h) {
+  write_stamp(kStampGateUp);
+  __shared__ ReuseLds<KS, 2, SG> lds;
+  const int G = H >> 7;
+  const int nck = H >> 5;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = blockIdx.x * 16;
+  const int b = blockIdx.y * kReuseBatch + (lane & 15);  // this lane's batch column
+  const int kq = lane >> 4;
+  const int rows = min(16, I - row0);
+  const __amdgpu_buffer_rsrc_t rw[2] = {
+      buffer_rsrc(gate + (size_t)row0 * nck, (uint32_t)(rows * (H / 2))),
+      buffer_rsrc(up + (size_t)row0 * nck, (uint32_t)(rows * (H / 2)))};
+  const __amdgpu_buffer_rsrc_t rs[2] = {
+      buffer_rsrc(gate_scales + (size_t)row0 * G, (uint32_t)(rows * G * 2)),
+      buffer_rsrc(up_scales + (size_t)row0 * G, (uint32_t)(rows * G * 2))};
+  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * H * 2));
+  const int xbase = b < B ? b * H * 2 + kq * 64 : kOutOfRange;
+  f4_t acc[2];
+  reuse_tile_loop<KS, 2, SG>(acc, lds.wst[wave], rw, rs, rx, xbase, G, nck, lane, wave, b < B);
+  reuse_tile_publish<KS, 2>(lds.red, acc, wave, lane);
+  __syncthreads();
+  if (wave == 0) {
+    const f4_t g = reuse_tile_sum<KS, 2>(lds.red, 0, lane);
+    const f4_t u = reuse_tile_sum<KS, 2>(lds.red, 1, lane);
+    if (b < B) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int orow = row0 + 4 * kq + v;
+        if (orow < I) h[(size_t)b * I + orow] = f2h(silu_f32(g[v]) * u[v]);
+      }
+    }
+  }
 }
 
 }  // namespace dk

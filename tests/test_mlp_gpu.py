@@ -56,7 +56,7 @@ def _check_tight(got: np.ndarray, ref: np.ndarray, label: str):
 
 @pytest.mark.parametrize("i,h,b", [
     (256, 128, 1), (256, 128, 3), (384, 640, 2), (1000, 256, 5), (11008, 4096, 1),
-    (11008, 4096, 4), (3584, 8192, 1), (3584, 8192, 2),
+    (11008, 4096, 4), (3584, 8192, 1), (3584, 8192, 2), (11008, 4096, 8), (3584, 8192, 16),
 ])
 def test_mlp_step_matches_oracle(i, h, b):
     from decode_kernel import _cuda, gate_up_silu, mlp_decode
@@ -78,7 +78,9 @@ def test_mlp_step_matches_oracle(i, h, b):
     hkn = hk.cpu().numpy()
     _check_tight(hkn.astype(np.float64), h_ref, f"h {i}x{h} B={b}")
     y = mlp_decode(x, gp, gs, up, us, dp, ds)
-    assert int(_cuda.last_kernel_stamp()) == 5  # the down projection is the v5 GEMV
+    # The down projection is the GEMV on h: v5 for one row, the reuse path
+    # for a batch.
+    assert int(_cuda.last_kernel_stamp()) == (15 if b > 1 else 5)
     yn = y.float().cpu().numpy()
     _check_tight(yn, oracle.linear_f64(hkn, ndp, nds), f"y from kernel h {i}x{h} B={b}")
     y_ref = oracle.mlp_decode_f64(xn, ngp, ngs, nup, nus, ndp, nds)
@@ -86,7 +88,7 @@ def test_mlp_step_matches_oracle(i, h, b):
     # The fused step is exactly gate_up_silu followed by gemv on its output.
     from decode_kernel import gemv
 
-    assert torch.equal(y, gemv(dp, ds, hk))
+    assert torch.equal(y, gemv(dp, ds, hk, reuse_weights=b > 1))
 
 
 # Ragged shapes in every I range (<= 2048, 4096, above) and H range (<= 4096,
@@ -97,17 +99,18 @@ GATE_UP_SHAPES = [(1000, 4224), (2000, 8320), (3000, 4224), (3000, 8320), (5000,
 
 @pytest.mark.parametrize("i,h", GATE_UP_SHAPES)
 def test_gate_up_every_dispatch_class(i, h):
-    # Batches 1-8 cover every tile size (one row, and tiles of 2, 3 and 4
-    # rows, the last one partly empty at B = 5 and 7). Each output row
-    # depends on its own activation row only, so the first b rows of one
-    # 8-row case give the reference for every b.
+    # Batches 1-8 cover every streaming tile size (one row, and tiles of 2, 3
+    # and 4 rows, the last one partly empty at B = 5 and 7); from 5 rows at
+    # I > 2048, and from 9 rows at I > 1024, the MFMA tiles run instead. Each
+    # output row depends on its own activation row only, so the first b rows
+    # of one 16-row case give the reference for every b.
     from decode_kernel import _cuda, gate_up_silu
 
     (gp, gs, up, us, _, _), (ngp, ngs, nup, nus, _, _) = _weights(i, h, seed=i + h)
-    x8 = _x(8, h, seed=i)
-    h_ref = oracle.gate_up_silu_f64(x8.cpu().numpy(), ngp, ngs, nup, nus)
-    for b in (1, 2, 3, 4, 5, 6, 7, 8):
-        hk = gate_up_silu(x8[:b].contiguous(), gp, gs, up, us)
+    x16 = _x(16, h, seed=i)
+    h_ref = oracle.gate_up_silu_f64(x16.cpu().numpy(), ngp, ngs, nup, nus)
+    for b in (1, 2, 3, 4, 5, 6, 7, 8, 12, 16):
+        hk = gate_up_silu(x16[:b].contiguous(), gp, gs, up, us)
         assert int(_cuda.last_kernel_stamp()) == 20
         _check_tight(hk.float().cpu().numpy(), h_ref[:b], f"h {i}x{h} B={b}")
 
