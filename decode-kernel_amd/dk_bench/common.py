@@ -39,6 +39,24 @@ def bytes_moved_w4(m: int, k: int, batch: int) -> int:
     return m * (k // 2) + m * (k // GROUP_SIZE) * 2 + batch * k * 2 + batch * m * 2
 
 
+def mlp_bytes(i: int, h: int, batch: int) -> int:
+    """Algorithmic HBM bytes of one MLP decode step: the three weight
+    matrices and their scales, x, h written and read back, and y."""
+    w = 3 * (i * h // 2 + i * h // GROUP_SIZE * 2)
+    return w + batch * h * 2 + 2 * batch * i * 2 + batch * h * 2
+
+
+def synthetic_case(m: int, k: int, batch: int, seed: int, w_std: float = 0.02):
+    """Benchmark inputs: W ~ N(0, w_std) fp32 and x ~ N(0, 1) fp16, both from
+    one PCG64 stream seeded with `seed` (numpy arrays)."""
+    import numpy as np
+
+    rng = np.random.Generator(np.random.PCG64(seed))
+    w = (rng.standard_normal((m, k), dtype=np.float32) * np.float32(w_std)).astype(np.float32)
+    x = rng.standard_normal((batch, k), dtype=np.float32).astype(np.float16)
+    return w, x
+
+
 def bytes_moved_fp16(m: int, k: int, batch: int) -> int:
     return m * k * 2 + batch * k * 2 + batch * m * 2
 

@@ -93,7 +93,7 @@ def main() -> None:
     from decode_kernel import _cuda, gemv
     from decode_kernel.quantize import quantize_and_pack
     from dk_bench.common import Flush, bytes_moved_w4
-    from oracle.oracle import make_case
+    from dk_bench.common import synthetic_case
 
     flush = Flush()
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
@@ -108,7 +108,7 @@ def main() -> None:
               flush=True)
         return
     m, k, b = SHAPES[args.config]
-    w, x = make_case(m, k, b, seed=1000)
+    w, x = synthetic_case(m, k, b, seed=1000)
     packed, scales = quantize_and_pack(torch.from_numpy(w))
     pd, sd, xd = packed.cuda(), scales.cuda(), torch.from_numpy(x).cuda()
     for _ in range(args.reps):
