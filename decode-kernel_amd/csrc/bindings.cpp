@@ -97,9 +97,15 @@ torch::Tensor gemv_common(torch::Tensor packed, torch::Tensor scales, torch::Ten
   const size_t ws_bytes = dk_gemv_workspace_bytes(M, K, B, &cfg);
   torch::Tensor workspace;
   void* ws_ptr = nullptr;
-  if (ws_bytes > 0) {
-    // [partials | tickets]: the partials are overwritten by every launch; the
-    // tickets (one per 4-row tile, at the end) must start at zero. A fill
+  if (ws_bytes > 0 && cfg.reuse_weights) {
+    // The reuse path's split-K tiles: tickets carry the call's generation, so
+    // the workspace needs no clearing (8-byte words keep it 8-byte aligned).
+    workspace = torch::empty({static_cast<int64_t>((ws_bytes + 7) / 8)},
+                             x.options().dtype(torch::kInt64));
+    ws_ptr = workspace.data_ptr();
+  } else if (ws_bytes > 0) {
+    // v4 [partials | tickets]: the partials are overwritten by every launch;
+    // the tickets (one per 4-row tile, at the end) must start at zero. A fill
     // kernel, not a memset, so the call stays capturable in a HIP graph.
     const int64_t words = static_cast<int64_t>((ws_bytes + 3) / 4);
     const int64_t partials = std::min<int64_t>(split_k, K / kGroupSize) * B * M;

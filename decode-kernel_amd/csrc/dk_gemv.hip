@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -328,6 +329,9 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 //   M = 1024, K = 11008: B = 8: streaming 6.82 (tiles 11.67)
 //                        B = 16: streaming 12.15 (tiles 15.43)
 //   M = 512, K = 8320:   B = 16: streaming 6.69 (tiles 11.61)
+//                        B = 32: streaming 11.66 (tiles 13.46); B = 64: tiles 13.32 (21.11)
+//   M = 40, K = 8192:    B = 64: streaming 5.92 (tiles 13.42)
+//   M = 1024, K = 4096:  B = 17: streaming 6.54 (tiles 7.16); B = 32: tiles 7.43 (9.40)
 // The tiles need B >= 5 to pay for 16 MFMA batch columns, and M / 16 tiles
 // leave most CUs idle at small M, where the streaming kernel splits the batch
 // over more workgroups instead. The tile kernel with weights through LDS
@@ -360,12 +364,65 @@ int launch_reuse(const Launch& L, const uint4* p, const uint16_t* s, const uint4
   return L("reuse launch", dk::gemv_reuse<KS, RT, SG>, grid, dim3(KS * 64), 0, p, s, x, y, M, K, B);
 }
 
+// h of the MLP step at the start of its workspace, padded to 256 bytes so
+// that the down projection's split-K workspace after it stays aligned.
+size_t mlp_h_bytes(int I, int B) { return ((size_t)B * (size_t)I * sizeof(uint16_t) + 255) / 256 * 256; }
+
+// Split-K tiles: S workgroups per set of RT tiles, the tickets (8 bytes per
+// set) first in the workspace, then the fp32 partials [S][B][M].
+constexpr int kSplitRT = 2;
+constexpr int kSplitS = 4;
+
+size_t split_tickets(int M, int B) {
+  return (size_t)((M + 16 * kSplitRT - 1) / (16 * kSplitRT)) *
+         (size_t)((B + dk::kReuseBatch - 1) / dk::kReuseBatch);
+}
+
+size_t split_ticket_bytes(int M, int B) { return (split_tickets(M, B) * 8 + 255) / 256 * 256; }
+
+size_t split_workspace_bytes(int M, int B) {
+  return split_ticket_bytes(M, B) + (size_t)kSplitS * B * M * sizeof(float);
+}
+
+// Generation of a split call: distinct for every launch in a process (32-bit
+// wrap), so a ticket left by an earlier call never reads as this call's.
+std::atomic<unsigned> g_split_gen{0x9E3779B9u};
+
+int launch_reuse_split(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x,
+                       uint16_t* y, int M, int K, int B, void* workspace) {
+  auto* tickets = static_cast<unsigned long long*>(workspace);
+  auto* partials =
+      reinterpret_cast<float*>(static_cast<char*>(workspace) + split_ticket_bytes(M, B));
+  const dim3 grid((M + 16 * kSplitRT - 1) / (16 * kSplitRT),
+                  (B + dk::kReuseBatch - 1) / dk::kReuseBatch, kSplitS);
+  const unsigned gen = g_split_gen.fetch_add(1u, std::memory_order_relaxed);
+  return L("reuse split launch", dk::gemv_reuse_split<8, kSplitRT, 2>, grid, dim3(8 * 64), 0, p, s,
+           x, y, partials, tickets, gen, M, K, B);
+}
+
 enum class ReuseShape { kStream, kTiles };
 
 ReuseShape reuse_shape(int M, int K, int B) {
   (void)K;
-  if (B <= 4 || (B <= 8 && M <= 2048) || (B <= 16 && M <= 1024)) return ReuseShape::kStream;
+  if (B <= 4 || (B <= 8 && M <= 2048) || (B <= 16 && M <= 1024) || (B <= 32 && M <= 512) ||
+      M <= 128)
+    return ReuseShape::kStream;
   return ReuseShape::kTiles;
+}
+
+// The tiles split K over workgroups, given a workspace, below 8192 rows
+// (fewer 16-row tiles than twice the CUs) when rows are long and the batch
+// large. Each split reads a quarter of the activations, which bound the
+// tiles at these batches, but the reduction across workgroups costs several
+// microseconds on this 8-XCD part: the partials and tickets pass the
+// non-coherent L2s (agent-scope atomics). Measured (us, single-pass tiles in
+// brackets): M = 4096, K = 11008: B = 16 17.04 (17.96), B = 32 24.78 (33.69);
+// M = 2048, K = 16384, B = 16: 16.30 (23.82); M = 6144, K = 8192: B = 16
+// 21.09 (25.02), B = 32 30.53 (37.41); M = 4096, K = 14336, B = 32 29.44
+// (40.52); and slower where the kernel is short: M = K = 4096: B = 8 11.93
+// (6.17), B = 32 16.38 (13.68); M = 4096, K = 11008, B = 8 14.52 (13.00).
+bool reuse_split(int M, int K, int B) {
+  return reuse_shape(M, K, B) == ReuseShape::kTiles && M < 8192 && K >= 8192 && B >= 16;
 }
 
 size_t v3_lds_bytes(int K) { return (size_t)kWavesPerBlock * (K / DK_GROUP_SIZE) * sizeof(uint16_t); }
@@ -395,12 +452,17 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
   if (!aligned(scales, 2) || !aligned(y, 2))
     return fail(DK_ERR_INVALID_ARGUMENT, "scales and y must be 2-byte aligned");
   const size_t need = dk_gemv_workspace_bytes(M, K, B, cfg);
-  if (need > 0) {
+  // The reuse path's split-K tiles run when a large enough workspace comes
+  // with the call; without one it runs the single-pass tiles.
+  const bool split = cfg->reuse_weights && need > 0 && workspace && workspace_bytes >= need;
+  if (need > 0 && !cfg->reuse_weights) {
     if (!workspace || workspace_bytes < need)
       return fail(DK_ERR_INVALID_ARGUMENT, "split-K needs a %zu-byte workspace (got %zu)", need,
                   workspace_bytes);
     if (!aligned(workspace, 4)) return fail(DK_ERR_INVALID_ARGUMENT, "workspace must be 4-byte aligned");
   }
+  if (split && !aligned(workspace, 8))
+    return fail(DK_ERR_INVALID_ARGUMENT, "workspace must be 8-byte aligned");
 
   const uint4* p4 = reinterpret_cast<const uint4*>(packed);
   const uint4* x4 = reinterpret_cast<const uint4*>(x);
@@ -408,6 +470,7 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
   if (cfg->reuse_weights) {
     if (reuse_shape(M, K, B) == ReuseShape::kStream)
       return launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B);
+    if (split) return launch_reuse_split(L, p4, scales, x4, y, M, K, B, workspace);
     if (M >= 8192) return launch_reuse<8, 2, 2>(L, p4, scales, x4, y, M, K, B);
     return B <= 8 ? launch_reuse<8, 1, 2>(L, p4, scales, x4, y, M, K, B)
                   : launch_reuse<8, 1, 4>(L, p4, scales, x4, y, M, K, B);
@@ -483,7 +546,8 @@ int dk_gemv_validate(int M, int K, int B, const dk_gemv_config* cfg) {
 size_t dk_gemv_workspace_bytes(int M, int K, int B, const dk_gemv_config* cfg) {
   if (dk_gemv_validate(M, K, B, cfg) != DK_OK) return 0;
   if (M <= 0 || K <= 0 || B <= 0) return 0;
-  if (cfg->reuse_weights || cfg->version != DK_V4) return 0;
+  if (cfg->reuse_weights) return reuse_split(M, K, B) ? split_workspace_bytes(M, B) : 0;
+  if (cfg->version != DK_V4) return 0;
   return v4_partials(M, K, B, cfg) * sizeof(float) + v4_tickets(M) * sizeof(unsigned int);
 }
 
@@ -553,7 +617,10 @@ int dk_gate_up_silu(const uint32_t* gate_packed, const uint16_t* gate_scales,
 
 size_t dk_mlp_workspace_bytes(int I, int H, int B) {
   if (I <= 0 || H <= 0 || B <= 0) return 0;
-  return (size_t)B * (size_t)I * sizeof(uint16_t);
+  dk_gemv_config cfg;
+  dk_gemv_config_default(&cfg);
+  cfg.reuse_weights = B > 1 ? 1 : 0;
+  return mlp_h_bytes(I, B) + dk_gemv_workspace_bytes(H, I, B, &cfg);
 }
 
 int dk_mlp_decode(const uint32_t* gate_packed, const uint16_t* gate_scales,
@@ -564,10 +631,12 @@ int dk_mlp_decode(const uint32_t* gate_packed, const uint16_t* gate_scales,
   if (I <= 0 || H <= 0 || B <= 0) return DK_OK;
   if (I % DK_GROUP_SIZE != 0)
     return fail(DK_ERR_INVALID_ARGUMENT, "I=%d must be divisible by group size 128", I);
-  const size_t need = dk_mlp_workspace_bytes(I, H, B);
-  if (!workspace || workspace_bytes < need)
-    return fail(DK_ERR_INVALID_ARGUMENT, "the MLP step needs a %zu-byte workspace (got %zu)", need,
-                workspace_bytes);
+  // h is required; the down projection's split-K workspace after it is used
+  // when the caller provides dk_mlp_workspace_bytes() in full.
+  const size_t need_h = (size_t)B * (size_t)I * sizeof(uint16_t);
+  if (!workspace || workspace_bytes < need_h)
+    return fail(DK_ERR_INVALID_ARGUMENT, "the MLP step needs a %zu-byte workspace (got %zu)",
+                need_h, workspace_bytes);
   if (!aligned(workspace, 16)) return fail(DK_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
   dk_gemv_config cfg;
   dk_gemv_config_default(&cfg);
@@ -586,7 +655,11 @@ int dk_mlp_decode(const uint32_t* gate_packed, const uint16_t* gate_scales,
   uint16_t* h = static_cast<uint16_t*>(workspace);
   rc = dk_gate_up_silu(gate_packed, gate_scales, up_packed, up_scales, x, h, I, H, B, stream);
   if (rc != DK_OK) return rc;
-  return gemv_impl(down_packed, down_scales, h, y, H, I, B, &cfg, nullptr, 0, Launch{stream});
+  const size_t down_ws = dk_gemv_workspace_bytes(H, I, B, &cfg);
+  const bool with_split = down_ws > 0 && workspace_bytes >= mlp_h_bytes(I, B) + down_ws;
+  void* ws = with_split ? static_cast<char*>(workspace) + mlp_h_bytes(I, B) : nullptr;
+  return gemv_impl(down_packed, down_scales, h, y, H, I, B, &cfg, ws, with_split ? down_ws : 0,
+                   Launch{stream});
 }
 
 const char* dk_last_error(void) { return dk::g_err.c_str(); }

@@ -575,9 +575,10 @@ __global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
 // partials are added in LDS in wave order. Loads are raw buffer loads; rows
 // past M, groups past G and batch rows past B read zero through out-of-range
 // offsets.
-// For up to four batch rows, and up to eight when M <= 2048, the reuse path
-// runs the streaming kernel above instead (each decoded weight still serves
-// every batch row of its tile): 16 MFMA batch columns cost more activation
+// For up to four batch rows, and more at small M (up to 8 rows at M <= 2048,
+// 16 at M <= 1024, 32 at M <= 512, any at M <= 128), the reuse path runs the
+// streaming kernel above instead (each decoded weight still serves every
+// batch row of its tile): 16 MFMA batch columns cost more activation
 // traffic than they save at small batches, and M / 16 tiles leave most CUs
 // idle at small M.
 // ---------------------------------------------------------------------------
@@ -593,7 +594,8 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 // The block loop of the tile kernels: KS waves per workgroup, RT 16-row
 // tiles per wave sharing each activation load (tile t's weights and scales
-// through descriptors rw[t], rs[t], rows 0..15 relative to them), SG
+// through descriptors rw[t], rs[t], rows 0..15 relative to them, starting at
+// the first of the G groups covered; a row's scales are Gstride apart), SG
 // consecutive groups per block. acc[t] is this lane's part of tile t's fp32
 // 16x16 result over the wave's blocks.
 template <int KS, int RT, int SG>
@@ -601,7 +603,8 @@ __device__ __forceinline__ void reuse_tile_loop(f4_t (&acc)[RT], uint4* wbuf,
                                                 const __amdgpu_buffer_rsrc_t (&rw)[RT],
                                                 const __amdgpu_buffer_rsrc_t (&rs)[RT],
                                                 __amdgpu_buffer_rsrc_t rx, int xbase, int G,
-                                                int nck, int lane, int wave, bool batch_ok) {
+                                                int Gstride, int nck, int lane, int wave,
+                                                bool batch_ok) {
   static_assert(SG == 2 || SG == 4, "a block is two or four groups");
   constexpr int kSlots = SG * 4 + 1;    // 16-byte slots per staged row, one of them padding
   constexpr int kLanesPerRow = SG * 4;  // lanes loading one row's block
@@ -624,7 +627,7 @@ __device__ __forceinline__ void reuse_tile_loop(f4_t (&acc)[RT], uint4* wbuf,
     for (int i = 0; i < kLoads; ++i) {
       const int r = (i % kLoadsPerTile) * kRowsPerLoad + lrow;
       wl[i] = buffer_load16<kLoadNonTemporal>(rw[i / kLoadsPerTile],
-                                              run < nck * 16 ? r * nck * 16 + run : kOutOfRange);
+                                              run < G * 64 ? r * nck * 16 + run : kOutOfRange);
     }
     uint4 xv[SG][4];
     float sc[RT][SG][4];
@@ -642,7 +645,7 @@ __device__ __forceinline__ void reuse_tile_loop(f4_t (&acc)[RT], uint4* wbuf,
         const int g = g0 + u;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const int off = g < G ? ((4 * kq + v) * G + g) * 2 : kOutOfRange;
+          const int off = g < G ? ((4 * kq + v) * Gstride + g) * 2 : kOutOfRange;
           sc[t][u][v] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs[t], off, 0, 0));
         }
       }
@@ -728,7 +731,8 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ 
   const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
   const int xbase = b < B ? b * K * 2 + kq * 64 : kOutOfRange;
   f4_t acc[RT];
-  reuse_tile_loop<KS, RT, SG>(acc, lds.wst[wave], rw, rs, rx, xbase, G, nck, lane, wave, b < B);
+  reuse_tile_loop<KS, RT, SG>(acc, lds.wst[wave], rw, rs, rx, xbase, G, G, nck, lane, wave,
+                              b < B);
   reuse_tile_publish<KS, RT>(lds.red, acc, wave, lane);
   __syncthreads();
   if (wave < RT) {
@@ -741,6 +745,108 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ 
       }
     }
   }
+}
+
+// Split-K form for rows too few to give every CU a tile with the whole row:
+// grid.z = S workgroups share each set of RT tiles, workgroup z covering
+// groups [z * ceil(G / S), +ceil(G / S)), so each reads only its slice of
+// the activations. Each writes its fp32 tile sums to partials[z][b][row]
+// (agent-scope stores, past the non-coherent L2s) and takes a ticket; the
+// last of the S adds the slices in order z = 0..S-1 (bit-reproducible) and
+// writes y. A ticket is 64 bits, the call's generation `gen` over an arrival
+// count: the first arrival of a call replaces whatever the ticket held (a
+// workspace need not be zeroed), the last resets it to (gen, 0), so replays
+// of one captured call with the same gen start from a clean count. A ticket
+// that already holds gen with a nonzero count before the call (left by no
+// call of this library; arbitrary memory matches with probability 2^-32)
+// would be miscounted.
+template <int KS, int RT, int SG>
+__global__ __launch_bounds__(KS * 64) void gemv_reuse_split(
+    const uint4* __restrict__ packed, const uint16_t* __restrict__ scales,
+    const uint4* __restrict__ x4, uint16_t* __restrict__ y, float* __restrict__ partials,
+    unsigned long long* __restrict__ tickets, unsigned gen, int M, int K, int B) {
+  write_stamp(DK_STAMP_REUSE);
+  __shared__ ReuseLds<KS, RT, SG> lds;
+  __shared__ int last;
+  const int S = gridDim.z;
+  const int split = blockIdx.z;
+  const int Gall = K >> 7;
+  const int gps = (Gall + S - 1) / S;
+  const int gbeg = min(split * gps, Gall);
+  const int G = min(gbeg + gps, Gall) - gbeg;  // groups of this slice (0 if none)
+  const int nck = K >> 5;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = blockIdx.x * 16 * RT;
+  const int b = blockIdx.y * kReuseBatch + (lane & 15);  // this lane's batch column
+  const int kq = lane >> 4;
+  __amdgpu_buffer_rsrc_t rw[RT], rs[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    // Descriptors start at the slice's first group of the tile's first row
+    // and end after its last group of the tile's last row.
+    const int rows = max(0, min(16, M - row0 - 16 * t));
+    const int rbase = rows > 0 ? row0 + 16 * t : 0;
+    const uint32_t wbytes = rows > 0 ? (uint32_t)((rows - 1) * (K / 2) + G * 64) : 0u;
+    const uint32_t sbytes = rows > 0 ? (uint32_t)(((rows - 1) * Gall + G) * 2) : 0u;
+    rw[t] = buffer_rsrc(packed + (size_t)rbase * nck + (size_t)gbeg * 4, wbytes);
+    rs[t] = buffer_rsrc(scales + (size_t)rbase * Gall + gbeg, sbytes);
+  }
+  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
+  const int xbase = b < B ? b * K * 2 + gbeg * 256 + kq * 64 : kOutOfRange;
+  f4_t acc[RT];
+  reuse_tile_loop<KS, RT, SG>(acc, lds.wst[wave], rw, rs, rx, xbase, G, Gall, nck, lane, wave,
+                              b < B);
+  reuse_tile_publish<KS, RT>(lds.red, acc, wave, lane);
+  __syncthreads();
+  if (wave < RT) {
+    const f4_t sum = reuse_tile_sum<KS, RT>(lds.red, wave, lane);
+    if (b < B) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int orow = row0 + 16 * wave + 4 * kq + v;
+        if (orow < M)
+          __hip_atomic_store(&partials[((size_t)split * B + b) * M + orow], sum[v],
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  // Every wave's partial stores are complete before the ticket is taken.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  unsigned long long* ticket = &tickets[blockIdx.y * gridDim.x + blockIdx.x];
+  if (threadIdx.x == 0) {
+    unsigned long long t = __hip_atomic_load(ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned arrived;
+    for (;;) {
+      const bool same = (unsigned)(t >> 32) == gen;
+      arrived = same ? (unsigned)t : 0u;
+      const unsigned long long next = ((unsigned long long)gen << 32) | (arrived + 1u);
+      // On failure t holds the current value; the loop ends when this
+      // workgroup's increment lands (at most S workgroups contend).
+      if (__hip_atomic_compare_exchange_strong(ticket, &t, next, __ATOMIC_RELAXED,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+        break;
+    }
+    last = arrived == (unsigned)(S - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  if (wave < RT && b < B) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int orow = row0 + 16 * wave + 4 * kq + v;
+      if (orow >= M) continue;
+      float sum = 0.f;
+      for (int z = 0; z < S; ++z)
+        sum += __hip_atomic_load(&partials[((size_t)z * B + b) * M + orow], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      y[(size_t)b * M + orow] = f2h(sum);
+    }
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(ticket, (unsigned long long)gen << 32, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace dk

@@ -101,7 +101,7 @@ __global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles(
   const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * H * 2));
   const int xbase = b < B ? b * H * 2 + kq * 64 : kOutOfRange;
   f4_t acc[2];
-  reuse_tile_loop<KS, 2, SG>(acc, lds.wst[wave], rw, rs, rx, xbase, G, nck, lane, wave, b < B);
+  reuse_tile_loop<KS, 2, SG>(acc, lds.wst[wave], rw, rs, rx, xbase, G, G, nck, lane, wave, b < B);
   reuse_tile_publish<KS, 2>(lds.red, acc, wave, lane);
   __syncthreads();
   if (wave == 0) {

@@ -52,8 +52,9 @@ typedef struct dk_gemv_config {
   int version;       /* dk_kernel_version, 0..5 */
   int split_k;       /* v4 only, 1..32; ignored otherwise */
   int reuse_weights; /* nonzero: weight-reuse path, ignores version: MFMA tiles
-                        from 5 batch rows (9 at M <= 2048, 17 at M <= 1024),
-                        the v5 kernel with batch tiles below that (stamp 15) */
+                        from 5 batch rows (9 at M <= 2048, 17 at M <= 1024,
+                        33 at M <= 512, none at M <= 128), the v5 kernel with
+                        batch tiles below that (stamp 15) */
   int warps_per_row; /* v1 only, 1..8: wave64s sharing one row's K */
 } dk_gemv_config;
 
@@ -67,15 +68,23 @@ typedef enum dk_status {
 /* Fill *cfg with the reference defaults (v5, split_k 4, reuse 0, 1 wave/row). */
 void dk_gemv_config_default(dk_gemv_config* cfg);
 
-/* Bytes of device workspace dk_w4a16_gemv needs for this call (0 for every
- * variant except split-K v4: fp32 partials [split_k', B, M], split_k' =
- * min(split_k, K/128), followed by one uint32 completion ticket per 4-row
- * tile, ceil(M/4)). The ticket area must be zero when a v4 call starts;
- * every v4 call leaves it zero again, so a workspace zeroed once can be
- * reused by later calls that run one after another (each stream its own
- * workspace). No counterpart in the reference, whose v4 took an fp32 [B, M]
- * buffer zeroed per call (include/decode_kernel/gemv_w4a16.h:33,
- * csrc/bindings.cpp:65-68). Returns 0 for invalid arguments. */
+/* Bytes of device workspace dk_w4a16_gemv takes for this call; 0 for every
+ * variant but two:
+ *  - split-K v4 (required): fp32 partials [split_k', B, M], split_k' =
+ *    min(split_k, K/128), followed by one uint32 completion ticket per 4-row
+ *    tile, ceil(M/4). The ticket area must be zero when a v4 call starts;
+ *    every v4 call leaves it zero again, so a workspace zeroed once can be
+ *    reused by later calls of the same shape that run one after another.
+ *  - the weight-reuse path when its MFMA tiles split K over workgroups (16
+ *    or more batch rows, M < 8192, K >= 8192; optional): one 8-byte ticket per set of
+ *    32 rows and 16 batch rows, padded to 256 bytes, then fp32 partials
+ *    [4, B, M]. It needs no clearing: each ticket carries the call's
+ *    generation. Without it (NULL or too small) the path runs its
+ *    single-pass tiles, same results within rounding.
+ * Calls that overlap in time need separate workspaces. No counterpart in the
+ * reference, whose v4 took an fp32 [B, M] buffer zeroed per call
+ * (include/decode_kernel/gemv_w4a16.h:33, csrc/bindings.cpp:65-68) and whose
+ * reuse path took none. Returns 0 for invalid arguments. */
 size_t dk_gemv_workspace_bytes(int M, int K, int B, const dk_gemv_config* cfg);
 
 /* Host-side argument check of dk_w4a16_gemv without launching anything
@@ -87,12 +96,12 @@ int dk_gemv_validate(int M, int K, int B, const dk_gemv_config* cfg);
  * `stream`. Replaces decode_kernel::w4a16_gemv
  * (include/decode_kernel/gemv_w4a16.h:34-36, csrc/gemv_w4a16.cu:568-591).
  * M, K or B <= 0 is a no-op returning DK_OK (csrc/gemv_w4a16.cu:571).
- * `workspace` must hold dk_gemv_workspace_bytes() bytes (may be NULL if 0).
+ * `workspace` must hold dk_gemv_workspace_bytes() bytes for v4 (may be NULL
+ * if 0); on the reuse path a workspace of that size is optional and 8-byte
+ * aligned.
  * Differences from the reference: launch errors are returned (the reference
  * printed and continued, csrc/gemv_w4a16.cu:9-16), and split-K is one
- * launch with a deterministic reduction instead of memset+atomics+convert.
- * Concurrent split-K calls on one device must not overlap in time: they
- * share the device's completion tickets. */
+ * launch with a deterministic reduction instead of memset+atomics+convert. */
 int dk_w4a16_gemv(const uint32_t* packed, const uint16_t* scales,
                   const uint16_t* x, uint16_t* y, int M, int K, int B,
                   const dk_gemv_config* cfg, void* workspace,

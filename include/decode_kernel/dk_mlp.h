@@ -36,11 +36,16 @@ int dk_gate_up_silu(const uint32_t* gate_packed, const uint16_t* gate_scales,
                     const uint16_t* x, uint16_t* h, int I, int H, int B,
                     hipStream_t stream);
 
-/* Bytes of the h workspace dk_mlp_decode needs: B * I fp16 (0 if empty). */
+/* Bytes of workspace dk_mlp_decode takes (0 if empty): h, B * I fp16 padded
+ * to 256 bytes, then the down projection's split-K workspace where its
+ * batch runs on the split MFMA tiles (dk_gemv_workspace_bytes with
+ * reuse_weights). Only the B * I * 2 bytes of h are required; with less than
+ * the full size the down projection runs its single-pass tiles. */
 size_t dk_mlp_workspace_bytes(int I, int H, int B);
 
 /* y = Wd fp16(silu(Wg x) * (Wu x)): the fused gate/up kernel into the
- * workspace (16-byte aligned, dk_mlp_workspace_bytes), then the v5 GEMV.
+ * workspace (16-byte aligned, dk_mlp_workspace_bytes), then the GEMV on h
+ * (v5 for one row, the weight-reuse path for a batch).
  * H % 128 == 0 and I % 128 == 0. I <= 0 leaves y unwritten (it is zero),
  * as the GEMV does for K = 0; H or B <= 0 is a no-op. */
 int dk_mlp_decode(const uint32_t* gate_packed, const uint16_t* gate_scales,

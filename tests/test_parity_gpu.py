@@ -131,16 +131,18 @@ def test_batch_sweep_c3(batch):
 
 
 def test_reuse_small_batches_run_the_streaming_kernel():
-    # Up to four batch rows, up to eight with M <= 2048 and up to 16 with
-    # M <= 1024: the reuse path runs the streaming kernel with its batch tiles
-    # (stamp 15), so its output is the v5 output bit for bit. Five rows with
-    # M > 2048 take the MFMA tile kernel, which still meets the oracle's bound.
+    # Up to four batch rows, up to 8 with M <= 2048, 16 with M <= 1024, 32
+    # with M <= 512 and any with M <= 128: the reuse path runs the streaming
+    # kernel with its batch tiles (stamp 15), so its output is the v5 output
+    # bit for bit. Five rows with M > 2048 take the MFMA tile kernel, which
+    # still meets the oracle's bound.
     from decode_kernel import _cuda
 
     for (m, k, b) in [(4096, 4096, 1), (4096, 4096, 2), (11008, 4096, 2), (300, 8192, 1),
                       (512, 8192, 2), (8192, 4096, 3), (9000, 8192, 4), (4096, 4096, 3),
                       (2000, 8192, 4), (512, 8320, 3), (4096, 11008, 4), (1024, 11008, 6),
-                      (2048, 4224, 8), (40, 197632, 3), (1000, 4224, 16)]:
+                      (2048, 4224, 8), (40, 197632, 3), (1000, 4224, 16), (500, 4224, 32),
+                      (100, 8192, 64)]:
         w, x = oracle.make_case(m, k, b, seed=m + k + b)
         _, _, pd, sd, xd = _upload(w, x)
         y_reuse = _gemv(pd, sd, xd, version=5, reuse_weights=True)
@@ -154,13 +156,14 @@ def test_reuse_small_batches_run_the_streaming_kernel():
     _check_against_oracle(y, oracle.linear_f64(x, packed, scales), "reuse 3000x8320 B=5")
 
 
-@pytest.mark.parametrize("m,k,b", [(40, 230400, 9), (4096, 4096, 8), (4096, 11008, 5),
+@pytest.mark.parametrize("m,k,b", [(1100, 65536, 9), (4096, 4096, 8), (4096, 11008, 5),
                                    (8192, 28672, 8), (11008, 4096, 16), (2048, 4096, 12),
                                    (8216, 4224, 6), (4096, 4096, 16)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
-    # The MFMA tile kernel in each of its shapes (one tile per wave with blocks
-    # of two or four groups, two tiles per wave from M = 8192, the second of
-    # them partly past M at M = 8216), long rows of 1800 groups, K = 4096 and
+    # The single-pass MFMA tile kernel in each of its shapes (one tile per
+    # wave with blocks of two or four groups; two tiles per wave from
+    # M = 8192, the second of them partly past M at M = 8216; the split form
+    # is test_reuse_split_tiles), long rows of 512 groups, K = 4096 and
     # K > 4096, one and two tiles of batch rows: a
     # one-hot batch row selects single scaled weights bit for bit, scaling x
     # by 2 or -1 scales y exactly (2 up to fp16 subnormal rounding), and rows
@@ -191,6 +194,77 @@ def test_reuse_tile_kernel_exact_properties(m, k, b):
         assert np.array_equal(ye[i].view(np.uint16), expect.view(np.uint16)), (i, kk)
     if m * k <= 64 << 20:
         _check_against_oracle(y, oracle.linear_f64(x, packed, scales), f"reuse {m}x{k} B={b}")
+
+
+@pytest.mark.parametrize("m,k,b", [(4096, 8192, 16), (3000, 8320, 16), (2100, 12416, 17),
+                                   (4000, 12416, 33), (600, 65536, 17)])
+def test_reuse_split_tiles(m, k, b):
+    # The MFMA tiles with K split over four workgroups (reuse path, M < 8192,
+    # K >= 8192, 16 or more batch rows, a workspace from the caller; M = 600
+    # ends in a partial set of 32 rows): against the oracle, bit-identical on
+    # repeated calls and
+    # with workspaces full of different garbage (each ticket carries the
+    # call's generation, so no clearing is needed), and the same bits through
+    # the extension. Without a workspace the single-pass tiles run and also
+    # meet the oracle.
+    from decode_kernel import _abi
+
+    lib = _abi.load()
+    # |y| grows as sqrt(K): smaller weights at K = 65536 keep one fp16 step
+    # of y inside the absolute gate.
+    w_std = 0.05 if k <= 28672 else 0.005
+    w, x = oracle.make_case(m, k, b, seed=m + b, w_std=w_std)
+    packed, scales, pd, sd, xd = _upload(w, x)
+    y_ref = oracle.linear_f64(x, packed, scales)
+    cfg = _abi.default_config(lib, reuse_weights=1)
+    need = lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(cfg))
+    assert need > 0
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def call(ws):
+        y = torch.empty(b, m, dtype=torch.float16, device="cuda")
+        rc = lib.dk_w4a16_gemv(pd.data_ptr(), sd.data_ptr(), xd.data_ptr(), y.data_ptr(), m, k, b,
+                               ctypes.byref(cfg), None if ws is None else ws.data_ptr(),
+                               0 if ws is None else need, stream)
+        _abi.check(lib, rc)
+        return y
+
+    gen = torch.Generator(device="cuda").manual_seed(m * b)
+    garbage = [torch.randint(-(2 ** 62), 2 ** 62, ((need + 7) // 8,), dtype=torch.int64,
+                             device="cuda", generator=gen) for _ in range(2)]
+    y_split = call(garbage[0])
+    _check_against_oracle(y_split, y_ref, f"split {m}x{k} B={b}")
+    for _ in range(3):
+        assert torch.equal(call(garbage[0]), y_split)
+    assert torch.equal(call(garbage[1]), y_split)
+    assert torch.equal(_gemv(pd, sd, xd, reuse_weights=True), y_split)
+    y_single = call(None)
+    _check_against_oracle(y_single, y_ref, f"single-pass {m}x{k} B={b}")
+
+
+def test_reuse_split_graph_replays():
+    # A captured split call replays with the generation it was captured with:
+    # the last workgroup of each set resets its ticket to that generation
+    # with a zero count. Every replay, with eager calls between them, gives
+    # the eager result.
+    m, k, b = 4096, 8192, 16
+    w, x = oracle.make_case(m, k, b, seed=5, w_std=0.05)
+    _, _, pd, sd, xd = _upload(w, x)
+    y_eager = _gemv(pd, sd, xd, reuse_weights=True)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _gemv(pd, sd, xd, reuse_weights=True)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y_graph = _gemv(pd, sd, xd, reuse_weights=True)
+    for _ in range(4):
+        graph.replay()
+        y_between = _gemv(pd, sd, xd, reuse_weights=True)
+        torch.cuda.synchronize()
+        assert torch.equal(y_graph, y_eager)
+        assert torch.equal(y_between, y_eager)
 
 
 @pytest.mark.parametrize("name", ["c0_4096x4096", "c2_4096x11008", "c4b_8192x28672"])
