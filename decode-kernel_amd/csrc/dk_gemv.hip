@@ -352,11 +352,15 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 //   M = 11008, K = 4096:  B = 5 9.56 (9.69), B = 8 10.18 (11.03), B = 16 13.22 (15.44)
 //   M = 8192, K = 28672:  B = 5 28.45 (36.66), B = 8 32.60 (42.26), B = 16 42.82 (61.91)
 //   M = 28672, K = 8192:  B = 5 30.57 (36.42), B = 8 34.56 (43.67), B = 16 45.15 (62.83)
-//   M = 4096, K = 4096 (one tile per wave, blocks of two up to 8 rows):
-//                         B = 5 4.79 (5.04), B = 8 5.17 (5.60), B = 16 6.85
-//   M = 4096, K = 14336:  B = 5 10.87 (11.79), B = 8 12.26 (13.04), B = 16 17.96
 // Within 6% of the best of 8 shapes (waves 4-16, tiles per wave 1-4, blocks
-// of 2 or 4 groups) at these shapes.
+// of 2 or 4 groups) at these shapes. Up to M = 4096 one tile per wave with
+// 16 waves per tile (blocks of two groups); between, 8 waves. 16 waves hide
+// more latency; boxes differ in how much that matters (us, 16 waves against
+// 8 with blocks of two and of four groups, two boxes):
+//   M = K = 4096,  B = 8:  5.79 (6.13, 6.37) and 5.35 (5.17, 5.60)
+//                  B = 16: 7.24 (7.39, 7.79) and 7.12 (7.01, 6.85)
+//   M = 4096, K = 11008, B = 16: 15.66 (16.62, 17.93)
+//   M = 6144, K = 8192,  B = 16: 22.08 (21.28, 25.07)
 template <int KS, int RT, int SG>
 int launch_reuse(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                  int M, int K, int B) {
@@ -410,19 +414,21 @@ ReuseShape reuse_shape(int M, int K, int B) {
   return ReuseShape::kTiles;
 }
 
-// The tiles split K over workgroups, given a workspace, below 8192 rows
-// (fewer 16-row tiles than twice the CUs) when rows are long and the batch
-// large. Each split reads a quarter of the activations, which bound the
+// The tiles split K over workgroups, given a workspace, for long rows
+// (K >= 8192) with few tiles (M <= 2048) or a large batch (32 or more rows,
+// M <= 4096). Each split reads a quarter of the activations, which bound the
 // tiles at these batches, but the reduction across workgroups costs several
 // microseconds on this 8-XCD part: the partials and tickets pass the
 // non-coherent L2s (agent-scope atomics). Measured (us, single-pass tiles in
-// brackets): M = 4096, K = 11008: B = 16 17.04 (17.96), B = 32 24.78 (33.69);
-// M = 2048, K = 16384, B = 16: 16.30 (23.82); M = 6144, K = 8192: B = 16
-// 21.09 (25.02), B = 32 30.53 (37.41); M = 4096, K = 14336, B = 32 29.44
-// (40.52); and slower where the kernel is short: M = K = 4096: B = 8 11.93
-// (6.17), B = 32 16.38 (13.68); M = 4096, K = 11008, B = 8 14.52 (13.00).
+// brackets): M = 2048, K = 16384: B = 16 16.16 (21.18), B = 64 30.66
+// (40.58); M = 4096, K = 11008: B = 32 24.70 (29.18), B = 64 43.24 (55.56);
+// M = 4096, K = 14336, B = 64 51.92 (69.70); M = 3072, K = 12288, B = 32
+// 22.83 (31.21); and slower or level elsewhere: M = 4096, K = 8192, B = 16
+// 16.10 (12.37); M = 4096, K = 11008, B = 16 17.21 (15.72); M = 6144,
+// K = 8192, B = 32 30.52 (30.05); M = K = 4096, B = 8 11.93 (6.17).
 bool reuse_split(int M, int K, int B) {
-  return reuse_shape(M, K, B) == ReuseShape::kTiles && M < 8192 && K >= 8192 && B >= 16;
+  return reuse_shape(M, K, B) == ReuseShape::kTiles && K >= 8192 &&
+         (M <= 2048 || (M <= 4096 && B >= 32));
 }
 
 size_t v3_lds_bytes(int K) { return (size_t)kWavesPerBlock * (K / DK_GROUP_SIZE) * sizeof(uint16_t); }
@@ -472,8 +478,8 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
       return launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B);
     if (split) return launch_reuse_split(L, p4, scales, x4, y, M, K, B, workspace);
     if (M >= 8192) return launch_reuse<8, 2, 2>(L, p4, scales, x4, y, M, K, B);
-    return B <= 8 ? launch_reuse<8, 1, 2>(L, p4, scales, x4, y, M, K, B)
-                  : launch_reuse<8, 1, 4>(L, p4, scales, x4, y, M, K, B);
+    if (M <= 4096) return launch_reuse<16, 1, 2>(L, p4, scales, x4, y, M, K, B);
+    return launch_reuse<8, 1, 2>(L, p4, scales, x4, y, M, K, B);
   }
   const dim3 block4(kWavesPerBlock * 64);
   const dim3 rows4((M + kWavesPerBlock - 1) / kWavesPerBlock);

@@ -75,8 +75,9 @@ void dk_gemv_config_default(dk_gemv_config* cfg);
  *    tile, ceil(M/4). The ticket area must be zero when a v4 call starts;
  *    every v4 call leaves it zero again, so a workspace zeroed once can be
  *    reused by later calls of the same shape that run one after another.
- *  - the weight-reuse path when its MFMA tiles split K over workgroups (16
- *    or more batch rows, M < 8192, K >= 8192; optional): one 8-byte ticket per set of
+ *  - the weight-reuse path when its MFMA tiles split K over workgroups
+ *    (K >= 8192 and M <= 2048, or M <= 4096 with 32 or more batch rows;
+ *    optional): one 8-byte ticket per set of
  *    32 rows and 16 batch rows, padded to 256 bytes, then fp32 partials
  *    [4, B, M]. It needs no clearing: each ticket carries the call's
  *    generation. Without it (NULL or too small) the path runs its

@@ -115,20 +115,21 @@ def test_split_k_workspace_contract(lib):
 
 
 def test_reuse_split_workspace_size(lib):
-    # The reuse path's split-K tiles (M < 8192, K >= 8192, 16 or more batch
-    # rows): 8-byte tickets per 32 rows x 16 batch rows, padded to 256 bytes,
-    # then fp32 partials [4, B, M]. Zero where the path streams or does not
-    # split.
+    # The reuse path's split-K tiles (K >= 8192 and M <= 2048, or M <= 4096
+    # with 32 or more batch rows): 8-byte tickets per 32 rows x 16 batch
+    # rows, padded to 256 bytes, then fp32 partials [4, B, M]. Zero where the
+    # path streams or does not split.
     cfg = _abi.default_config(lib, reuse_weights=1)
     ws = lambda m, k, b: lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(cfg))
-    assert ws(4096, 8192, 16) == 1024 + 4 * 16 * 4096 * 4
-    assert ws(4096, 11008, 17) == 2048 + 4 * 17 * 4096 * 4
-    assert ws(3000, 8192, 16) == 768 + 4 * 16 * 3000 * 4  # 94 tickets -> 752 -> 768 bytes
-    assert ws(4096, 4096, 16) == 0     # short rows: single-pass tiles
-    assert ws(4096, 8192, 8) == 0      # small batch: single-pass tiles
+    assert ws(4096, 8192, 32) == 2048 + 4 * 32 * 4096 * 4  # 128 x 2 tickets
+    assert ws(2048, 11008, 17) == 1024 + 4 * 17 * 2048 * 4
+    assert ws(3000, 8192, 32) == 1536 + 4 * 32 * 3000 * 4  # 188 tickets -> 1504 -> 1536 bytes
+    assert ws(4096, 8192, 16) == 0     # single-pass tiles
+    assert ws(6144, 8192, 32) == 0     # single-pass tiles
+    assert ws(4096, 4096, 32) == 0     # short rows: single-pass tiles
     assert ws(4096, 4096, 4) == 0      # streaming kernel
     assert ws(1024, 8192, 16) == 0     # streaming kernel at small M
-    assert ws(8192, 8192, 16) == 0     # two tiles per wave, no split
+    assert ws(8192, 8192, 32) == 0     # two tiles per wave, no split
 
 
 def test_probe_argument_checks(lib):

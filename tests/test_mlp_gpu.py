@@ -57,7 +57,7 @@ def _check_tight(got: np.ndarray, ref: np.ndarray, label: str):
 @pytest.mark.parametrize("i,h,b", [
     (256, 128, 1), (256, 128, 3), (384, 640, 2), (1000, 256, 5), (11008, 4096, 1),
     (11008, 4096, 4), (3584, 8192, 1), (3584, 8192, 2), (11008, 4096, 8), (3584, 8192, 16),
-    (11008, 4096, 16),
+    (11008, 4096, 16), (11008, 2048, 16),
 ])
 def test_mlp_step_matches_oracle(i, h, b):
     from decode_kernel import _cuda, gate_up_silu, mlp_decode

@@ -196,13 +196,13 @@ def test_reuse_tile_kernel_exact_properties(m, k, b):
         _check_against_oracle(y, oracle.linear_f64(x, packed, scales), f"reuse {m}x{k} B={b}")
 
 
-@pytest.mark.parametrize("m,k,b", [(4096, 8192, 16), (3000, 8320, 16), (2100, 12416, 17),
-                                   (4000, 12416, 33), (600, 65536, 17)])
+@pytest.mark.parametrize("m,k,b", [(4096, 8192, 32), (3000, 8320, 33), (2000, 12416, 17),
+                                   (2048, 8192, 9), (600, 65536, 17)])
 def test_reuse_split_tiles(m, k, b):
-    # The MFMA tiles with K split over four workgroups (reuse path, M < 8192,
-    # K >= 8192, 16 or more batch rows, a workspace from the caller; M = 600
-    # ends in a partial set of 32 rows): against the oracle, bit-identical on
-    # repeated calls and
+    # The MFMA tiles with K split over four workgroups (reuse path, K >= 8192
+    # and M <= 2048 or 32 or more batch rows, a workspace from the caller;
+    # M = 600 and 3000 end in partial sets of 32 rows): against the oracle,
+    # bit-identical on repeated calls and
     # with workspaces full of different garbage (each ticket carries the
     # call's generation, so no clearing is needed), and the same bits through
     # the extension. Without a workspace the single-pass tiles run and also
@@ -247,7 +247,7 @@ def test_reuse_split_graph_replays():
     # the last workgroup of each set resets its ticket to that generation
     # with a zero count. Every replay, with eager calls between them, gives
     # the eager result.
-    m, k, b = 4096, 8192, 16
+    m, k, b = 2048, 8192, 16
     w, x = oracle.make_case(m, k, b, seed=5, w_std=0.05)
     _, _, pd, sd, xd = _upload(w, x)
     y_eager = _gemv(pd, sd, xd, reuse_weights=True)
