@@ -246,7 +246,7 @@ def test_gemv_brute_force_tiny():
 
 
 def test_bytes_moved_matches_reference_formula():
-    # bench/common.py:111-117 at 4096x4096 B=1 (SURVEY figure 8,667,136 B).
+    # bench/common.py:111-117 at 4096x4096 B=1 (8,667,136 B for one c0 launch).
     assert oracle.bytes_moved_w4(4096, 4096, 1) == 8_667_136
     assert oracle.flop_gemv(4096, 4096, 1) == 33_554_432
 
