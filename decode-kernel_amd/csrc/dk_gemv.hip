@@ -226,17 +226,20 @@ int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x
 }
 #undef DK_BATCH
 
-// Batches that the MFMA tiles take on the fused gate/up step: the thresholds
-// of the GEMV's reuse path, with I rows per matrix. Against the streaming
-// kernel's batch tiles (us per launch, both matrices; 8 waves, blocks of two
-// groups, chosen over 4 waves with blocks of two or four):
-//                        B = 5           B = 8           B = 16
-//   I = 11008, H = 4096: 13.78 (24.31)   14.62 (31.51)   18.72 (58.31)
-//   I = 3584,  H = 8192: 11.39 (18.88)   11.96 (23.55)   13.89 (45.13)
-//   I = 28672, H = 8192: 52.96 (108.97)  59.11 (129.76)  76.80 (256.50)
-//   I = 2752,  H = 4096: 6.75 (11.62)    7.20 (15.39)    8.26 (22.66)
-bool gate_up_tiles(int I, int B) {
-  return !(B <= 4 || (B <= 8 && I <= 2048) || (B <= 16 && I <= 1024));
+// Batches that the MFMA tiles take on the fused gate/up step. Tiles against
+// the streaming kernel's batch tiles in brackets (us per launch, both
+// matrices; 8 waves, blocks of two groups, chosen over 4 waves with blocks
+// of two or four; * marks the streaming kernel where it is chosen):
+//                        B = 3           B = 4           B = 5           B = 8           B = 16
+//   I = 11008, H = 4096: 13.62 (14.92)   13.77 (19.25)   13.78 (24.31)   14.62 (31.51)   18.72 (58.31)
+//   I = 3584,  H = 8192: 11.07 (10.74*)  11.15 (12.64)   11.39 (18.88)   11.96 (23.55)   13.89 (45.13)
+//   I = 28672, H = 8192: 50.73 (59.49)   52.05 (70.56)   52.96 (108.97)  59.11 (129.76)  76.80 (256.50)
+//   I = 2752,  H = 4096: 6.62 (7.03)     6.66 (8.34)     6.75 (11.62)    7.20 (15.39)    8.26 (22.66)
+//   I = 1376,  H = 4096: 6.37 (4.66*)    6.42 (5.28*)    6.42 (5.53*)
+// Two batch rows stream everywhere (I = 11008: 13.38 against 12.56).
+bool gate_up_tiles(int I, int H, int B) {
+  return !(B <= 2 || (B == 3 && I <= 4096 && H > 4096) || (B <= 8 && I <= 2048) ||
+           (B <= 16 && I <= 1024));
 }
 
 // Fused gate/up, R rows of each matrix per wave, on the LDS stage loop (U
@@ -284,7 +287,7 @@ int launch_gate_up_lds_t(const Launch& L, const uint4* g, const uint16_t* gs, co
   launch_gate_up_lds_t<R, U, W, PF, NB>(L, g, gs, u, us, x, h, I, H, B)
 int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const uint4* u,
                    const uint16_t* us, const uint4* x, uint16_t* h, int I, int H, int B) {
-  if (gate_up_tiles(I, B)) {
+  if (gate_up_tiles(I, H, B)) {
     const dim3 grid((I + 15) / 16, (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
     return L("gate/up launch", dk::gate_up_silu_tiles<8, 2>, grid, dim3(8 * 64), 0, g, gs, u, us,
              x, I, H, B, h);
@@ -311,56 +314,37 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 }
 #undef DK_GATE_UP
 
-// Reuse path: the MFMA tile kernel (8 waves per 16-row tile, blocks of four
-// groups, weights through wave-private LDS) against the streaming kernel
-// with its batch tiles, measured on MI355X back-to-back over cold weights
-// (us per launch, chosen first; the tile figures are from the earlier tile
-// kernel, which loaded the weights straight into the MFMA layout and is
-// 3-20% slower than the one here):
-//   M = K = 4096:        B = 4: streaming 4.96 (tiles 5.19)
-//                        B = 5: tiles 5.48 (streaming 6.20)
-//                        B = 8: tiles 5.74 (streaming 7.51); B = 16: 7.00 (13.49)
-//   M = 4096, K = 11008: B = 4: streaming 10.00 (tiles 10.36)
-//                        B = 5: tiles 11.35 (streaming 12.92)
-//   M = 8192, K = 28672: B = 4: streaming 35.5; B = 5: tiles 42.0 (streaming 57.5)
-//   M = 3072, K = 12288: B = 5: tiles 12.00 (streaming 12.70)
-//   M = 2048, K = 16384: B = 8: streaming 12.10 (tiles 15.64)
-//                        B = 12: tiles 18.14 (streaming 22.54)
-//   M = 1024, K = 11008: B = 8: streaming 6.82 (tiles 11.67)
-//                        B = 16: streaming 12.15 (tiles 15.43)
-//   M = 512, K = 8320:   B = 16: streaming 6.69 (tiles 11.61)
-//                        B = 32: streaming 11.66 (tiles 13.46); B = 64: tiles 13.32 (21.11)
-//   M = 40, K = 8192:    B = 64: streaming 5.92 (tiles 13.42)
-//   M = 1024, K = 4096:  B = 17: streaming 6.54 (tiles 7.16); B = 32: tiles 7.43 (9.40)
-// The tiles need B >= 5 to pay for 16 MFMA batch columns, and M / 16 tiles
-// leave most CUs idle at small M, where the streaming kernel splits the batch
-// over more workgroups instead. The tile kernel with weights through LDS
-// (us; 8 waves, one tile per wave, blocks of four groups), against the
-// direct-load tile kernel:
-//   M = K = 4096:        B = 5 5.02 (5.46), B = 8 5.56 (5.76), B = 16 6.82 (7.03)
-//   M = 11008, K = 4096: B = 5 9.57 (10.55), B = 8 11.03 (12.63), B = 16 15.40 (17.30)
-//   M = 8192, K = 28672: B = 5 36.7 (42.4), B = 8 42.4 (52.8), B = 16 62.1 (70.8)
-//   M = 28672, K = 8192: B = 5 37.1 (40.6), B = 8 43.6 (48.4), B = 16 62.9 (68.1)
-// At 5-16 batch rows the activations (16 columns of x for every tile) are
-// 1.3-4x the weight bytes through each CU's L1; with them nearly free (a
-// timing probe) B = 16 ran 31-39% faster. Two tiles per wave share each
-// activation load, which pays once there are enough tiles for the chip
-// (M >= 8192; at M = 4096 half the CUs would idle); blocks of two groups
-// keep the two tiles' LDS within 64 KiB. Chosen (us), against one tile per
-// wave with blocks of four groups:
-//   M = 8192, K = 8192:   B = 5 11.02 (13.69), B = 8 11.44 (15.53), B = 16 15.21 (20.56)
-//   M = 11008, K = 4096:  B = 5 9.56 (9.69), B = 8 10.18 (11.03), B = 16 13.22 (15.44)
-//   M = 8192, K = 28672:  B = 5 28.45 (36.66), B = 8 32.60 (42.26), B = 16 42.82 (61.91)
-//   M = 28672, K = 8192:  B = 5 30.57 (36.42), B = 8 34.56 (43.67), B = 16 45.15 (62.83)
-// Within 6% of the best of 8 shapes (waves 4-16, tiles per wave 1-4, blocks
-// of 2 or 4 groups) at these shapes. Up to M = 4096 one tile per wave with
-// 16 waves per tile (blocks of two groups); between, 8 waves. 16 waves hide
-// more latency; boxes differ in how much that matters (us, 16 waves against
-// 8 with blocks of two and of four groups, two boxes):
-//   M = K = 4096,  B = 8:  5.79 (6.13, 6.37) and 5.35 (5.17, 5.60)
-//                  B = 16: 7.24 (7.39, 7.79) and 7.12 (7.01, 6.85)
-//   M = 4096, K = 11008, B = 16: 15.66 (16.62, 17.93)
-//   M = 6144, K = 8192,  B = 16: 22.08 (21.28, 25.07)
+// Reuse path: the MFMA tile kernel (KS waves per 16-row tile, RT tiles per
+// wave, blocks of two groups, weights through wave-private LDS) against the
+// streaming kernel with its batch tiles, measured on MI355X back-to-back over
+// cold weights (us per launch, tiles first, * where the streaming kernel is
+// chosen):
+//                        B = 2          B = 3          B = 4          B = 5    B = 8    B = 16
+//   M = 28672, K = 8192: 29.08 (25.69*) 29.59 (33.42)  30.31 (36.87)  30.29    33.65    44.04
+//   M = 8192, K = 28672: 29.65 (24.58*) 29.40 (30.99)  29.68 (35.14)  30.24    32.76    40.91
+//   M = 4096, K = 11008: 8.68 (7.44*)   8.78 (8.62*)   8.94 (10.14)   9.06     10.64    15.71
+//   M = 3072, K = 8192:  6.84 (5.89*)   6.97 (6.93*)   7.13 (8.09)
+//   M = K = 4096:        4.66 (3.93*)   4.73 (4.44*)   4.82 (4.95)    4.82     5.23     6.82
+//   M = 11008, K = 4096: 9.36 (6.80*)   9.47 (8.50*)   9.56 (9.65)    9.45     10.10    13.09
+//   M = 6144, K = 8192:  11.46 (8.22*)  11.69 (10.03*) 11.88 (11.68)  11.87    13.57    19.73
+// and at small M, with the streaming kernel in brackets:
+//   M = 2048, K = 8192:  B = 4 6.91 (5.55*), B = 5 6.91 (6.45*), B = 8 7.74 (7.39*), B = 16 11.41 (13.09)
+//   M = 2048, K = 16384: B = 5 11.34 (10.35*), B = 8 13.34 (12.13*), B = 16 20.05 (22.60)
+//   M = 1024, K = 11008: B = 16 14.50 (12.15*), B = 32 14.21 (22.40)
+//   M = 1024, K = 4096:  B = 16 6.62 (5.55*), B = 32 6.60 (9.40)
+//   M = 512, K = 8320:   B = 16 11.63 (6.70*), B = 32 11.47 (11.67*)
+// The tiles cost about the same from one batch row to five (16 MFMA batch
+// columns), so they take three rows on the 70B shapes (M * K >= 2^27) and
+// four from M = 3072 (within 2% of the streaming kernel at M = 6144,
+// K = 8192); M / 16 tiles leave most CUs idle at small M, where the
+// streaming kernel splits the batch over more workgroups instead. Two tiles
+// per wave share each activation load once there are enough tiles for the
+// chip (M >= 8192); up to M = 4096 one tile per wave with 16 waves per tile,
+// except rows of 8192 weights or more at M <= 2048, and between 4096 and
+// 8192, with 8 (M = 2048, K = 16384, B = 16: 20.05 against 21.51 us;
+// M = K = 4096, B = 16: 7.24 against 7.39 in an earlier form of the kernel).
+// The weights come through LDS in 128-256 contiguous bytes per row (8-20%
+// faster than loading the MFMA layout directly at M = 11008 or K = 28672).
 template <int KS, int RT, int SG>
 int launch_reuse(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                  int M, int K, int B) {
@@ -407,28 +391,29 @@ int launch_reuse_split(const Launch& L, const uint4* p, const uint16_t* s, const
 enum class ReuseShape { kStream, kTiles };
 
 ReuseShape reuse_shape(int M, int K, int B) {
-  (void)K;
-  if (B <= 4 || (B <= 8 && M <= 2048) || (B <= 16 && M <= 1024) || (B <= 32 && M <= 512) ||
-      M <= 128)
+  if (B <= 2 || (B == 3 && (size_t)M * (size_t)K < ((size_t)1 << 27)) || (B == 4 && M < 3072) ||
+      (B <= 8 && M <= 2048) || (B <= 16 && M <= 1024) || (B <= 32 && M <= 512) || M <= 128)
     return ReuseShape::kStream;
   return ReuseShape::kTiles;
 }
 
-// The tiles split K over workgroups, given a workspace, for long rows
-// (K >= 8192) with few tiles (M <= 2048) or a large batch (32 or more rows,
-// M <= 4096). Each split reads a quarter of the activations, which bound the
-// tiles at these batches, but the reduction across workgroups costs several
-// microseconds on this 8-XCD part: the partials and tickets pass the
-// non-coherent L2s (agent-scope atomics). Measured (us, single-pass tiles in
-// brackets): M = 2048, K = 16384: B = 16 16.16 (21.18), B = 64 30.66
-// (40.58); M = 4096, K = 11008: B = 32 24.70 (29.18), B = 64 43.24 (55.56);
-// M = 4096, K = 14336, B = 64 51.92 (69.70); M = 3072, K = 12288, B = 32
-// 22.83 (31.21); and slower or level elsewhere: M = 4096, K = 8192, B = 16
-// 16.10 (12.37); M = 4096, K = 11008, B = 16 17.21 (15.72); M = 6144,
-// K = 8192, B = 32 30.52 (30.05); M = K = 4096, B = 8 11.93 (6.17).
+// The tiles split K over workgroups, given a workspace, where that measured
+// faster: rows longer than 8192 weights with few tiles (M <= 2048) or 32 or
+// more batch rows (M <= 4096), and rows of 8192 at 2049-4096 rows with 32 or
+// more batch rows. Each split reads a quarter of the activations, which
+// bound the tiles at these batches, but the reduction across workgroups
+// costs several microseconds on this 8-XCD part: the partials and tickets
+// pass the non-coherent L2s (agent-scope atomics). Measured (us, single-pass
+// tiles in brackets): M = 2048, K = 16384, B = 16 16.26 (20.05);
+// M = 4096, K = 11008: B = 32 24.67 (29.31), B = 64 43.41 (56.23);
+// M = 3072, K = 12288, B = 32 22.77 (32.17); M = 4096, K = 14336, B = 64
+// 52.00 (71.88); M = 4096, K = 8192: B = 32 21.29 (22.35), B = 64 36.94
+// (42.59); and slower or level elsewhere: M = 2048, K = 8192: B = 16 12.39
+// (11.41), B = 32 15.29 (11.38); M = 1024, K = 8192, B = 32 12.05 (11.29);
+// M = 4096, K = 11008, B = 16 15.77 (15.72).
 bool reuse_split(int M, int K, int B) {
-  return reuse_shape(M, K, B) == ReuseShape::kTiles && K >= 8192 &&
-         (M <= 2048 || (M <= 4096 && B >= 32));
+  if (reuse_shape(M, K, B) != ReuseShape::kTiles || K < 8192 || M > 4096) return false;
+  return K > 8192 ? (M <= 2048 || B >= 32) : (M > 2048 && B >= 32);
 }
 
 size_t v3_lds_bytes(int K) { return (size_t)kWavesPerBlock * (K / DK_GROUP_SIZE) * sizeof(uint16_t); }
@@ -478,7 +463,8 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
       return launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B);
     if (split) return launch_reuse_split(L, p4, scales, x4, y, M, K, B, workspace);
     if (M >= 8192) return launch_reuse<8, 2, 2>(L, p4, scales, x4, y, M, K, B);
-    if (M <= 4096) return launch_reuse<16, 1, 2>(L, p4, scales, x4, y, M, K, B);
+    if (M <= 4096 && (M > 2048 || K < 8192))
+      return launch_reuse<16, 1, 2>(L, p4, scales, x4, y, M, K, B);
     return launch_reuse<8, 1, 2>(L, p4, scales, x4, y, M, K, B);
   }
   const dim3 block4(kWavesPerBlock * 64);

@@ -18,9 +18,9 @@
 //
 // Mapping: the v5 streaming kernel with 2R rows per wave, rows 0..R-1 of the
 // stage taken from Wg and rows R..2R-1 from Wu at the same row indices, so
-// each activation stage in LDS serves both matrices; from 5 batch rows (9 at
-// I <= 2048, 17 at I <= 1024) the MFMA tiles of the reuse path, one tile of
-// Wg and one of Wu per wave.
+// each activation stage in LDS serves both matrices; from 3 batch rows (4
+// at I <= 4096 with H > 4096, 9 at I <= 2048, 17 at I <= 1024) the MFMA
+// tiles of the reuse path, one tile of Wg and one of Wu per wave.
 #pragma once
 
 #include "dk_kernels.hpp"
@@ -102,11 +102,11 @@ __global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles(
   const int xbase = b < B ? b * H * 2 + kq * 64 : kOutOfRange;
   f4_t acc[2];
   reuse_tile_loop<KS, 2, SG>(acc, lds.wst[wave], rw, rs, rx, xbase, G, G, nck, lane, wave, b < B);
-  reuse_tile_publish<KS, 2>(lds.red, acc, wave, lane);
+  reuse_tile_publish(lds, acc, wave, lane);
   __syncthreads();
   if (wave == 0) {
-    const f4_t g = reuse_tile_sum<KS, 2>(lds.red, 0, lane);
-    const f4_t u = reuse_tile_sum<KS, 2>(lds.red, 1, lane);
+    const f4_t g = reuse_tile_sum(lds, 0, lane);
+    const f4_t u = reuse_tile_sum(lds, 1, lane);
     if (b < B) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {

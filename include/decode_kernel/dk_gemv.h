@@ -52,8 +52,9 @@ typedef struct dk_gemv_config {
   int version;       /* dk_kernel_version, 0..5 */
   int split_k;       /* v4 only, 1..32; ignored otherwise */
   int reuse_weights; /* nonzero: weight-reuse path, ignores version: MFMA tiles
-                        from 5 batch rows (9 at M <= 2048, 17 at M <= 1024,
-                        33 at M <= 512, none at M <= 128), the v5 kernel with
+                        from 5 batch rows (3 at M * K >= 2^27, 4 at
+                        M >= 3072; 9 at M <= 2048, 17 at M <= 1024, 33 at
+                        M <= 512, none at M <= 128), the v5 kernel with
                         batch tiles below that (stamp 15) */
   int warps_per_row; /* v1 only, 1..8: wave64s sharing one row's K */
 } dk_gemv_config;
@@ -76,7 +77,8 @@ void dk_gemv_config_default(dk_gemv_config* cfg);
  *    every v4 call leaves it zero again, so a workspace zeroed once can be
  *    reused by later calls of the same shape that run one after another.
  *  - the weight-reuse path when its MFMA tiles split K over workgroups
- *    (K >= 8192 and M <= 2048, or M <= 4096 with 32 or more batch rows;
+ *    (K > 8192 with M <= 2048, or with M <= 4096 and 32 or more batch
+ *    rows; K = 8192 with M of 2049-4096 and 32 or more batch rows;
  *    optional): one 8-byte ticket per set of
  *    32 rows and 16 batch rows, padded to 256 bytes, then fp32 partials
  *    [4, B, M]. It needs no clearing: each ticket carries the call's

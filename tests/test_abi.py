@@ -115,10 +115,11 @@ def test_split_k_workspace_contract(lib):
 
 
 def test_reuse_split_workspace_size(lib):
-    # The reuse path's split-K tiles (K >= 8192 and M <= 2048, or M <= 4096
-    # with 32 or more batch rows): 8-byte tickets per 32 rows x 16 batch
-    # rows, padded to 256 bytes, then fp32 partials [4, B, M]. Zero where the
-    # path streams or does not split.
+    # The reuse path's split-K tiles (K > 8192 with M <= 2048 or with M <=
+    # 4096 and 32 or more batch rows; K = 8192 with M of 2049-4096 and 32 or
+    # more batch rows): 8-byte tickets per 32 rows x 16 batch rows, padded
+    # to 256 bytes, then fp32 partials [4, B, M]. Zero where the path
+    # streams or does not split.
     cfg = _abi.default_config(lib, reuse_weights=1)
     ws = lambda m, k, b: lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(cfg))
     assert ws(4096, 8192, 32) == 2048 + 4 * 32 * 4096 * 4  # 128 x 2 tickets
@@ -127,7 +128,10 @@ def test_reuse_split_workspace_size(lib):
     assert ws(4096, 8192, 16) == 0     # single-pass tiles
     assert ws(6144, 8192, 32) == 0     # single-pass tiles
     assert ws(4096, 4096, 32) == 0     # short rows: single-pass tiles
-    assert ws(4096, 4096, 4) == 0      # streaming kernel
+    assert ws(4096, 4096, 4) == 0      # short rows: single-pass tiles
+    assert ws(2048, 8192, 4) == 0      # streaming kernel
+    assert ws(2048, 8192, 16) == 0     # rows of 8192 at M <= 2048: single-pass tiles
+    assert ws(2048, 8320, 16) == 512 + 4 * 16 * 2048 * 4  # 64 tickets
     assert ws(1024, 8192, 16) == 0     # streaming kernel at small M
     assert ws(8192, 8192, 32) == 0     # two tiles per wave, no split
 

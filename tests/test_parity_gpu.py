@@ -131,16 +131,18 @@ def test_batch_sweep_c3(batch):
 
 
 def test_reuse_small_batches_run_the_streaming_kernel():
-    # Up to four batch rows, up to 8 with M <= 2048, 16 with M <= 1024, 32
-    # with M <= 512 and any with M <= 128: the reuse path runs the streaming
-    # kernel with its batch tiles (stamp 15), so its output is the v5 output
-    # bit for bit. Five rows with M > 2048 take the MFMA tile kernel, which
-    # still meets the oracle's bound.
+    # Up to two batch rows, three below 2^27 weights, four below M = 3072, up
+    # to 8 with M <= 2048, 16 with M <= 1024, 32 with M <= 512 and any with
+    # M <= 128: the reuse path runs the streaming kernel with its batch tiles
+    # (stamp 15), so its output is the v5 output bit for bit. Five rows with
+    # M > 2048 take the MFMA tile kernel, which still meets the oracle's
+    # bound.
     from decode_kernel import _cuda
 
     for (m, k, b) in [(4096, 4096, 1), (4096, 4096, 2), (11008, 4096, 2), (300, 8192, 1),
-                      (512, 8192, 2), (8192, 4096, 3), (9000, 8192, 4), (4096, 4096, 3),
-                      (2000, 8192, 4), (512, 8320, 3), (4096, 11008, 4), (1024, 11008, 6),
+                      (512, 8192, 2), (8192, 4096, 3), (28672, 8192, 2), (4096, 4096, 3),
+                      (2000, 8192, 4), (512, 8320, 3), (8192, 8192, 3), (1024, 11008, 6),
+                      (3000, 8192, 4),
                       (2048, 4224, 8), (40, 197632, 3), (1000, 4224, 16), (500, 4224, 32),
                       (100, 8192, 64)]:
         w, x = oracle.make_case(m, k, b, seed=m + k + b)
@@ -158,13 +160,15 @@ def test_reuse_small_batches_run_the_streaming_kernel():
 
 @pytest.mark.parametrize("m,k,b", [(1100, 65536, 9), (4096, 4096, 8), (4096, 11008, 5),
                                    (8192, 28672, 8), (11008, 4096, 16), (2048, 4096, 12),
-                                   (8216, 4224, 6), (4096, 4096, 16)])
+                                   (8216, 4224, 6), (4096, 4096, 16), (3072, 8192, 4),
+                                   (8192, 16384, 3), (2048, 8192, 16)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
     # The single-pass MFMA tile kernel in each of its shapes (one tile per
-    # wave with blocks of two or four groups; two tiles per wave from
-    # M = 8192, the second of them partly past M at M = 8216; the split form
-    # is test_reuse_split_tiles), long rows of 512 groups, K = 4096 and
-    # K > 4096, one and two tiles of batch rows: a
+    # wave with 16 or 8 waves per tile; two tiles per wave from M = 8192, the
+    # second of them partly past M at M = 8216; the split form is
+    # test_reuse_split_tiles), three and four batch rows on the shapes that
+    # take the tiles there, long rows of 512 groups, K = 4096 and K > 4096,
+    # one and two tiles of batch rows: a
     # one-hot batch row selects single scaled weights bit for bit, scaling x
     # by 2 or -1 scales y exactly (2 up to fp16 subnormal rounding), and rows
     # of a batch do not mix.
@@ -197,10 +201,11 @@ def test_reuse_tile_kernel_exact_properties(m, k, b):
 
 
 @pytest.mark.parametrize("m,k,b", [(4096, 8192, 32), (3000, 8320, 33), (2000, 12416, 17),
-                                   (2048, 8192, 9), (600, 65536, 17)])
+                                   (2048, 8320, 9), (600, 65536, 17)])
 def test_reuse_split_tiles(m, k, b):
-    # The MFMA tiles with K split over four workgroups (reuse path, K >= 8192
-    # and M <= 2048 or 32 or more batch rows, a workspace from the caller;
+    # The MFMA tiles with K split over four workgroups (reuse path, K > 8192
+    # with M <= 2048 or 32 or more batch rows, K = 8192 with M of 2049-4096
+    # and 32 or more batch rows, a workspace from the caller;
     # M = 600 and 3000 end in partial sets of 32 rows): against the oracle,
     # bit-identical on repeated calls and
     # with workspaces full of different garbage (each ticket carries the
