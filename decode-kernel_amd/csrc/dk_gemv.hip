@@ -289,8 +289,13 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
                    const uint16_t* us, const uint4* x, uint16_t* h, int I, int H, int B) {
   if (gate_up_tiles(I, H, B)) {
     const dim3 grid((I + 15) / 16, (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
-    return L("gate/up launch", dk::gate_up_silu_tiles<8, 2>, grid, dim3(8 * 64), 0, g, gs, u, us,
-             x, I, H, B, h);
+    // Paired scale loads up to 8 batch rows, as for the GEMV: I = 11008,
+    // H = 4096, B = 4: 12.28 against 13.67 us; B = 16: 18.95 against 18.56.
+    if (B <= 8 && (H / DK_GROUP_SIZE) % 2 == 0 && aligned(gs, 4) && aligned(us, 4))
+      return L("gate/up launch", dk::gate_up_silu_tiles<8, 2, true>, grid, dim3(8 * 64), 0, g, gs, u,
+               us, x, I, H, B, h);
+    return L("gate/up launch", dk::gate_up_silu_tiles<8, 2, false>, grid, dim3(8 * 64), 0, g, gs, u,
+             us, x, I, H, B, h);
   }
   if (B == 1) {
     // Few rows of up to 8192 weights: one stage of U = 4 per row.
@@ -340,16 +345,29 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 // streaming kernel splits the batch over more workgroups instead. Two tiles
 // per wave share each activation load once there are enough tiles for the
 // chip (M >= 8192); up to M = 4096 one tile per wave with 16 waves per tile,
-// except rows of 8192 weights or more at M <= 2048, and between 4096 and
-// 8192, with 8 (M = 2048, K = 16384, B = 16: 20.05 against 21.51 us;
-// M = K = 4096, B = 16: 7.24 against 7.39 in an earlier form of the kernel).
+// except rows of 8192 weights or more at M <= 2048, with 8 (M = 2048,
+// K = 16384, B = 16: 20.05 against 21.51 us; M = K = 4096, B = 16: 7.24
+// against 7.39 in an earlier form of the kernel); between 4096 and 8192
+// rows, 4 waves, so that 7 workgroups fit a CU (M = 6144, K = 8192: B = 8
+// 12.82 against 13.94 with 8 waves, B = 16 19.13 against 21.10).
 // The weights come through LDS in 128-256 contiguous bytes per row (8-20%
 // faster than loading the MFMA layout directly at M = 11008 or K = 28672).
 template <int KS, int RT, int SG>
 int launch_reuse(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                  int M, int K, int B) {
   const dim3 grid((M + 16 * RT - 1) / (16 * RT), (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
-  return L("reuse launch", dk::gemv_reuse<KS, RT, SG>, grid, dim3(KS * 64), 0, p, s, x, y, M, K, B);
+  // Paired scale loads (fewer registers: 92 against 98 for two tiles per
+  // wave) need an even number of groups per row and 4-byte aligned scales
+  // (the API asks for 2). They pay up to 8 batch rows and between 4096 and
+  // 8192 rows (us, against single scale loads): M = 8192, K = 28672, B = 4
+  // 26.04 (29.73); M = 8192, K = 8192, B = 4 9.84 (11.32); M = K = 4096,
+  // B = 4 4.70 (4.83); level at B = 8; at B = 16 they cost 0-5%
+  // (M = 28672, K = 8192: 46.03 against 43.93).
+  if ((K / DK_GROUP_SIZE) % 2 == 0 && aligned(s, 4) && (B <= 8 || (M > 4096 && M < 8192)))
+    return L("reuse launch", dk::gemv_reuse<KS, RT, SG, true>, grid, dim3(KS * 64), 0, p, s, x, y, M,
+             K, B);
+  return L("reuse launch", dk::gemv_reuse<KS, RT, SG, false>, grid, dim3(KS * 64), 0, p, s, x, y, M,
+           K, B);
 }
 
 // h of the MLP step at the start of its workspace, padded to 256 bytes so
@@ -465,6 +483,7 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
     if (M >= 8192) return launch_reuse<8, 2, 2>(L, p4, scales, x4, y, M, K, B);
     if (M <= 4096 && (M > 2048 || K < 8192))
       return launch_reuse<16, 1, 2>(L, p4, scales, x4, y, M, K, B);
+    if (M > 4096) return launch_reuse<4, 1, 2>(L, p4, scales, x4, y, M, K, B);
     return launch_reuse<8, 1, 2>(L, p4, scales, x4, y, M, K, B);
   }
   const dim3 block4(kWavesPerBlock * 64);

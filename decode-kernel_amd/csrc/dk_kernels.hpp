@@ -597,8 +597,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 // through descriptors rw[t], rs[t], rows 0..15 relative to them, starting at
 // the first of the G groups covered; a row's scales are Gstride apart), SG
 // consecutive groups per block. acc[t] is this lane's part of tile t's fp32
-// 16x16 result over the wave's blocks.
-template <int KS, int RT, int SG>
+// 16x16 result over the wave's blocks. kPairs (two groups per block, an even
+// number of groups per row, 4-byte aligned scales): one 4-byte load brings
+// the scales of both groups of a block, which takes a lane's scale registers
+// from 4 * RT * SG to 4 * RT.
+template <int KS, int RT, int SG, bool kPairs = false>
 __device__ __forceinline__ void reuse_tile_loop(f4_t (&acc)[RT], uint4* wbuf,
                                                 const __amdgpu_buffer_rsrc_t (&rw)[RT],
                                                 const __amdgpu_buffer_rsrc_t (&rs)[RT],
@@ -606,6 +609,7 @@ __device__ __forceinline__ void reuse_tile_loop(f4_t (&acc)[RT], uint4* wbuf,
                                                 int Gstride, int nck, int lane, int wave,
                                                 bool batch_ok) {
   static_assert(SG == 2 || SG == 4, "a block is two or four groups");
+  static_assert(!kPairs || SG == 2, "paired scales take blocks of two groups");
   constexpr int kSlots = SG * 4 + 1;    // 16-byte slots per staged row, one of them padding
   constexpr int kLanesPerRow = SG * 4;  // lanes loading one row's block
   constexpr int kRowsPerLoad = 64 / kLanesPerRow;
@@ -630,7 +634,8 @@ __device__ __forceinline__ void reuse_tile_loop(f4_t (&acc)[RT], uint4* wbuf,
                                               run < G * 64 ? r * nck * 16 + run : kOutOfRange);
     }
     uint4 xv[SG][4];
-    float sc[RT][SG][4];
+    float sc[RT][kPairs ? 1 : SG][4];
+    uint32_t sc2[RT][kPairs ? 4 : 1];
 #pragma unroll
     for (int u = 0; u < SG; ++u) {
       const int g = g0 + u;
@@ -639,16 +644,24 @@ __device__ __forceinline__ void reuse_tile_loop(f4_t (&acc)[RT], uint4* wbuf,
       for (int j = 0; j < 4; ++j) xv[u][j] = buffer_load16<0>(rx, xo + 16 * j);
     }
 #pragma unroll
-    for (int t = 0; t < RT; ++t)
+    for (int t = 0; t < RT; ++t) {
+      if constexpr (kPairs) {
+        // g0 is even and G is even, so g0 + 1 < G as well.
 #pragma unroll
-      for (int u = 0; u < SG; ++u) {
-        const int g = g0 + u;
+        for (int v = 0; v < 4; ++v)
+          sc2[t][v] = __builtin_amdgcn_raw_buffer_load_b32(rs[t], ((4 * kq + v) * Gstride + g0) * 2, 0, 0);
+      } else {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int off = g < G ? ((4 * kq + v) * Gstride + g) * 2 : kOutOfRange;
-          sc[t][u][v] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs[t], off, 0, 0));
+        for (int u = 0; u < SG; ++u) {
+          const int g = g0 + u;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int off = g < G ? ((4 * kq + v) * Gstride + g) * 2 : kOutOfRange;
+            sc[t][u][v] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs[t], off, 0, 0));
+          }
         }
       }
+    }
     // Every load of the block issues before the first wait.
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -669,7 +682,10 @@ __device__ __forceinline__ void reuse_tile_loop(f4_t (&acc)[RT], uint4* wbuf,
           c = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_word_h8(words[j]), xp[j], c, 0, 0, 0);
         // A group past G loaded zero weights and scales, so it adds nothing.
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(c[v], sc[t][u][v], acc[t][v]);
+        for (int v = 0; v < 4; ++v) {
+          const float scale = kPairs ? h2f((uint16_t)(sc2[t][v] >> (16 * u))) : sc[t][kPairs ? 0 : u][v];
+          acc[t][v] = __builtin_fmaf(c[v], scale, acc[t][v]);
+        }
       }
     }
     wave_lds_sync();  // the reads above complete before the next block's writes
@@ -711,7 +727,7 @@ __device__ __forceinline__ void reuse_tile_publish(ReuseLds<KS, RT, SG>& lds, co
 }
 
 // GEMV: tile t of a workgroup is rows row0 + 16 t .. + 15.
-template <int KS, int RT, int SG>
+template <int KS, int RT, int SG, bool kPairs>
 __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ packed,
                                                       const uint16_t* __restrict__ scales,
                                                       const uint4* __restrict__ x4,
@@ -741,7 +757,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ 
   const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
   const int xbase = b < B ? b * K * 2 + kq * 64 : kOutOfRange;
   f4_t acc[RT];
-  reuse_tile_loop<KS, RT, SG>(acc, lds.wst[wave], rw, rs, rx, xbase, G, G, nck, lane, wave,
+  reuse_tile_loop<KS, RT, SG, kPairs>(acc, lds.wst[wave], rw, rs, rx, xbase, G, G, nck, lane, wave,
                               b < B);
   reuse_tile_publish(lds, acc, wave, lane);
   __syncthreads();

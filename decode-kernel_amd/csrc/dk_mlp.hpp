@@ -77,7 +77,7 @@ __global__ __launch_bounds__(W * kWave) void gate_up_silu_lds(
 // serves both matrices and each decoded weight serves up to 16 batch rows.
 // The epilogue adds each tile's wave partials in wave order and forms h from
 // the two fp32 sums, as the streaming kernel above does.
-template <int KS, int SG>
+template <int KS, int SG, bool kPairs>
 __global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles(
     const uint4* __restrict__ gate, const uint16_t* __restrict__ gate_scales,
     const uint4* __restrict__ up, const uint16_t* __restrict__ up_scales,
@@ -101,7 +101,8 @@ __global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles(
   const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * H * 2));
   const int xbase = b < B ? b * H * 2 + kq * 64 : kOutOfRange;
   f4_t acc[2];
-  reuse_tile_loop<KS, 2, SG>(acc, lds.wst[wave], rw, rs, rx, xbase, G, G, nck, lane, wave, b < B);
+  reuse_tile_loop<KS, 2, SG, kPairs>(acc, lds.wst[wave], rw, rs, rx, xbase, G, G, nck, lane, wave,
+                                      b < B);
   reuse_tile_publish(lds, acc, wave, lane);
   __syncthreads();
   if (wave == 0) {

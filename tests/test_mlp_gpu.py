@@ -234,3 +234,31 @@ def test_c_abi_mlp_matches_extension():
     _abi.check(lib, lib.dk_gate_up_silu(gp.data_ptr(), gs.data_ptr(), up.data_ptr(), us.data_ptr(),
                                         x.data_ptr(), hk.data_ptr(), i, h, b, stream))
     assert torch.equal(hk, ws.view(b, i))
+
+
+@pytest.mark.parametrize("i,h,b", [(11008, 4096, 4), (3584, 8192, 8)])
+def test_gate_up_tiles_scale_alignment(i, h, b):
+    # The gate/up tiles load two groups' scales at once up to 8 batch rows
+    # when both scale arrays are 4-byte aligned; 2-byte aligned scales take
+    # 2-byte loads and give the same bits.
+    from decode_kernel import _abi
+
+    lib = _abi.load()
+    (gp, gs, up, us, _, _), _ = _weights(i, h, seed=i + b)
+    x = _x(b, h, seed=b)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def shifted(t):
+        buf = torch.empty(t.numel() + 1, dtype=torch.float16, device="cuda")
+        buf[1:] = t.reshape(-1)
+        assert buf[1:].data_ptr() % 4 == 2
+        return buf
+
+    def call(gsp, usp):
+        hk = torch.empty(b, i, dtype=torch.float16, device="cuda")
+        _abi.check(lib, lib.dk_gate_up_silu(gp.data_ptr(), gsp, up.data_ptr(), usp, x.data_ptr(),
+                                            hk.data_ptr(), i, h, b, stream))
+        return hk
+
+    g2, u2 = shifted(gs), shifted(us)
+    assert torch.equal(call(g2[1:].data_ptr(), u2[1:].data_ptr()), call(gs.data_ptr(), us.data_ptr()))

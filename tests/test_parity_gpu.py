@@ -161,7 +161,8 @@ def test_reuse_small_batches_run_the_streaming_kernel():
 @pytest.mark.parametrize("m,k,b", [(1100, 65536, 9), (4096, 4096, 8), (4096, 11008, 5),
                                    (8192, 28672, 8), (11008, 4096, 16), (2048, 4096, 12),
                                    (8216, 4224, 6), (4096, 4096, 16), (3072, 8192, 4),
-                                   (8192, 16384, 3), (2048, 8192, 16)])
+                                   (8192, 16384, 3), (2048, 8192, 16), (6144, 8192, 16),
+                                   (5000, 4224, 5)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
     # The single-pass MFMA tile kernel in each of its shapes (one tile per
     # wave with 16 or 8 waves per tile; two tiles per wave from M = 8192, the
@@ -198,6 +199,36 @@ def test_reuse_tile_kernel_exact_properties(m, k, b):
         assert np.array_equal(ye[i].view(np.uint16), expect.view(np.uint16)), (i, kk)
     if m * k <= 64 << 20:
         _check_against_oracle(y, oracle.linear_f64(x, packed, scales), f"reuse {m}x{k} B={b}")
+
+
+@pytest.mark.parametrize("m,k,b", [(4096, 4096, 8), (8192, 8192, 4), (6144, 8192, 16),
+                                   (28672, 1024, 5)])
+def test_reuse_tiles_scale_alignment(m, k, b):
+    # With 4-byte aligned scales and an even number of groups per row the
+    # tiles load the scales of two groups at once (up to 8 batch rows, and
+    # between 4096 and 8192 rows); scales that are only 2-byte aligned take
+    # 2-byte loads. Both give the same bits.
+    from decode_kernel import _abi
+
+    lib = _abi.load()
+    w, x = oracle.make_case(m, k, b, seed=m + k + b)
+    packed, scales, pd, sd, xd = _upload(w, x)
+    buf = torch.empty(sd.numel() + 1, dtype=torch.float16, device="cuda")
+    buf[1:] = sd.reshape(-1)
+    shifted = buf[1:]
+    assert shifted.data_ptr() % 4 == 2
+    cfg = _abi.default_config(lib, reuse_weights=1)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def call(sptr):
+        y = torch.empty(b, m, dtype=torch.float16, device="cuda")
+        _abi.check(lib, lib.dk_w4a16_gemv(pd.data_ptr(), sptr, xd.data_ptr(), y.data_ptr(), m, k, b,
+                                          ctypes.byref(cfg), None, 0, stream))
+        return y
+
+    y = call(sd.data_ptr())
+    assert torch.equal(call(shifted.data_ptr()), y)
+    _check_against_oracle(y, oracle.linear_f64(x, packed, scales), f"reuse {m}x{k} B={b}")
 
 
 @pytest.mark.parametrize("m,k,b", [(4096, 8192, 32), (3000, 8320, 33), (2000, 12416, 17),
