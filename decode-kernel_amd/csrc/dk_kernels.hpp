@@ -733,6 +733,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ 
                                                       const uint4* __restrict__ x4,
                                                       uint16_t* __restrict__ y, int M, int K,
                                                       int B) {
+  static_assert(KS >= RT, "wave t sums tile t");
   write_stamp(DK_STAMP_REUSE);
   __shared__ ReuseLds<KS, RT, SG> lds;
   const int G = K >> 7;
@@ -791,6 +792,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_split(
     const uint4* __restrict__ packed, const uint16_t* __restrict__ scales,
     const uint4* __restrict__ x4, uint16_t* __restrict__ y, float* __restrict__ partials,
     unsigned long long* __restrict__ tickets, unsigned gen, int M, int K, int B) {
+  static_assert(KS >= RT, "wave t sums tile t");
   write_stamp(DK_STAMP_REUSE);
   __shared__ ReuseLds<KS, RT, SG> lds;
   __shared__ int last;
