@@ -121,6 +121,15 @@ struct Launch {
 // M = 1024, K = 28672, where R1 U3 W4 is 0.3% faster).
 // At M = 4096 the wide stages lose (M = 4096, K = 11008: R1 U6 W4 7.26
 // against R1 U2 W16 prefetch 6.04).
+// Rows of 4097-8191 weights above 3072 rows: stages of 2048 weights (U = 1,
+// 16 waves) leave less of the last stage empty than stages of 4096 (R1 U2
+// W8, the rule for K <= 4096), 10-22% faster (us):
+//   M = 3328, K = 5120: 4.24 (4.85)     M = 4096, K = 5120: 4.32 (4.98)
+//   M = 4096, K = 6144: 4.35 (5.02)     M = 4608, K = 6144: 5.25 (5.90)
+//   M = 5120, K = 5120: 5.30 (5.89)     M = 6144, K = 6144: 5.43 (6.22)
+//   M = 8192, K = 5120: 5.71 (7.27)     M = 8192, K = 6144: 5.88 (7.53)
+// and rows of 8192 up to 5120 rows take one stage of U = 4 per row:
+// M = 3584: 4.83 (4.89); M = 4096: 5.02 (5.16); M = 5120: 6.11 (6.43).
 template <int R, int U, int W, bool kPrefetch, typename Layout, int kStamp, int NB = 1>
 int launch_lds_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                  int M, int K, int B = 1) {
@@ -140,6 +149,9 @@ int launch_lds(const Launch& L, const uint4* p, const uint16_t* s, const uint4* 
     if (M <= 1024) return launch_lds_t<1, 4, 4, true, Layout, kStamp>(L, p, s, x, y, M, K);
     return launch_lds_t<1, 4, 8, true, Layout, kStamp>(L, p, s, x, y, M, K);
   }
+  if (M <= 8192 && K > 4096 && K < 8192)
+    return launch_lds_t<1, 1, 16, true, Layout, kStamp>(L, p, s, x, y, M, K);
+  if (M <= 5120 && K == 8192) return launch_lds_t<1, 4, 4, true, Layout, kStamp>(L, p, s, x, y, M, K);
   if (M > 8192) {
     if (K <= 8192) return launch_lds_t<2, 2, 4, false, Layout, kStamp>(L, p, s, x, y, M, K);
     return launch_lds_t<2, 1, 8, false, Layout, kStamp>(L, p, s, x, y, M, K);

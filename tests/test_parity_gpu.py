@@ -378,7 +378,8 @@ def test_large_batches_all_paths(batch):
 # dispatch tells apart.
 DISPATCH_SHAPES = [(5000, 1920), (9001, 4224), (8197, 8320), (3000, 8320), (6001, 8320),
                    (2500, 4224), (500, 8320), (1000, 4224), (2000, 12416), (4000, 12416),
-                   (700, 3968), (1500, 6144), (900, 16512), (3072, 2048), (400, 5120)]
+                   (700, 3968), (1500, 6144), (900, 16512), (3072, 2048), (400, 5120),
+                   (5000, 6144), (3200, 5248), (4500, 8192)]
 
 
 @pytest.mark.parametrize("m,k", DISPATCH_SHAPES)
