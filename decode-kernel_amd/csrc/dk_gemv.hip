@@ -130,6 +130,9 @@ struct Launch {
 //   M = 8192, K = 5120: 5.71 (7.27)     M = 8192, K = 6144: 5.88 (7.53)
 // and rows of 8192 up to 5120 rows take one stage of U = 4 per row:
 // M = 3584: 4.83 (4.89); M = 4096: 5.02 (5.16); M = 5120: 6.11 (6.43).
+// Above 8192 rows the same rows take two rows per wave with stages of 2048
+// weights (R2 U1 W8 prefetch): M = 11008, K = 5120: 7.80 (8.73 for R2 U2 W4);
+// M = 13824, K = 5120: 9.27 (9.85).
 template <int R, int U, int W, bool kPrefetch, typename Layout, int kStamp, int NB = 1>
 int launch_lds_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                  int M, int K, int B = 1) {
@@ -153,6 +156,7 @@ int launch_lds(const Launch& L, const uint4* p, const uint16_t* s, const uint4* 
     return launch_lds_t<1, 1, 16, true, Layout, kStamp>(L, p, s, x, y, M, K);
   if (M <= 5120 && K == 8192) return launch_lds_t<1, 4, 4, true, Layout, kStamp>(L, p, s, x, y, M, K);
   if (M > 8192) {
+    if (K > 4096 && K < 8192) return launch_lds_t<2, 1, 8, true, Layout, kStamp>(L, p, s, x, y, M, K);
     if (K <= 8192) return launch_lds_t<2, 2, 4, false, Layout, kStamp>(L, p, s, x, y, M, K);
     return launch_lds_t<2, 1, 8, false, Layout, kStamp>(L, p, s, x, y, M, K);
   }
