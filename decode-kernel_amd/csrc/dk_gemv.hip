@@ -317,6 +317,11 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
     // Few rows of up to 8192 weights: one stage of U = 4 per row.
     if (I <= 2048 && H > 4096 && H <= 8192) return DK_GATE_UP(1, 4, 4, true, 1);
     if (I <= 4096) return H > 4096 ? DK_GATE_UP(1, 1, 16, true, 1) : DK_GATE_UP(1, 2, 4, true, 1);
+    // Rows of 4097-8191 weights: stages of 2048 (us, against R1 U2 W8):
+    // I = 11008, H = 5120: 12.80 (15.34); I = 13824, H = 5120: 14.99
+    // (17.38); I = 14336, H = 6144: 16.47 (18.31); I = 8192, H = 6144: 10.35
+    // (11.69).
+    if (H > 4096 && H < 8192) return DK_GATE_UP(1, 1, 8, true, 1);
     return H <= 4096 ? DK_GATE_UP(1, 2, 4, false, 1) : DK_GATE_UP(1, 2, 8, false, 1);
   }
   if (B == 2) {

@@ -95,7 +95,7 @@ def test_mlp_step_matches_oracle(i, h, b):
 # Ragged shapes in every I range (<= 2048, 4096, above) and H range (<= 4096,
 # 8192, above) the gate/up dispatch tells apart.
 GATE_UP_SHAPES = [(1000, 4224), (2000, 8320), (3000, 4224), (3000, 8320), (5000, 4224),
-                  (4500, 8320), (1800, 6144), (700, 3968)]
+                  (4500, 8320), (1800, 6144), (700, 3968), (5000, 5120)]
 
 
 @pytest.mark.parametrize("i,h", GATE_UP_SHAPES)
