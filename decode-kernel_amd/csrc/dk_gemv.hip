@@ -203,6 +203,22 @@ int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x
   const bool long_rows = K > 8192;
   // Few rows with one-stage rows of up to 8192 weights (U = 4).
   const bool one_wide_stage = K > 4096 && K <= 8192;
+  // Above 2048 rows, rows of 4097-8191 weights take stages of 2048 weights
+  // (us, against the rule for K <= 4096 or K = 8192 in brackets):
+  //   B = 2: M = 4096, K = 6144 4.95 (6.07); M = 5120, K = 5120 5.79 (6.56);
+  //          M = 8192, K = 6144 7.26 (7.34); M = 11008, K = 5120 9.32 (11.60);
+  //          M = 13824, K = 5120 11.78 (14.24)
+  //   B = 4: M = 4096, K = 6144 6.58 (8.32); M = 5120, K = 5120 8.99 (11.31);
+  //          M = 8192, K = 6144 9.62 (12.05); M = 11008, K = 5120 12.79 (13.32)
+  const bool mid_rows = M > 2048 && K > 4096 && K < 8192;
+  if (mid_rows && B == 2) {
+    if (M <= 4096) return DK_BATCH(1, 1, 16, true, 2);
+    if (M <= 6144) return DK_BATCH(1, 1, 8, true, 2);
+    if (M <= 8192) return DK_BATCH(1, 1, 16, true, 2);
+    return DK_BATCH(2, 1, 8, true, 2);
+  }
+  if (mid_rows && B == 3) return DK_BATCH(2, 1, 8, true, 3);
+  if (mid_rows && B == 4) return DK_BATCH(2, 1, 8, true, 4);
   if (B == 2) {
     if (one_wide_stage && M <= 1024) return DK_BATCH(1, 4, 4, true, 2);
     if (one_wide_stage && M <= 2048) return DK_BATCH(2, 4, 4, true, 2);
@@ -359,6 +375,9 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 //   M = 1024, K = 11008: B = 16 14.50 (12.15*), B = 32 14.21 (22.40)
 //   M = 1024, K = 4096:  B = 16 6.62 (5.55*), B = 32 6.60 (9.40)
 //   M = 512, K = 8320:   B = 16 11.63 (6.70*), B = 32 11.47 (11.67*)
+// At rows of 4097-8191 weights from M = 3072 the tiles take three rows too
+// (M = K = 5120: 7.59 against 9.75 us; M = 4096, K = 6144: 5.69 against
+// 7.25; M = 13824, K = 5120: 10.42 against 18.57).
 // The tiles cost about the same from one batch row to five (16 MFMA batch
 // columns), so they take three rows on the 70B shapes (M * K >= 2^27) and
 // four from M = 3072 (within 2% of the streaming kernel at M = 6144,
@@ -430,7 +449,9 @@ int launch_reuse_split(const Launch& L, const uint4* p, const uint16_t* s, const
 enum class ReuseShape { kStream, kTiles };
 
 ReuseShape reuse_shape(int M, int K, int B) {
-  if (B <= 2 || (B == 3 && (size_t)M * (size_t)K < ((size_t)1 << 27)) || (B == 4 && M < 3072) ||
+  const bool mid_rows = M >= 3072 && K > 4096 && K < 8192;
+  if (B <= 2 || (B == 3 && !mid_rows && (size_t)M * (size_t)K < ((size_t)1 << 27)) ||
+      (B == 4 && M < 3072) ||
       (B <= 8 && M <= 2048) || (B <= 16 && M <= 1024) || (B <= 32 && M <= 512) || M <= 128)
     return ReuseShape::kStream;
   return ReuseShape::kTiles;

@@ -575,7 +575,8 @@ __global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
 // partials are added in LDS in wave order. Loads are raw buffer loads; rows
 // past M, groups past G and batch rows past B read zero through out-of-range
 // offsets.
-// For up to two batch rows (three below 2^27 weights, four below M = 3072),
+// For up to two batch rows (three below 2^27 weights unless rows of
+// 4097-8191 weights and M >= 3072, four below M = 3072),
 // and more at small M (up to 8 rows at M <= 2048, 16 at M <= 1024, 32 at
 // M <= 512, any at M <= 128), the reuse path runs the streaming kernel above
 // instead (each decoded weight still serves every batch row of its tile):

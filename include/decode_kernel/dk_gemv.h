@@ -52,10 +52,11 @@ typedef struct dk_gemv_config {
   int version;       /* dk_kernel_version, 0..5 */
   int split_k;       /* v4 only, 1..32; ignored otherwise */
   int reuse_weights; /* nonzero: weight-reuse path, ignores version: MFMA tiles
-                        from 5 batch rows (3 at M * K >= 2^27, 4 at
-                        M >= 3072; 9 at M <= 2048, 17 at M <= 1024, 33 at
-                        M <= 512, none at M <= 128), the v5 kernel with
-                        batch tiles below that (stamp 15) */
+                        from 5 batch rows (3 at M * K >= 2^27 or with
+                        4096 < K < 8192 and M >= 3072, 4 at M >= 3072; 9 at
+                        M <= 2048, 17 at M <= 1024, 33 at M <= 512, none at
+                        M <= 128), the v5 kernel with batch tiles below that
+                        (stamp 15) */
   int warps_per_row; /* v1 only, 1..8: wave64s sharing one row's K */
 } dk_gemv_config;
 

@@ -131,7 +131,8 @@ def test_batch_sweep_c3(batch):
 
 
 def test_reuse_small_batches_run_the_streaming_kernel():
-    # Up to two batch rows, three below 2^27 weights, four below M = 3072, up
+    # Up to two batch rows, three below 2^27 weights (but not with rows of
+    # 4097-8191 weights at M >= 3072), four below M = 3072, up
     # to 8 with M <= 2048, 16 with M <= 1024, 32 with M <= 512 and any with
     # M <= 128: the reuse path runs the streaming kernel with its batch tiles
     # (stamp 15), so its output is the v5 output bit for bit. Five rows with
@@ -162,7 +163,7 @@ def test_reuse_small_batches_run_the_streaming_kernel():
                                    (8192, 28672, 8), (11008, 4096, 16), (2048, 4096, 12),
                                    (8216, 4224, 6), (4096, 4096, 16), (3072, 8192, 4),
                                    (8192, 16384, 3), (2048, 8192, 16), (6144, 8192, 16),
-                                   (5000, 4224, 5)])
+                                   (5000, 4224, 5), (5120, 5120, 3)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
     # The single-pass MFMA tile kernel in each of its shapes (one tile per
     # wave with 16 or 8 waves per tile; two tiles per wave from M = 8192, the
