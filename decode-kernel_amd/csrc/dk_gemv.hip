@@ -449,8 +449,11 @@ int launch_reuse_split(const Launch& L, const uint4* p, const uint16_t* s, const
 enum class ReuseShape { kStream, kTiles };
 
 ReuseShape reuse_shape(int M, int K, int B) {
-  const bool mid_rows = M >= 3072 && K > 4096 && K < 8192;
-  if (B <= 2 || (B == 3 && !mid_rows && (size_t)M * (size_t)K < ((size_t)1 << 27)) ||
+  // Three batch rows take the tiles on large matrices and, from 3072 rows,
+  // on rows of 4097-8191 weights.
+  const bool three_rows_tiles =
+      (size_t)M * (size_t)K >= ((size_t)1 << 27) || (M >= 3072 && K > 4096 && K < 8192);
+  if (B <= 2 || (B == 3 && !three_rows_tiles) ||
       (B == 4 && M < 3072) ||
       (B <= 8 && M <= 2048) || (B <= 16 && M <= 1024) || (B <= 32 && M <= 512) || M <= 128)
     return ReuseShape::kStream;
