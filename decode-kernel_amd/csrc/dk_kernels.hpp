@@ -557,8 +557,10 @@ __global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
 // Weight-reuse path (stamp 15): each decoded weight is used for up to 16
 // batch rows at once by v_mfma_f32_16x16x32_f16, so latency is nearly flat
 // in B instead of the reference's O(B) re-decode (csrc/gemv_w4a16.cu:364-413).
-// A workgroup of KS waves owns one 16-row tile; wave w takes the blocks of
-// four consecutive groups w, w + KS, ... The MFMA operands:
+// A workgroup of KS waves owns RT 16-row tiles (one or two; with two, each
+// activation load serves both); wave w takes the blocks of SG consecutive
+// groups (two in every shape used) starting at groups SG w, SG (w + KS), ...
+// The MFMA operands:
 //   A (16x32, weights): lane l -> row l%16, 8 k-slots of lane group l/16
 //   B (32x16, x):       lane l -> batch l%16, same 8 k-slots
 //   D (16x16):          lane l -> rows 4(l/16)+v, batch l%16
@@ -566,15 +568,17 @@ __global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
 // four words = four MFMA k-steps that together cover exactly group g, so
 // the fp32 tile result of a group is scaled once and accumulated. Loading
 // those 16 bytes directly (one instruction reads 64 bytes from each of 16
-// rows) is slow at long rows; instead each block's weights come in four
-// instructions of 4 rows x 256 contiguous bytes, go through a wave-private
-// LDS buffer (one pad slot per row against bank conflicts) and are read back
-// in the A layout. Measured against the direct loads on MI355X: 8-20%
-// faster at M = 11008 or K = 28672 and 3-8% at M = K = 4096 for 5-16 batch
-// rows. Each lane loads the scales of its four D rows directly. The KS wave
-// partials are added in LDS in wave order. Loads are raw buffer loads; rows
-// past M, groups past G and batch rows past B read zero through out-of-range
-// offsets.
+// rows) is slow at long rows; instead each block's weights come in
+// instructions of 64 / (4 SG) rows x 64 SG contiguous bytes (8 rows x 128
+// bytes for two groups), go through a wave-private LDS buffer (one pad slot
+// per row against bank conflicts) and are read back in the A layout.
+// Measured against the direct loads on MI355X: 8-20% faster at M = 11008 or
+// K = 28672 and 3-8% at M = K = 4096 for 5-16 batch rows. Each lane loads
+// the scales of its four D rows directly (a block's two groups in one 4-byte
+// load where the scales allow). Each wave stores its partials over its own
+// staging buffer and the KS of them are added in wave order. Loads are raw
+// buffer loads through wave-uniform descriptors; rows past M, groups past G
+// and batch rows past B read zero through out-of-range offsets.
 // For up to two batch rows (three below 2^27 weights unless rows of
 // 4097-8191 weights and M >= 3072, four below M = 3072),
 // and more at small M (up to 8 rows at M <= 2048, 16 at M <= 1024, 32 at
