@@ -389,7 +389,13 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 // K = 16384, B = 16: 20.05 against 21.51 us; M = K = 4096, B = 16: 7.24
 // against 7.39 in an earlier form of the kernel); between 4096 and 8192
 // rows, 4 waves, so that 7 workgroups fit a CU (M = 6144, K = 8192: B = 8
-// 12.82 against 13.94 with 8 waves, B = 16 19.13 against 21.10).
+// 12.82 against 13.94 with 8 waves, B = 16 19.13 against 21.10). From 2049
+// to 4096 rows, with the paired scale loads and uniform descriptors, 8 waves
+// now beat 16 up to 8 batch rows, and blocks of four groups beat two above
+// (us, 16 waves with blocks of two in brackets): M = K = 4096: B = 8 5.02
+// (5.19), B = 16 6.77 with 8 waves (6.87); M = 4096, K = 11008: B = 5 8.40
+// (8.60), B = 16 15.25 with 16 waves (15.77); M = 3072, K = 8192: B = 8 7.74
+// (7.98), B = 16 11.39 (12.17).
 // The weights come through LDS in 128-256 contiguous bytes per row (8-20%
 // faster than loading the MFMA layout directly at M = 11008 or K = 28672).
 template <int KS, int RT, int SG>
@@ -403,9 +409,11 @@ int launch_reuse(const Launch& L, const uint4* p, const uint16_t* s, const uint4
   // 26.04 (29.73); M = 8192, K = 8192, B = 4 9.84 (11.32); M = K = 4096,
   // B = 4 4.70 (4.83); level at B = 8; at B = 16 they cost 0-5%
   // (M = 28672, K = 8192: 46.03 against 43.93).
-  if ((K / DK_GROUP_SIZE) % 2 == 0 && aligned(s, 4) && (B <= 8 || (M > 4096 && M < 8192)))
-    return L("reuse launch", dk::gemv_reuse<KS, RT, SG, true>, grid, dim3(KS * 64), 0, p, s, x, y, M,
-             K, B);
+  if constexpr (SG == 2) {
+    if ((K / DK_GROUP_SIZE) % 2 == 0 && aligned(s, 4) && (B <= 8 || (M > 4096 && M < 8192)))
+      return L("reuse launch", dk::gemv_reuse<KS, RT, SG, true>, grid, dim3(KS * 64), 0, p, s, x, y,
+               M, K, B);
+  }
   return L("reuse launch", dk::gemv_reuse<KS, RT, SG, false>, grid, dim3(KS * 64), 0, p, s, x, y, M,
            K, B);
 }
@@ -526,9 +534,13 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
       return launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B);
     if (split) return launch_reuse_split(L, p4, scales, x4, y, M, K, B, workspace);
     if (M >= 8192) return launch_reuse<8, 2, 2>(L, p4, scales, x4, y, M, K, B);
-    if (M <= 4096 && (M > 2048 || K < 8192))
-      return launch_reuse<16, 1, 2>(L, p4, scales, x4, y, M, K, B);
     if (M > 4096) return launch_reuse<4, 1, 2>(L, p4, scales, x4, y, M, K, B);
+    if (M > 2048) {
+      if (B <= 8) return launch_reuse<8, 1, 2>(L, p4, scales, x4, y, M, K, B);
+      return K <= 4096 ? launch_reuse<8, 1, 4>(L, p4, scales, x4, y, M, K, B)
+                       : launch_reuse<16, 1, 4>(L, p4, scales, x4, y, M, K, B);
+    }
+    if (K < 8192) return launch_reuse<16, 1, 2>(L, p4, scales, x4, y, M, K, B);
     return launch_reuse<8, 1, 2>(L, p4, scales, x4, y, M, K, B);
   }
   const dim3 block4(kWavesPerBlock * 64);
