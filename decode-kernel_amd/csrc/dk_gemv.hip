@@ -260,8 +260,9 @@ int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x
 
 // Batches that the MFMA tiles take on the fused gate/up step. Tiles against
 // the streaming kernel's batch tiles in brackets (us per launch, both
-// matrices; 8 waves, blocks of two groups, chosen over 4 waves with blocks
-// of two or four; * marks the streaming kernel where it is chosen):
+// matrices; 8 waves, blocks of two groups, chosen over 4 or 16 waves with
+// blocks of two and 8 waves with blocks of four, 2-40% slower at B = 4, 8
+// and 16 on five shapes; * marks the streaming kernel where it is chosen):
 //                        B = 3           B = 4           B = 5           B = 8           B = 16
 //   I = 11008, H = 4096: 13.62 (14.92)   13.77 (19.25)   13.78 (24.31)   14.62 (31.51)   18.72 (58.31)
 //   I = 3584,  H = 8192: 11.07 (10.74*)  11.15 (12.64)   11.39 (18.88)   11.96 (23.55)   13.89 (45.13)
