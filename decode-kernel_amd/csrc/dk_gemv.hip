@@ -390,7 +390,12 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 // K = 16384, B = 16: 20.05 against 21.51 us; M = K = 4096, B = 16: 7.24
 // against 7.39 in an earlier form of the kernel); between 4096 and 8192
 // rows, 4 waves, so that 7 workgroups fit a CU (M = 6144, K = 8192: B = 8
-// 12.82 against 13.94 with 8 waves, B = 16 19.13 against 21.10). From 2049
+// 12.82 against 13.94 with 8 waves), and from 9 batch rows two tiles per
+// wave with blocks of four groups, 16-31% faster (us, B = 16, against 4
+// waves with one tile and blocks of two): M = K = 5120 10.13 (13.55);
+// M = 6144, K = 4096 8.21 (11.13); M = 4608, K = 8192 14.29 (18.96);
+// M = 7168, K = 8192 15.23 (19.30); M = 6144, K = 14336 22.90 (31.75);
+// M = 5120, K = 13824 21.39 (31.15); M = 6144, K = 8192 14.76 (19.07). From 2049
 // to 4096 rows, with the paired scale loads and uniform descriptors, 8 waves
 // now beat 16 up to 8 batch rows, and blocks of four groups beat two above
 // (us, 16 waves with blocks of two in brackets): M = K = 4096: B = 8 5.02
@@ -535,7 +540,10 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
       return launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B);
     if (split) return launch_reuse_split(L, p4, scales, x4, y, M, K, B, workspace);
     if (M >= 8192) return launch_reuse<8, 2, 2>(L, p4, scales, x4, y, M, K, B);
-    if (M > 4096) return launch_reuse<4, 1, 2>(L, p4, scales, x4, y, M, K, B);
+    if (M > 4096) {
+      if (B > 8) return launch_reuse<8, 2, 4>(L, p4, scales, x4, y, M, K, B);
+      return launch_reuse<4, 1, 2>(L, p4, scales, x4, y, M, K, B);
+    }
     if (M > 2048) {
       if (B <= 8) return launch_reuse<8, 1, 2>(L, p4, scales, x4, y, M, K, B);
       return K <= 4096 ? launch_reuse<8, 1, 4>(L, p4, scales, x4, y, M, K, B)

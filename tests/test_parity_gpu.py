@@ -163,7 +163,8 @@ def test_reuse_small_batches_run_the_streaming_kernel():
                                    (8192, 28672, 8), (11008, 4096, 16), (2048, 4096, 12),
                                    (8216, 4224, 6), (4096, 4096, 16), (3072, 8192, 4),
                                    (8192, 16384, 3), (2048, 8192, 16), (6144, 8192, 16),
-                                   (5000, 4224, 5), (5120, 5120, 3), (3000, 8320, 16)])
+                                   (5000, 4224, 5), (5120, 5120, 3), (3000, 8320, 16),
+                                   (4500, 5248, 12)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
     # The single-pass MFMA tile kernel in each of its shapes (one tile per
     # wave with 16 or 8 waves per tile; two tiles per wave from M = 8192, the
