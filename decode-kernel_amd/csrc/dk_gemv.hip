@@ -385,13 +385,16 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 // K = 8192); M / 16 tiles leave most CUs idle at small M, where the
 // streaming kernel splits the batch over more workgroups instead. Two tiles
 // per wave share each activation load once there are enough tiles for the
-// chip (M >= 8192); up to M = 4096 one tile per wave with 16 waves per tile,
+// chip (M > 4096); up to M = 4096 one tile per wave with 16 waves per tile,
 // except rows of 8192 weights or more at M <= 2048, with 8 (M = 2048,
 // K = 16384, B = 16: 20.05 against 21.51 us; M = K = 4096, B = 16: 7.24
 // against 7.39 in an earlier form of the kernel); between 4096 and 8192
-// rows, 4 waves, so that 7 workgroups fit a CU (M = 6144, K = 8192: B = 8
-// 12.82 against 13.94 with 8 waves), and from 9 batch rows two tiles per
-// wave with blocks of four groups, 16-31% faster (us, B = 16, against 4
+// rows, two tiles per wave as well: up to 8 batch rows with blocks of two
+// groups, 11-21% faster than 4 waves with one tile (us, B = 4 and 8):
+// M = K = 5120 6.57 (7.72), 7.78 (9.18); M = 4608, K = 8192 8.85 (10.88),
+// 10.98 (12.74); M = 7168, K = 8192 9.57 (11.37), 11.37 (13.01);
+// M = 6144, K = 14336 13.70 (17.35), 17.24 (20.74); from 9 batch rows
+// with blocks of four groups, 16-31% faster (us, B = 16, against 4
 // waves with one tile and blocks of two): M = K = 5120 10.13 (13.55);
 // M = 6144, K = 4096 8.21 (11.13); M = 4608, K = 8192 14.29 (18.96);
 // M = 7168, K = 8192 15.23 (19.30); M = 6144, K = 14336 22.90 (31.75);
@@ -410,13 +413,13 @@ int launch_reuse(const Launch& L, const uint4* p, const uint16_t* s, const uint4
   const dim3 grid((M + 16 * RT - 1) / (16 * RT), (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
   // Paired scale loads (fewer registers: 92 against 98 for two tiles per
   // wave) need an even number of groups per row and 4-byte aligned scales
-  // (the API asks for 2). They pay up to 8 batch rows and between 4096 and
-  // 8192 rows (us, against single scale loads): M = 8192, K = 28672, B = 4
+  // (the API asks for 2). They pay up to 8 batch rows (us, against single
+  // scale loads): M = 8192, K = 28672, B = 4
   // 26.04 (29.73); M = 8192, K = 8192, B = 4 9.84 (11.32); M = K = 4096,
   // B = 4 4.70 (4.83); level at B = 8; at B = 16 they cost 0-5%
   // (M = 28672, K = 8192: 46.03 against 43.93).
   if constexpr (SG == 2) {
-    if ((K / DK_GROUP_SIZE) % 2 == 0 && aligned(s, 4) && (B <= 8 || (M > 4096 && M < 8192)))
+    if ((K / DK_GROUP_SIZE) % 2 == 0 && aligned(s, 4) && B <= 8)
       return L("reuse launch", dk::gemv_reuse<KS, RT, SG, true>, grid, dim3(KS * 64), 0, p, s, x, y,
                M, K, B);
   }
@@ -539,11 +542,8 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
     if (reuse_shape(M, K, B) == ReuseShape::kStream)
       return launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B);
     if (split) return launch_reuse_split(L, p4, scales, x4, y, M, K, B, workspace);
-    if (M >= 8192) return launch_reuse<8, 2, 2>(L, p4, scales, x4, y, M, K, B);
-    if (M > 4096) {
-      if (B > 8) return launch_reuse<8, 2, 4>(L, p4, scales, x4, y, M, K, B);
-      return launch_reuse<4, 1, 2>(L, p4, scales, x4, y, M, K, B);
-    }
+    if (M > 4096 && M < 8192 && B > 8) return launch_reuse<8, 2, 4>(L, p4, scales, x4, y, M, K, B);
+    if (M > 4096) return launch_reuse<8, 2, 2>(L, p4, scales, x4, y, M, K, B);
     if (M > 2048) {
       if (B <= 8) return launch_reuse<8, 1, 2>(L, p4, scales, x4, y, M, K, B);
       return K <= 4096 ? launch_reuse<8, 1, 4>(L, p4, scales, x4, y, M, K, B)
