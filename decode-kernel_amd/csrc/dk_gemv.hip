@@ -251,6 +251,12 @@ int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x
     if (M <= 4096 || K > 4096) return DK_BATCH(2, 1, 16, true, 3);
     return DK_BATCH(2, 2, 8, false, 3);
   }
+  // Seven or eight rows of 4097-8191 weights at 513-2048 rows: stages of
+  // 2048 weights in two four-row tiles (us, B = 8): M = 2048, K = 5120 6.26
+  // (7.36); M = 1536, K = 6144 6.19 (7.25); M = 1024, K = 6144 4.90 (5.52);
+  // level at M = 400, K = 5120 (5.07 against 5.02).
+  if (B <= 8 && M > 512 && M <= 2048 && K > 4096 && K < 8192)
+    return M <= 1024 ? DK_BATCH(1, 1, 8, true, 4) : DK_BATCH(1, 1, 16, true, 4);
   if (M <= 1024) return DK_BATCH(1, 2, 8, true, 2);
   if (M <= 2048) return DK_BATCH(2, 2, 8, true, 4);
   if (M <= 4096) return DK_BATCH(2, 1, 16, true, 4);
