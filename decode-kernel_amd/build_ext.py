@@ -6,6 +6,7 @@
 Outputs (next to the Python package so they travel with the source tree):
     decode_kernel/libdk_hip.so   hipcc --offload-arch=gfx950: kernels + C ABI
     decode_kernel/_cuda*.so      g++: pybind/torch binding linked to libdk_hip.so
+    dk_bench/libdk_bench.so      hipcc: measurement-only kernels (not the product)
     _build/*.s                   device assembly for inspection (with --asm)
 
 Replaces the reference's nvcc CUDAExtension (setup.py:47-76). No hipify pass
@@ -51,6 +52,11 @@ HIP_FLAGS = [
 ]
 
 LIB = PKG / "libdk_hip.so"
+# Measurement-only kernels (read-floor probes, the load-only ablation, the
+# one-stage and split-K shape variants): dk_bench/libdk_bench.so, never
+# linked into the product library.
+BENCH_SOURCES = [CSRC / "bench" / "dk_bench_kernels.hip"]
+BENCH_LIB = PKG_ROOT / "dk_bench" / "libdk_bench.so"
 
 
 def ext_path() -> Path:
@@ -79,6 +85,15 @@ def build_lib() -> Path:
          quiet_warning="packed-fp32-ops' is not a recognized feature")
     os.replace(tmp, LIB)
     return LIB
+
+
+def build_bench_lib() -> Path:
+    tmp = BENCH_LIB.with_suffix(".so.tmp")
+    _run([hipcc(), *HIP_FLAGS, "-fvisibility=hidden", "-shared", f"-I{INCLUDE}", f"-I{CSRC}",
+          *map(str, BENCH_SOURCES), "-o", str(tmp)],
+         quiet_warning="packed-fp32-ops' is not a recognized feature")
+    os.replace(tmp, BENCH_LIB)
+    return BENCH_LIB
 
 
 def build_asm() -> list[Path]:
@@ -129,6 +144,7 @@ def build_binding() -> Path:
 def build(asm: bool = False) -> None:
     build_lib()
     build_binding()
+    build_bench_lib()
     if asm:
         build_asm()
 
@@ -137,9 +153,12 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--asm", action="store_true", help="also write device assembly to _build/")
     ap.add_argument("--lib-only", action="store_true", help="only build libdk_hip.so")
+    ap.add_argument("--bench-only", action="store_true", help="only build dk_bench/libdk_bench.so")
     args = ap.parse_args()
     if args.lib_only:
         build_lib()
+    elif args.bench_only:
+        build_bench_lib()
     else:
         build(asm=args.asm)
     return 0

@@ -1,0 +1,402 @@
+// Measurement-only kernels for the benchmark tools (dk_bench), built into
+// dk_bench/libdk_bench.so and never linked into the product library.
+//
+//  * read-floor probes: one pass over a buffer with L 16-byte loads per lane
+//    all issued before the first wait, over a chosen grid, with or without
+//    the non-temporal hint: the fastest a kernel that only reads N bytes can
+//    run on this part, per launch;
+//  * the load-only ablation of the streaming GEMV: the product kernel
+//    (gemv_v5_lds) with its decode and products replaced (same loads, LDS
+//    stages, grid and reduction), to separate the arithmetic from the
+//    bandwidth (the open question of the reference's README.md:44);
+//  * one-stage GEMV variants for short rows (K <= 4096): activations through
+//    LDS or per wave in registers, weights issued first or last, one or two
+//    waves per row;
+//  * every instance of the split-K kernel (gemv_v4_lds) that the v4 shape
+//    sweep times, including one that stores its partials and stops, which
+//    prices the cross-workgroup reduction.
+// Outputs of the ablation kernels are meaningless by design; every other
+// kernel here computes the GEMV (checked against the product by the tools).
+#include <hip/hip_runtime.h>
+
+#include "dk_kernels.hpp"
+
+#define DKB_API extern "C" __attribute__((visibility("default")))
+
+namespace dkb {
+
+using namespace dk;
+
+// ---------------------------------------------------------------------------
+// Read-floor probe. Lane g of the grid (g = block * T + thread) reads 16-byte
+// pieces g, g + P, ..., g + (L - 1) P of each pass, P = G T lanes, all L
+// loads issued before the first is used; passes repeat until the buffer
+// ends. Pieces past the end read zero (out-of-range buffer offsets). Each
+// wave writes one fp32 sum to partials[block * T / 64 + wave].
+// ---------------------------------------------------------------------------
+template <int L, bool kNt>
+__global__ __launch_bounds__(1024) void read_probe(const uint4* __restrict__ src, unsigned bytes,
+                                                   float* __restrict__ partials) {
+  const auto r = buffer_rsrc(src, bytes);
+  const unsigned P = gridDim.x * blockDim.x;
+  const unsigned g = blockIdx.x * blockDim.x + threadIdx.x;
+  const unsigned pieces = bytes / 16;
+  float a = 0.f;
+  for (unsigned base = 0; base < pieces; base += P * L) {
+    uint4 v[L];
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+      const unsigned p = base + g + (unsigned)i * P;
+      v[i] = buffer_load16<kNt ? kLoadNonTemporal : 0>(r, p < pieces ? (int)(p * 16) : kOutOfRange);
+    }
+#pragma unroll
+    for (int i = 0; i < L; ++i)
+      a += __builtin_bit_cast(float, v[i].x ^ v[i].y) + __builtin_bit_cast(float, v[i].z ^ v[i].w);
+  }
+  a = wave_sum(a);
+  if ((threadIdx.x & 63) == 63) partials[(blockIdx.x * blockDim.x + threadIdx.x) / 64] = a;
+}
+
+// ---------------------------------------------------------------------------
+// Ablation maths for the stage loop (see StageMath). Both keep every load of
+// the product kernel live by folding the loaded words into the result.
+//  NoDecode: reads the stage's activation pieces from LDS as the product
+//            does and XOR-folds them with the weight words (two logic ops
+//            per word instead of the decode and four v_dot2);
+//  LoadsOnly: folds only the weight words and scales (no LDS reads).
+// ---------------------------------------------------------------------------
+struct MathNoDecode {
+  template <int R, int U, int W, int NB, typename Layout>
+  static __device__ __forceinline__ void compute(const LdsStage<R, U, W, NB>& st,
+                                                 const uint4 (&xs)[LdsActsT<U, NB>::kSlots],
+                                                 float (&acc)[NB][R], int lane) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        uint32_t h[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) h[r] = 0u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint4 pv = xs[((b * U + u) * 4 + j) * kWave + lane];
+          const uint32_t xw = pv.x ^ pv.y ^ pv.z ^ pv.w;
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            const uint32_t words[4] = {st.w[u][r].x, st.w[u][r].y, st.w[u][r].z, st.w[u][r].w};
+            h[r] ^= words[j] ^ xw;
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          acc[b][r] += h2f((uint16_t)st.s[u][r]) * (float)(h[r] & 0xFFu);
+      }
+  }
+};
+
+struct MathLoadsOnly {
+  template <int R, int U, int W, int NB, typename Layout>
+  static __device__ __forceinline__ void compute(const LdsStage<R, U, W, NB>& st,
+                                                 const uint4 (&)[LdsActsT<U, NB>::kSlots],
+                                                 float (&acc)[NB][R], int) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint32_t h = st.w[u][r].x ^ st.w[u][r].y ^ st.w[u][r].z ^ st.w[u][r].w;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[b][r] += h2f((uint16_t)st.s[u][r]) * (float)(h & 0xFFu);
+      }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// One-stage GEMV for rows of up to S * U * 2048 weights, one batch row: each
+// row is taken by S waves (wave s of the row takes chunks [64 U s, 64 U
+// (s + 1)), lane l its chunks 64 U s + 64 u + l), W waves per workgroup, so
+// W / S rows per workgroup. kLds: the workgroup loads the activations once,
+// pairs them and shares them through LDS (the product's stage); otherwise
+// each wave loads its own chunks' activations (four 16-byte loads per chunk,
+// L1/L2 hits after the first wave) and pairs them in registers.
+// kWeightsFirst: the weight loads issue before the activation and scale
+// loads (with LDS the publish then waits for the weights too: loads return
+// in order). With S = 2 the two halves' fp32 sums are added in wave order
+// through LDS. Workgroups are renumbered per XCD as in v5.
+// ---------------------------------------------------------------------------
+template <int U, int W, int S, bool kLds, bool kWeightsFirst>
+__global__ __launch_bounds__(W * kWave) void gemv_onestage(const uint4* __restrict__ packed,
+                                                           const uint16_t* __restrict__ scales,
+                                                           const uint4* __restrict__ x4,
+                                                           uint16_t* __restrict__ y, int M, int K) {
+  static_assert(W % S == 0, "whole rows per workgroup");
+  constexpr int kRowsPerWg = W / S;
+  constexpr int kChunks = S * U * kWave;  // chunks of one stage (the whole row)
+  __shared__ uint4 xs[kLds ? kChunks * 4 : 1];
+  __shared__ float red[W];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wg = xcd_contiguous_block(blockIdx.x, (M + kRowsPerWg - 1) / kRowsPerWg);
+  const int row = wg * kRowsPerWg + wave % kRowsPerWg;
+  const int half = wave / kRowsPerWg;  // which part of the row this wave takes
+  const bool active = row < M;
+  const int nck = K >> 5;
+  const int G = K >> 7;
+  const auto rw = buffer_rsrc(packed + (size_t)(active ? row : 0) * nck, active ? (uint32_t)(K / 2) : 0u);
+  const auto rs = buffer_rsrc(scales + (size_t)(active ? row : 0) * G, active ? (uint32_t)(G * 2) : 0u);
+  const auto rx = buffer_rsrc(x4, (uint32_t)(K * 2));
+
+  uint4 w[U];
+  uint32_t sc[U];
+  uint4 xv[kLds ? (kChunks * 4 + W * kWave - 1) / (W * kWave) : 4 * U];
+  constexpr int kXLoads = sizeof(xv) / sizeof(uint4);
+  auto load_w = [&]() {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = (half * U + u) * kWave + lane;
+      sc[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, c < nck ? (c >> 2) * 2 : kOutOfRange, 0, 0);
+      w[u] = buffer_load16<kLoadNonTemporal>(rw, c < nck ? c * 16 : kOutOfRange);
+    }
+  };
+  auto load_x = [&]() {
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i) {
+      if constexpr (kLds) {
+        const int piece = tid + i * W * kWave;  // 16-byte piece of the row's activations
+        xv[i] = buffer_load16<0>(rx, piece < kChunks * 4 && (piece >> 2) < nck ? piece * 16 : kOutOfRange);
+      } else {
+        const int c = (half * U + i / 4) * kWave + lane;
+        xv[i] = buffer_load16<0>(rx, c < nck ? (c * 4 + (i & 3)) * 16 : kOutOfRange);
+      }
+    }
+  };
+  if constexpr (kWeightsFirst) {
+    load_w();
+    load_x();
+  } else {
+    load_x();
+    load_w();
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  h2_t xp[U][4][4];
+  if constexpr (kLds) {
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i) {
+      const int piece = tid + i * W * kWave;
+      if (piece < kChunks * 4) {
+        h2_t p[4];
+        pair_x(xv[i], p);
+        // slot (chunk c, piece j) at (j * kChunks + c): lane-consecutive reads
+        xs[(piece & 3) * kChunks + (piece >> 2)] =
+            make_uint4(__builtin_bit_cast(uint32_t, p[0]), __builtin_bit_cast(uint32_t, p[1]),
+                       __builtin_bit_cast(uint32_t, p[2]), __builtin_bit_cast(uint32_t, p[3]));
+      }
+    }
+    lds_barrier();
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 pv = xs[j * kChunks + (half * U + u) * kWave + lane];
+        xp[u][j][0] = as_h2(pv.x);
+        xp[u][j][1] = as_h2(pv.y);
+        xp[u][j][2] = as_h2(pv.z);
+        xp[u][j][3] = as_h2(pv.w);
+      }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pair_x(xv[4 * u + j], xp[u][j]);
+  }
+  float acc = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t words[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) part = dot_word(words[j], xp[u][j], part);
+    acc = __builtin_fmaf(part, h2f((uint16_t)sc[u]), acc);
+  }
+  const float t = wave_sum(acc);
+  if constexpr (S == 1) {
+    if (active && lane == 63) y[row] = f2h(t);
+  } else {
+    if (lane == 63) red[wave] = t;
+    __syncthreads();
+    if (half == 0 && active && lane == 63) {
+      float sum = 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s) sum += red[s * kRowsPerWg + wave];
+      y[row] = f2h(sum);
+    }
+  }
+}
+
+}  // namespace dkb
+
+namespace {
+
+int launch_error(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    fprintf(stderr, "%s: %s\n", what, hipGetErrorString(e));
+    return 2;
+  }
+  return 0;
+}
+
+}  // namespace
+
+// Read-floor probe: `blocks` workgroups of `threads` (64..1024, multiple of
+// 64) lanes, `loads` (1, 2, 4, 8) loads per lane per pass, nt = non-temporal
+// hint. `partials` holds blocks * threads / 64 floats. Returns 0 or an error.
+DKB_API int dkb_read_probe(const void* src, size_t bytes, float* partials, int blocks, int threads,
+                           int loads, int nt, hipStream_t stream) {
+  if (!src || !partials || bytes % 16 || bytes > 0x7fffffffu || blocks < 1 || threads < 64 ||
+      threads > 1024 || threads % 64)
+    return 1;
+  const auto* s = static_cast<const uint4*>(src);
+  const unsigned b = (unsigned)bytes;
+#define DKB_READ(L)                                                                         \
+  if (nt)                                                                                    \
+    hipLaunchKernelGGL((dkb::read_probe<L, true>), dim3(blocks), dim3(threads), 0, stream, s, b, \
+                       partials);                                                            \
+  else                                                                                       \
+    hipLaunchKernelGGL((dkb::read_probe<L, false>), dim3(blocks), dim3(threads), 0, stream, s, b, \
+                       partials);
+  switch (loads) {
+    case 1: DKB_READ(1) break;
+    case 2: DKB_READ(2) break;
+    case 4: DKB_READ(4) break;
+    case 8: DKB_READ(8) break;
+    default: return 1;
+  }
+#undef DKB_READ
+  return launch_error("read probe");
+}
+
+namespace {
+
+// The streaming-kernel shapes the product uses at one batch row
+// (launch_lds in dk_gemv.hip), by (R, U, W, prefetch), with the ablation
+// maths. math: 0 product, 1 no decode, 2 loads only.
+template <int R, int U, int W, bool PF>
+int v5_math(int math, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y, int M, int K,
+            hipStream_t stream) {
+  const dim3 grid((M + W * R - 1) / (W * R)), block(W * 64);
+  switch (math) {
+    case 0:
+      hipLaunchKernelGGL((dk::gemv_v5_lds<R, U, W, 1, PF, dk::LayoutLogical, 5, dk::StageMath>), grid,
+                         block, 0, stream, p, s, x, y, M, K, 1);
+      break;
+    case 1:
+      hipLaunchKernelGGL((dk::gemv_v5_lds<R, U, W, 1, PF, dk::LayoutLogical, 5, dkb::MathNoDecode>),
+                         grid, block, 0, stream, p, s, x, y, M, K, 1);
+      break;
+    case 2:
+      hipLaunchKernelGGL((dk::gemv_v5_lds<R, U, W, 1, PF, dk::LayoutLogical, 5, dkb::MathLoadsOnly>),
+                         grid, block, 0, stream, p, s, x, y, M, K, 1);
+      break;
+    default:
+      return 1;
+  }
+  return launch_error("v5 math");
+}
+
+}  // namespace
+
+// The streaming GEMV at one batch row with shape (R, U, W, prefetch) and
+// math 0 (product), 1 (no decode) or 2 (loads only). Returns 3 for a shape
+// that is not instantiated here.
+DKB_API int dkb_v5(int math, int R, int U, int W, int prefetch, const void* packed,
+                   const void* scales, const void* x, void* y, int M, int K, hipStream_t stream) {
+  const auto* p = static_cast<const uint4*>(packed);
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* xx = static_cast<const uint4*>(x);
+  auto* yy = static_cast<uint16_t*>(y);
+#define DKB_V5(r, u, w, pf)                                   \
+  if (R == r && U == u && W == w && (prefetch != 0) == pf) \
+    return v5_math<r, u, w, pf>(math, p, s, xx, yy, M, K, stream);
+  DKB_V5(1, 1, 16, true)
+  DKB_V5(1, 2, 4, true)
+  DKB_V5(1, 4, 4, true)
+  DKB_V5(1, 6, 4, true)
+  DKB_V5(1, 4, 8, true)
+  DKB_V5(2, 1, 8, true)
+  DKB_V5(2, 2, 4, false)
+  DKB_V5(2, 1, 8, false)
+  DKB_V5(1, 2, 16, true)
+  DKB_V5(2, 1, 16, true)
+  DKB_V5(1, 2, 8, true)
+  DKB_V5(1, 2, 8, false)
+  DKB_V5(1, 2, 16, false)
+  DKB_V5(1, 1, 8, true)
+#undef DKB_V5
+  return 3;
+}
+
+// One-stage GEMV (B = 1, K <= S * U * 2048): variant bits lds, weights_first;
+// S = 1 (U = 2) or 2 (U = 1); W in {4, 8, 16}. Returns 3 if not instantiated.
+DKB_API int dkb_onestage(int W, int S, int lds, int weights_first, const void* packed,
+                         const void* scales, const void* x, void* y, int M, int K,
+                         hipStream_t stream) {
+  if (K > S * (S == 1 ? 2 : 1) * 2048 || K % 128) return 1;
+  const auto* p = static_cast<const uint4*>(packed);
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* xx = static_cast<const uint4*>(x);
+  auto* yy = static_cast<uint16_t*>(y);
+#define DKB_ONE(w, ss, l, wf)                                                                     \
+  if (W == w && S == ss && (lds != 0) == l && (weights_first != 0) == wf) {                       \
+    hipLaunchKernelGGL((dkb::gemv_onestage<ss == 1 ? 2 : 1, w, ss, l, wf>),                      \
+                       dim3((M + w / ss - 1) / (w / ss)), dim3(w * 64), 0, stream, p, s, xx, yy, M, K); \
+    return launch_error("onestage");                                                              \
+  }
+#define DKB_ONE4(w, ss) DKB_ONE(w, ss, true, false) DKB_ONE(w, ss, true, true) \
+                        DKB_ONE(w, ss, false, false) DKB_ONE(w, ss, false, true)
+  DKB_ONE4(4, 1)
+  DKB_ONE4(8, 1)
+  DKB_ONE4(16, 1)
+  DKB_ONE4(8, 2)
+  DKB_ONE4(16, 2)
+#undef DKB_ONE4
+#undef DKB_ONE
+  return 3;
+}
+
+// Split-K instances for the v4 shape sweep (B = 1): shape (R, U, W,
+// prefetch), S slices, reduce 0 (tickets: the product's), 2 (partials only:
+// no ticket and no y; prices the reduction). `tickets` holds ceil(M / (W R))
+// 8-byte tickets, `ws` [S, M] floats; gen as for the product (low 6 bits 0).
+DKB_API int dkb_v4(int R, int U, int W, int prefetch, int reduce, int S, const void* packed,
+                   const void* scales, const void* x, void* y, float* ws, void* tickets,
+                   unsigned long long gen, int M, int K, hipStream_t stream) {
+  const auto* p = static_cast<const uint4*>(packed);
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* xx = static_cast<const uint4*>(x);
+  auto* yy = static_cast<uint16_t*>(y);
+  auto* t = static_cast<unsigned long long*>(tickets);
+  if (S < 1 || S > 32) return 1;
+#define DKB_V4(r, u, w, pf, red)                                                                  \
+  if (R == r && U == u && W == w && (prefetch != 0) == pf && reduce == red) {                    \
+    hipLaunchKernelGGL((dk::gemv_v4_lds<r, u, w, 1, pf, red>), dim3((M + w * r - 1) / (w * r), 1, S), \
+                       dim3(w * 64), 0, stream, p, s, xx, yy, ws, t, gen, M, K, 1);              \
+    return launch_error("v4");                                                                    \
+  }
+#define DKB_V4R(r, u, w, pf) DKB_V4(r, u, w, pf, 0) DKB_V4(r, u, w, pf, 2)
+  DKB_V4R(1, 1, 4, true)
+  DKB_V4R(1, 2, 4, true)
+  DKB_V4R(1, 4, 4, true)
+  DKB_V4R(1, 1, 8, true)
+  DKB_V4R(1, 2, 8, true)
+  DKB_V4R(1, 4, 8, true)
+  DKB_V4R(1, 2, 4, false)
+  DKB_V4R(1, 4, 4, false)
+  DKB_V4R(2, 1, 4, true)
+  DKB_V4R(2, 2, 4, true)
+  DKB_V4R(1, 1, 16, true)
+  DKB_V4R(1, 2, 16, true)
+#undef DKB_V4R
+#undef DKB_V4
+  return 3;
+}

@@ -7,9 +7,9 @@
 //     printed launch errors and returned garbage, csrc/gemv_w4a16.cu:9-16);
 //   * work is issued on the current HIP stream of the tensors' device under a
 //     device guard (the reference assumed the current device);
-//   * the split-K workspace comes from torch's caching allocator and only
-//     its small ticket area is zero-filled (the reference zeroed a [B, M]
-//     fp32 buffer, csrc/bindings.cpp:65-68).
+//   * the split-K workspace comes from torch's caching allocator and needs
+//     no clearing (the reference zeroed a [B, M] fp32 buffer,
+//     csrc/bindings.cpp:65-68).
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
@@ -94,24 +94,15 @@ torch::Tensor gemv_common(torch::Tensor packed, torch::Tensor scales, torch::Ten
   cfg.reuse_weights = reuse_weights ? 1 : 0;
   cfg.warps_per_row = warps_per_row;
 
+  // v4 and the reuse path's split-K tiles take a workspace from the caching
+  // allocator: tickets that carry the call's generation, then fp32 partials,
+  // so it needs no clearing (8-byte words keep it 8-byte aligned).
   const size_t ws_bytes = dk_gemv_workspace_bytes(M, K, B, &cfg);
   torch::Tensor workspace;
   void* ws_ptr = nullptr;
-  if (ws_bytes > 0 && cfg.reuse_weights) {
-    // The reuse path's split-K tiles: tickets carry the call's generation, so
-    // the workspace needs no clearing (8-byte words keep it 8-byte aligned).
+  if (ws_bytes > 0) {
     workspace = torch::empty({static_cast<int64_t>((ws_bytes + 7) / 8)},
                              x.options().dtype(torch::kInt64));
-    ws_ptr = workspace.data_ptr();
-  } else if (ws_bytes > 0) {
-    // v4 [partials | tickets]: the partials are overwritten by every launch;
-    // the tickets (one per 4-row tile, at the end) must start at zero. A fill
-    // kernel, not a memset, so the call stays capturable in a HIP graph.
-    const int64_t words = static_cast<int64_t>((ws_bytes + 3) / 4);
-    const int64_t partials = std::min<int64_t>(split_k, K / kGroupSize) * B * M;
-    const int64_t tickets = words - partials;
-    workspace = torch::empty({words}, x.options().dtype(torch::kInt32));
-    workspace.narrow(0, words - tickets, tickets).zero_();
     ws_ptr = workspace.data_ptr();
   }
 

@@ -11,10 +11,14 @@
 // the MLP decode step (dk_mlp.h) is in dk_mlp.hpp and shares the stamp.
 #include <hip/hip_runtime.h>
 
+#include <cxxabi.h>
+#include <dlfcn.h>
+
 #include <algorithm>
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <string>
 
 #include "dk_host.hpp"
@@ -72,13 +76,41 @@ int clamp_wpr(int wpr) { return std::max(2, std::min(wpr, 8)); }
 
 int lds_limit_bytes() { return 64 * 1024; }
 
+// Kernel name of a launch target: the host-side handle of a __global__
+// function carries the kernel's mangled name, which dladdr finds in the
+// library's dynamic symbol table (no GPU needed); demangled, it is the name
+// a rocprofv3 kernel trace shows.
+void kernel_name(const void* handle, char* out, size_t len) {
+  Dl_info di{};
+  const char* mangled = (dladdr(handle, &di) && di.dli_sname) ? di.dli_sname : "?";
+  int st = 0;
+  char* dem = abi::__cxa_demangle(mangled, nullptr, nullptr, &st);
+  std::snprintf(out, len, "%s", (st == 0 && dem) ? dem : mangled);
+  std::free(dem);
+}
+
 // Launches one kernel on `stream` and reports a launch error as DK_ERR_HIP.
+// With `info` set it launches nothing and records the kernel and its launch
+// shape instead (dk_gemv_describe); the first launch of a call is recorded
+// and every launch is counted.
 struct Launch {
   hipStream_t stream;
+  dk_launch_info* info = nullptr;
 
   template <typename... KArgs, typename... Args>
   int operator()(const char* what, void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds,
                  Args... args) const {
+    if (info) {
+      if (info->launches++ == 0) {
+        kernel_name(reinterpret_cast<const void*>(kernel), info->kernel, sizeof(info->kernel));
+        const unsigned g[3] = {grid.x, grid.y, grid.z}, b[3] = {block.x, block.y, block.z};
+        for (int i = 0; i < 3; ++i) {
+          info->grid[i] = g[i];
+          info->block[i] = b[i];
+        }
+      }
+      return DK_OK;
+    }
     hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
     return dk::check_launch(what);
   }
@@ -453,9 +485,13 @@ size_t split_workspace_bytes(int M, int B) {
   return split_ticket_bytes(M, B) + (size_t)kSplitS * B * M * sizeof(float);
 }
 
-// Generation of a split call: distinct for every launch in a process (32-bit
-// wrap), so a ticket left by an earlier call never reads as this call's.
-std::atomic<unsigned> g_split_gen{0x9E3779B9u};
+// Generation of a split call (take_ticket): distinct for every launch in a
+// process, 58 bits shifted above the 6-bit arrival count.
+std::atomic<unsigned long long> g_ticket_gen{0x2545F4914F6CDD1Dull};
+
+unsigned long long next_gen() {
+  return (g_ticket_gen.fetch_add(1ull, std::memory_order_relaxed) & ((1ull << 58) - 1ull)) << 6;
+}
 
 int launch_reuse_split(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x,
                        uint16_t* y, int M, int K, int B, void* workspace) {
@@ -464,9 +500,8 @@ int launch_reuse_split(const Launch& L, const uint4* p, const uint16_t* s, const
       reinterpret_cast<float*>(static_cast<char*>(workspace) + split_ticket_bytes(M, B));
   const dim3 grid((M + 16 * kSplitRT - 1) / (16 * kSplitRT),
                   (B + dk::kReuseBatch - 1) / dk::kReuseBatch, kSplitS);
-  const unsigned gen = g_split_gen.fetch_add(1u, std::memory_order_relaxed);
   return L("reuse split launch", dk::gemv_reuse_split<8, kSplitRT, 2>, grid, dim3(8 * 64), 0, p, s,
-           x, y, partials, tickets, gen, M, K, B);
+           x, y, partials, tickets, next_gen(), M, K, B);
 }
 
 enum class ReuseShape { kStream, kTiles };
@@ -509,12 +544,65 @@ int effective_split(int K, int split_k) {
   return std::max(1, std::min(split_k, G));
 }
 
-// v4 workspace: fp32 partials [S, B, M], then one uint32 ticket per tile.
-size_t v4_partials(int M, int K, int B, const dk_gemv_config* cfg) {
-  return (size_t)effective_split(K, cfg->split_k) * (size_t)B * (size_t)M;
+// v4 (split-K) launch plan: S slices of ceil(G / S) groups; four one-row
+// waves per workgroup; U 16-byte chunks per lane per stage, so that a slice
+// of up to 256 chunks is one stage; NB batch rows per stage.
+constexpr int kV4Rows = 4;  // rows per workgroup (W R) of every v4 instance
+struct V4Plan {
+  int S, U, NB;
+};
+
+V4Plan v4_plan(int K, int B, int split_k) {
+  V4Plan p;
+  p.S = effective_split(K, split_k);
+  const int G = K / DK_GROUP_SIZE;
+  const int slice_chunks = 4 * ((G + p.S - 1) / p.S);
+  p.U = slice_chunks <= 64 ? 1 : slice_chunks <= 128 ? 2 : 4;
+  p.NB = B == 1 ? 1 : B == 2 ? 2 : 4;
+  return p;
 }
 
-size_t v4_tickets(int M) { return ((size_t)M + dk::kV4TileRows - 1) / dk::kV4TileRows; }
+// v4 workspace: one 8-byte ticket per (workgroup, batch tile), padded to 256
+// bytes, then fp32 partials [S, B, M].
+size_t v4_ticket_bytes(int M, int B, const V4Plan& p) {
+  const size_t n = (size_t)((M + kV4Rows - 1) / kV4Rows) * (size_t)((B + p.NB - 1) / p.NB);
+  return (n * 8 + 255) / 256 * 256;
+}
+
+size_t v4_workspace_bytes(int M, int K, int B, int split_k) {
+  const V4Plan p = v4_plan(K, B, split_k);
+  return v4_ticket_bytes(M, B, p) + (size_t)p.S * B * M * sizeof(float);
+}
+
+template <int U, int NB, int kReduce>
+int launch_v4_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
+                float* ws, unsigned long long* tickets, unsigned long long gen, int M, int K, int B,
+                int S) {
+  const dim3 grid((M + kV4Rows - 1) / kV4Rows, (B + NB - 1) / NB, S);
+  return L("v4 launch", dk::gemv_v4_lds<1, U, kV4Rows, NB, true, kReduce>, grid,
+           dim3(kV4Rows * 64), 0, p, s, x, y, ws, tickets, gen, M, K, B);
+}
+
+template <int kReduce>
+int launch_v4(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
+              float* ws, unsigned long long* tickets, int M, int K, int B, const V4Plan& plan) {
+  const unsigned long long gen = kReduce == dk::kV4Tickets ? next_gen() : 0ull;
+#define DK_V4(U, NB) launch_v4_t<U, NB, kReduce>(L, p, s, x, y, ws, tickets, gen, M, K, B, plan.S)
+#define DK_V4_NB(U) (plan.NB == 1 ? DK_V4(U, 1) : plan.NB == 2 ? DK_V4(U, 2) : DK_V4(U, 4))
+  return plan.U == 1 ? DK_V4_NB(1) : plan.U == 2 ? DK_V4_NB(2) : DK_V4_NB(4);
+#undef DK_V4_NB
+#undef DK_V4
+}
+
+int check_io(const uint32_t* packed, const uint16_t* scales, const uint16_t* x, const uint16_t* y) {
+  if (!packed || !scales || !x || !y)
+    return fail(DK_ERR_INVALID_ARGUMENT, "packed, scales, x and y must not be NULL");
+  if (!aligned(packed, 16) || !aligned(x, 16))
+    return fail(DK_ERR_INVALID_ARGUMENT, "packed and x must be 16-byte aligned");
+  if (!aligned(scales, 2) || !aligned(y, 2))
+    return fail(DK_ERR_INVALID_ARGUMENT, "scales and y must be 2-byte aligned");
+  return DK_OK;
+}
 
 int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x, uint16_t* y, int M,
               int K, int B, const dk_gemv_config* cfg, void* workspace, size_t workspace_bytes,
@@ -522,12 +610,8 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
   int rc = dk_gemv_validate(M, K, B, cfg);
   if (rc != DK_OK) return rc;
   if (M <= 0 || K <= 0 || B <= 0) return DK_OK;
-  if (!packed || !scales || !x || !y)
-    return fail(DK_ERR_INVALID_ARGUMENT, "packed, scales, x and y must not be NULL");
-  if (!aligned(packed, 16) || !aligned(x, 16))
-    return fail(DK_ERR_INVALID_ARGUMENT, "packed and x must be 16-byte aligned");
-  if (!aligned(scales, 2) || !aligned(y, 2))
-    return fail(DK_ERR_INVALID_ARGUMENT, "scales and y must be 2-byte aligned");
+  rc = check_io(packed, scales, x, y);
+  if (rc != DK_OK) return rc;
   const size_t need = dk_gemv_workspace_bytes(M, K, B, cfg);
   // The reuse path's split-K tiles run when a large enough workspace comes
   // with the call; without one it runs the single-pass tiles.
@@ -536,7 +620,7 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
     if (!workspace || workspace_bytes < need)
       return fail(DK_ERR_INVALID_ARGUMENT, "split-K needs a %zu-byte workspace (got %zu)", need,
                   workspace_bytes);
-    if (!aligned(workspace, 4)) return fail(DK_ERR_INVALID_ARGUMENT, "workspace must be 4-byte aligned");
+    if (!aligned(workspace, 8)) return fail(DK_ERR_INVALID_ARGUMENT, "workspace must be 8-byte aligned");
   }
   if (split && !aligned(workspace, 8))
     return fail(DK_ERR_INVALID_ARGUMENT, "workspace must be 8-byte aligned");
@@ -577,18 +661,43 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
       return L("v3 launch", dk::gemv_v23<true>, rows4, block4, v3_lds_bytes(K), p4, scales, x4, y,
                M, K, B);
     case DK_V4: {
-      const int S = effective_split(K, cfg->split_k);
-      dim3 grid((M + dk::kV4TileRows - 1) / dk::kV4TileRows, S);
-      float* partials = static_cast<float*>(workspace);
-      auto* tickets = reinterpret_cast<unsigned int*>(partials + v4_partials(M, K, B, cfg));
-      return L("v4 launch", dk::gemv_v4, grid, dim3(dk::kV4TileRows * 64), 0, p4, scales, x4, y,
-               partials, tickets, M, K, B);
+      const V4Plan plan = v4_plan(K, B, cfg->split_k);
+      auto* tickets = static_cast<unsigned long long*>(workspace);
+      auto* partials = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                v4_ticket_bytes(M, B, plan));
+      return launch_v4<dk::kV4Tickets>(L, p4, scales, x4, y, partials, tickets, M, K, B, plan);
     }
     case DK_V5:
       return launch_v5(L, p4, scales, x4, y, M, K, B);
     default:
       return fail(DK_ERR_INVALID_ARGUMENT, "unknown version %d", cfg->version);
   }
+}
+
+// The reference's workspace contract: v4 accumulates its slices into the
+// caller-zeroed fp32 [B, M] buffer `acc` and converts it to y in a second
+// kernel; every other variant runs as dk_w4a16_gemv without a workspace.
+int gemv_ref_workspace_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
+                            uint16_t* y, int M, int K, int B, const dk_gemv_config* cfg,
+                            float* acc, const Launch& L) {
+  int rc = dk_gemv_validate(M, K, B, cfg);
+  if (rc != DK_OK) return rc;
+  if (cfg->reuse_weights || cfg->version != DK_V4)
+    return gemv_impl(packed, scales, x, y, M, K, B, cfg, nullptr, 0, L);
+  if (M <= 0 || K <= 0 || B <= 0) return DK_OK;
+  rc = check_io(packed, scales, x, y);
+  if (rc != DK_OK) return rc;
+  if (!acc)
+    return fail(DK_ERR_INVALID_ARGUMENT, "v4 needs the caller-zeroed fp32 [B, M] workspace");
+  if (!aligned(acc, 4)) return fail(DK_ERR_INVALID_ARGUMENT, "workspace must be 4-byte aligned");
+  const V4Plan plan = v4_plan(K, B, cfg->split_k);
+  rc = launch_v4<dk::kV4Accumulate>(L, reinterpret_cast<const uint4*>(packed), scales,
+                                    reinterpret_cast<const uint4*>(x), y, acc, nullptr, M, K, B,
+                                    plan);
+  if (rc != DK_OK) return rc;
+  const long long n = (long long)B * M;
+  return L("v4 convert launch", dk::v4_to_fp16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+           acc, y, n);
 }
 
 }  // namespace
@@ -631,13 +740,32 @@ size_t dk_gemv_workspace_bytes(int M, int K, int B, const dk_gemv_config* cfg) {
   if (M <= 0 || K <= 0 || B <= 0) return 0;
   if (cfg->reuse_weights) return reuse_split(M, K, B) ? split_workspace_bytes(M, B) : 0;
   if (cfg->version != DK_V4) return 0;
-  return v4_partials(M, K, B, cfg) * sizeof(float) + v4_tickets(M) * sizeof(unsigned int);
+  return v4_workspace_bytes(M, K, B, cfg->split_k);
 }
 
 int dk_w4a16_gemv(const uint32_t* packed, const uint16_t* scales, const uint16_t* x, uint16_t* y,
                   int M, int K, int B, const dk_gemv_config* cfg, void* workspace,
                   size_t workspace_bytes, hipStream_t stream) {
   return gemv_impl(packed, scales, x, y, M, K, B, cfg, workspace, workspace_bytes, Launch{stream});
+}
+
+int dk_w4a16_gemv_ref_workspace(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
+                                uint16_t* y, int M, int K, int B, const dk_gemv_config* cfg,
+                                float* workspace, hipStream_t stream) {
+  return gemv_ref_workspace_impl(packed, scales, x, y, M, K, B, cfg, workspace, Launch{stream});
+}
+
+int dk_gemv_describe(int M, int K, int B, const dk_gemv_config* cfg, size_t workspace_bytes,
+                     dk_launch_info* info) {
+  if (!info) return fail(DK_ERR_INVALID_ARGUMENT, "info must not be NULL");
+  *info = dk_launch_info{};
+  // Placeholder addresses with every alignment the checks ask for; in
+  // describe mode nothing is launched and nothing is dereferenced.
+  const auto* p = reinterpret_cast<const uint32_t*>(uintptr_t{4096});
+  const auto* h = reinterpret_cast<const uint16_t*>(uintptr_t{4096});
+  void* ws = workspace_bytes > 0 ? reinterpret_cast<void*>(uintptr_t{4096}) : nullptr;
+  Launch L{nullptr, info};
+  return gemv_impl(p, h, h, const_cast<uint16_t*>(h), M, K, B, cfg, ws, workspace_bytes, L);
 }
 
 int dk_last_kernel_stamp(void) {

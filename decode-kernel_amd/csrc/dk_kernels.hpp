@@ -251,8 +251,8 @@ template <int R, int U, int W, int NB, int kSplit>
 __device__ __forceinline__ void lds_stage_load(LdsStage<R, U, W, NB>& st, __amdgpu_buffer_rsrc_t rw,
                                                __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rw2,
                                                __amdgpu_buffer_rsrc_t rs2, __amdgpu_buffer_rsrc_t rx,
-                                               int c0, int nck, int G, int K, int b0, int B, int tid,
-                                               int lane) {
+                                               int c0, int nck, int wstride, int G, int K, int b0,
+                                               int B, int tid, int lane) {
   using S = LdsStage<R, U, W, NB>;
   // Activations of chunks [c0, c0 + 64U) of batch row b0 + b: piece p of
   // that row is bytes [16p, 16p + 16) of the range, so consecutive lanes
@@ -280,7 +280,7 @@ __device__ __forceinline__ void lds_stage_load(LdsStage<R, U, W, NB>& st, __amdg
     for (int r = 0; r < R; ++r) {
       const int rr = r < kSplit ? r : r - kSplit;
       st.w[u][r] = buffer_load16<kLoadNonTemporal>(r < kSplit ? rw : rw2,
-                                                   ok ? (rr * nck + c) * 16 : kOutOfRange);
+                                                   ok ? (rr * wstride + c) * 16 : kOutOfRange);
     }
   }
 }
@@ -361,14 +361,28 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// The stage loop shared by the GEMV and the fused gate/up kernel: acc[b][r]
-// is row r's fp32 sum for batch row b0 + b over this lane's chunks of K.
-template <int R, int U, int W, int NB, bool kPrefetch, typename Layout, int kSplit>
+// The decode and products of one stage (the default math of the stage loop).
+struct StageMath {
+  template <int R, int U, int W, int NB, typename Layout>
+  static __device__ __forceinline__ void compute(const LdsStage<R, U, W, NB>& st,
+                                                 const uint4 (&xs)[LdsActsT<U, NB>::kSlots],
+                                                 float (&acc)[NB][R], int lane) {
+    lds_stage_compute<R, U, W, NB, Layout>(st, xs, acc, lane);
+  }
+};
+
+// The stage loop shared by the GEMV, split-K and the fused gate/up kernel:
+// acc[b][r] is row r's fp32 sum for batch row b0 + b over this lane's chunks
+// of [0, nck) (a whole row, or one K slice of it). Weight row r starts
+// wstride chunks after row r - 1 in its descriptor; scales G entries; batch
+// rows of x K elements.
+template <int R, int U, int W, int NB, bool kPrefetch, typename Layout, int kSplit,
+          typename Math = StageMath>
 __device__ __forceinline__ void lds_stream(LdsActs<U, NB>& xs, float (&acc)[NB][R],
                                            __amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs,
                                            __amdgpu_buffer_rsrc_t rw2, __amdgpu_buffer_rsrc_t rs2,
-                                           __amdgpu_buffer_rsrc_t rx, int nck, int G, int K, int b0,
-                                           int B, int tid, int lane) {
+                                           __amdgpu_buffer_rsrc_t rx, int nck, int wstride, int G,
+                                           int K, int b0, int B, int tid, int lane) {
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
@@ -385,22 +399,23 @@ __device__ __forceinline__ void lds_stream(LdsActs<U, NB>& xs, float (&acc)[NB][
     // activation pieces keep the publish test: giving the spare lanes
     // padding slots instead (so every lane loads and stores) cost 11-17%.
     LdsStage<R, U, W, NB> sa, sb;
-    lds_stage_load<R, U, W, NB, kSplit>(sa, rw, rs, rw2, rs2, rx, 0, nck, G, K, b0, B, tid, lane);
+    lds_stage_load<R, U, W, NB, kSplit>(sa, rw, rs, rw2, rs2, rx, 0, nck, wstride, G, K, b0, B, tid,
+                                        lane);
     for (int c0 = 0;;) {
       lds_stage_publish<R, U, W, NB, Layout>(sa, xs[0], tid);
       __syncthreads();
-      lds_stage_load<R, U, W, NB, kSplit>(sb, rw, rs, rw2, rs2, rx, c0 + kStep, nck, G, K, b0, B,
-                                          tid, lane);
+      lds_stage_load<R, U, W, NB, kSplit>(sb, rw, rs, rw2, rs2, rx, c0 + kStep, nck, wstride, G, K,
+                                          b0, B, tid, lane);
       __builtin_amdgcn_sched_barrier(0);
-      lds_stage_compute<R, U, W, NB, Layout>(sa, xs[0], acc, lane);
+      Math::template compute<R, U, W, NB, Layout>(sa, xs[0], acc, lane);
       c0 += kStep;
       if (c0 >= nck) break;
       lds_stage_publish<R, U, W, NB, Layout>(sb, xs[1], tid);
       __syncthreads();
-      lds_stage_load<R, U, W, NB, kSplit>(sa, rw, rs, rw2, rs2, rx, c0 + kStep, nck, G, K, b0, B,
-                                          tid, lane);
+      lds_stage_load<R, U, W, NB, kSplit>(sa, rw, rs, rw2, rs2, rx, c0 + kStep, nck, wstride, G, K,
+                                          b0, B, tid, lane);
       __builtin_amdgcn_sched_barrier(0);
-      lds_stage_compute<R, U, W, NB, Layout>(sb, xs[1], acc, lane);
+      Math::template compute<R, U, W, NB, Layout>(sb, xs[1], acc, lane);
       c0 += kStep;
       if (c0 >= nck) break;
     }
@@ -408,20 +423,21 @@ __device__ __forceinline__ void lds_stream(LdsActs<U, NB>& xs, float (&acc)[NB][
     LdsStage<R, U, W, NB> st;
     int buf = 0;
     for (int c0 = 0; c0 < nck; c0 += kStep, buf ^= 1) {
-      lds_stage_load<R, U, W, NB, kSplit>(st, rw, rs, rw2, rs2, rx, c0, nck, G, K, b0, B, tid, lane);
+      lds_stage_load<R, U, W, NB, kSplit>(st, rw, rs, rw2, rs2, rx, c0, nck, wstride, G, K, b0, B,
+                                          tid, lane);
       // Every load of the stage issues before the publish waits on the
       // activation pieces (left alone, the scheduler can put that wait
       // between the loads).
       __builtin_amdgcn_sched_barrier(0);
       lds_stage_publish<R, U, W, NB, Layout>(st, xs[buf], tid);
       lds_barrier();
-      lds_stage_compute<R, U, W, NB, Layout>(st, xs[buf], acc, lane);
+      Math::template compute<R, U, W, NB, Layout>(st, xs[buf], acc, lane);
     }
   }
 }
 
 template <int R, int U, int W, int NB, bool kPrefetch, typename Layout = LayoutLogical,
-          int kStamp = Layout::kStamp>
+          int kStamp = Layout::kStamp, typename Math = StageMath>
 __global__ __launch_bounds__(W * kWave) void gemv_v5_lds(const uint4* __restrict__ packed,
                                                          const uint16_t* __restrict__ scales,
                                                          const uint4* __restrict__ x4,
@@ -447,8 +463,8 @@ __global__ __launch_bounds__(W * kWave) void gemv_v5_lds(const uint4* __restrict
   const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
 
   float acc[NB][R];
-  lds_stream<R, U, W, NB, kPrefetch, Layout, R>(xs, acc, rw, rs, rw, rs, rx, nck, G, K, b0, B, tid,
-                                                lane);
+  lds_stream<R, U, W, NB, kPrefetch, Layout, R, Math>(xs, acc, rw, rs, rw, rs, rx, nck, nck, G, K,
+                                                      b0, B, tid, lane);
   if (!active) return;  // after the last barrier
 #pragma unroll
   for (int b = 0; b < NB; ++b)
@@ -460,97 +476,143 @@ __global__ __launch_bounds__(W * kWave) void gemv_v5_lds(const uint4* __restrict
 }
 
 // ---------------------------------------------------------------------------
-// v4: split-K. grid = (row tiles of 4, S). Workgroup (tile, s) computes the
-// fp32 partial of its 4 rows over group slice s and stores it to
-// ws[s][b][row]; the last workgroup of a tile to finish adds the S partials
-// in slice order and writes fp16 y. One launch, deterministic.
-// Reference: csrc/gemv_w4a16.cu:264-313, 415-419 (memset + atomics + convert).
+// v4: split-K on the stage loop of v5 (stamp 4). grid = (row blocks of W R
+// rows, batch tiles of NB rows, S slices). Workgroup (x, y, z) streams its
+// rows over group slice z, groups [z ceil(G/S), +ceil(G/S)), with the same
+// LDS-shared activation stages, buffer loads through wave-uniform
+// descriptors (scoped to the slice, so chunks past it read zero) and decode
+// as v5; each slice reads only its share of the activations.
+// Reference: csrc/gemv_w4a16.cu:264-313, 415-419, 474-481 (a caller-zeroed
+// fp32 [B, M] buffer, fp32 atomicAdd of each slice's row sums, then a
+// separate fp32 -> fp16 kernel).
 //
-// The completion tickets (one uint32 per tile) live in the caller's
-// workspace after the partials, so launches on different streams with their
-// own workspaces never share them. They must be zero when a launch starts;
-// the last workgroup of each tile resets its ticket, so a workspace that was
-// zeroed once stays valid for every later launch that uses it in turn.
-//
-// Cross-workgroup visibility on an 8-XCD part (one L2 per XCD, not coherent
-// with each other) uses agent-scope atomic stores and loads for the partials
-// (they bypass the non-coherent L2s) and a wait for their completion before
-// the ticket, instead of agent-scope fences: a fence writes back and
-// invalidates a whole L2 per wave and made this kernel ~35x slower.
+// Reductions (kReduce):
+//  * kV4Tickets: one launch, bit-reproducible. Each wave stores its fp32 row
+//    sums to partials[z][b][row] with agent-scope stores (past the
+//    non-coherent per-XCD L2s) and waits for them; thread 0 then takes the
+//    ticket of its (row block, batch tile). The last of the S workgroups to
+//    arrive adds the S partials in slice order z = 0..S-1 and writes fp16 y.
+//    A ticket is 64 bits, (generation << 6) | arrivals: the first arrival of
+//    a call replaces whatever the ticket held, so the workspace needs no
+//    clearing; the last resets it to (generation, 0), so graph replays of
+//    one captured call (same generation) start clean. Generations are 58
+//    bits and never repeat in a process, so only a ticket holding this
+//    call's exact generation before the call (2^-58 for arbitrary memory)
+//    would be miscounted. A fence-based version of the earlier v4 was ~35x
+//    slower: an agent-scope fence writes back and invalidates a whole L2.
+//  * kV4Accumulate: the reference's contract, kept for callers of its C++
+//    API: fp32 agent-scope atomic adds of each slice's row sums into the
+//    caller-zeroed fp32 [B, M] buffer `ws`; a second kernel (v4_to_fp16)
+//    converts it to y. The order of the adds, and so the last bit of the
+//    fp32 sums, is not fixed (as in the reference).
+// Any other kReduce stores the partials and stops, without y (the benchmark
+// tools time it to price the reduction).
 // ---------------------------------------------------------------------------
-constexpr int kV4TileRows = 4;  // rows per workgroup and ticket tile: one wave per row
+constexpr int kV4Tickets = 0;
+constexpr int kV4Accumulate = 1;
 
-__global__ __launch_bounds__(256) void gemv_v4(const uint4* __restrict__ packed,
-                                               const uint16_t* __restrict__ scales,
-                                               const uint4* __restrict__ x4,
-                                               uint16_t* __restrict__ y, float* __restrict__ ws,
-                                               unsigned int* __restrict__ tickets, int M, int K,
-                                               int B) {
+// Takes the ticket of a split reduction for generation `gen` (low 6 bits
+// zero); true for the last of `S` arrivals. One thread per workgroup.
+__device__ __forceinline__ bool take_ticket(unsigned long long* ticket, unsigned long long gen, int S) {
+  unsigned long long t = __hip_atomic_load(ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  unsigned long long arrived;
+  for (;;) {
+    arrived = (t & ~63ull) == gen ? (t & 63ull) : 0ull;
+    // On failure t holds the current value; the loop ends when this
+    // workgroup's increment lands (at most S workgroups contend).
+    if (__hip_atomic_compare_exchange_strong(ticket, &t, gen | (arrived + 1ull), __ATOMIC_RELAXED,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      break;
+  }
+  return arrived == (unsigned long long)(S - 1);
+}
+
+__device__ __forceinline__ void release_ticket(unsigned long long* ticket, unsigned long long gen) {
+  __hip_atomic_store(ticket, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int R, int U, int W, int NB, bool kPrefetch, int kReduce>
+__global__ __launch_bounds__(W * kWave) void gemv_v4_lds(const uint4* __restrict__ packed,
+                                                         const uint16_t* __restrict__ scales,
+                                                         const uint4* __restrict__ x4,
+                                                         uint16_t* __restrict__ y,
+                                                         float* __restrict__ ws,
+                                                         unsigned long long* __restrict__ tickets,
+                                                         unsigned long long gen, int M, int K,
+                                                         int B) {
   write_stamp(4);
+  __shared__ LdsActs<U, NB> xs;
   __shared__ int last;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int rows_per_tile = kV4TileRows;
-  const int tile = blockIdx.x;
-  const int row_raw = tile * rows_per_tile + wave;
-  const int row = row_raw < M ? row_raw : M - 1;
-  const int S = gridDim.y;
-  const int split = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nblk = (M + W * R - 1) / (W * R);
+  const int wg = xcd_contiguous_block(blockIdx.x, nblk);
+  const int row0 = (wg * W + wave) * R;
+  const bool active = row0 < M;  // wave-uniform
+  const int b0 = blockIdx.y * NB;
+  const int S = gridDim.z;
+  const int z = blockIdx.z;
+  const int nck = K >> 5;
   const int G = K >> 7;
   const int gps = (G + S - 1) / S;
-  const int g0 = min(split * gps, G);
-  const int g1 = min(g0 + gps, G);
-  const int nck = K >> 5;
-  const uint4* rw = packed + (size_t)row * nck;
-  const uint16_t* rs = scales + (size_t)row * G;
+  const int gbeg = min(z * gps, G);
+  const int Gs = min(gbeg + gps, G) - gbeg;  // groups of this slice (0 if none)
+  const int rows = active ? min(R, M - row0) : 0;
+  const int rbase = active ? row0 : 0;
+  // The slice of row r is chunks [4 gbeg, 4 (gbeg + Gs)) at r * nck chunks
+  // from the descriptor base; the range ends after the last row's slice.
+  const auto rw = buffer_rsrc(packed + (size_t)rbase * nck + (size_t)gbeg * 4,
+                              rows > 0 ? (uint32_t)((rows - 1) * (K / 2) + Gs * 64) : 0u);
+  const auto rs = buffer_rsrc(scales + (size_t)rbase * G + gbeg,
+                              rows > 0 ? (uint32_t)(((rows - 1) * G + Gs) * 2) : 0u);
+  const auto rx = buffer_rsrc(x4 + (size_t)gbeg * 16, (uint32_t)((size_t)B * K * 2 - (size_t)gbeg * 256));
 
-  for (int b = 0; b < B; ++b) {
-    const uint4* xb = x4 + (size_t)b * (K >> 3);
-    float acc = 0.f;
-    for (int c = 4 * g0 + lane; c < 4 * g1; c += kWave) {
-      const uint4 w = rw[c];
-      float part = 0.f;
-      h2_t xp[4];
-      pair_x(xb[4 * c + 0], xp);
-      part = dot_word(w.x, xp, part);
-      pair_x(xb[4 * c + 1], xp);
-      part = dot_word(w.y, xp, part);
-      pair_x(xb[4 * c + 2], xp);
-      part = dot_word(w.z, xp, part);
-      pair_x(xb[4 * c + 3], xp);
-      part = dot_word(w.w, xp, part);
-      acc += h2f(rs[c >> 2]) * part;
+  float acc[NB][R];
+  lds_stream<R, U, W, NB, kPrefetch, LayoutLogical, R>(xs, acc, rw, rs, rw, rs, rx, 4 * Gs, nck, G,
+                                                        K, b0, B, tid, lane);
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float t = wave_sum(acc[b][r]);
+      if (active && lane == 63 && row0 + r < M && b0 + b < B) {
+        const size_t o = (size_t)(b0 + b) * M + row0 + r;
+        if constexpr (kReduce == kV4Accumulate)
+          __hip_atomic_fetch_add(&ws[o], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          __hip_atomic_store(&ws[(size_t)z * B * M + o], t, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
-    acc = wave_sum(acc);
-    if (lane == 63 && row_raw < M)
-      __hip_atomic_store(&ws[((size_t)split * B + b) * M + row], acc, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+  if constexpr (kReduce == kV4Tickets) {
+    // Every wave's partial stores are complete before the ticket is taken.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    unsigned long long* ticket = &tickets[(size_t)blockIdx.y * nblk + wg];
+    if (tid == 0) last = take_ticket(ticket, gen, S);
+    __syncthreads();
+    if (!last) return;
+    constexpr int kOut = W * R * NB;
+    for (int t = tid; t < kOut; t += W * kWave) {
+      const int row = wg * W * R + t % (W * R);
+      const int b = b0 + t / (W * R);
+      if (row >= M || b >= B) continue;
+      float sum = 0.f;
+      for (int s = 0; s < S; ++s)
+        sum += __hip_atomic_load(&ws[((size_t)s * B + b) * M + row], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      y[(size_t)b * M + row] = f2h(sum);
+    }
+    if (tid == 0) release_ticket(ticket, gen);
   }
+}
 
-  // Every wave's partial stores are complete before the ticket is taken.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev =
-        __hip_atomic_fetch_add(&tickets[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = (prev == (unsigned)(S - 1));
-  }
-  __syncthreads();
-  if (!last) return;
-  const int row_base = tile * rows_per_tile;
-  const int n_out = rows_per_tile * B;
-  for (int t = threadIdx.x; t < n_out; t += blockDim.x) {
-    const int r = row_base + (t % rows_per_tile);
-    const int b = t / rows_per_tile;
-    if (r >= M) continue;
-    float sum = 0.f;
-    for (int s = 0; s < S; ++s)
-      sum += __hip_atomic_load(&ws[((size_t)s * B + b) * M + r], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    y[(size_t)b * M + r] = f2h(sum);
-  }
-  if (threadIdx.x == 0)
-    __hip_atomic_store(&tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// The second kernel of the accumulate form: y = fp16(acc), n = B * M values.
+__global__ __launch_bounds__(256) void v4_to_fp16(const float* __restrict__ acc,
+                                                  uint16_t* __restrict__ y, long long n) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = f2h(acc[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -785,18 +847,13 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ 
 // the activations. Each writes its fp32 tile sums to partials[z][b][row]
 // (agent-scope stores, past the non-coherent L2s) and takes a ticket; the
 // last of the S adds the slices in order z = 0..S-1 (bit-reproducible) and
-// writes y. A ticket is 64 bits, the call's generation `gen` over an arrival
-// count: the first arrival of a call replaces whatever the ticket held (a
-// workspace need not be zeroed), the last resets it to (gen, 0), so replays
-// of one captured call with the same gen start from a clean count. A ticket
-// that already holds gen with a nonzero count before the call (left by no
-// call of this library; arbitrary memory matches with probability 2^-32)
-// would be miscounted.
+// writes y. The tickets are those of the v4 split-K (take_ticket): a
+// workspace needs no clearing.
 template <int KS, int RT, int SG>
 __global__ __launch_bounds__(KS * 64) void gemv_reuse_split(
     const uint4* __restrict__ packed, const uint16_t* __restrict__ scales,
     const uint4* __restrict__ x4, uint16_t* __restrict__ y, float* __restrict__ partials,
-    unsigned long long* __restrict__ tickets, unsigned gen, int M, int K, int B) {
+    unsigned long long* __restrict__ tickets, unsigned long long gen, int M, int K, int B) {
   static_assert(KS >= RT, "wave t sums tile t");
   write_stamp(DK_STAMP_REUSE);
   __shared__ ReuseLds<KS, RT, SG> lds;
@@ -848,21 +905,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_split(
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   unsigned long long* ticket = &tickets[blockIdx.y * gridDim.x + blockIdx.x];
-  if (threadIdx.x == 0) {
-    unsigned long long t = __hip_atomic_load(ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    unsigned arrived;
-    for (;;) {
-      const bool same = (unsigned)(t >> 32) == gen;
-      arrived = same ? (unsigned)t : 0u;
-      const unsigned long long next = ((unsigned long long)gen << 32) | (arrived + 1u);
-      // On failure t holds the current value; the loop ends when this
-      // workgroup's increment lands (at most S workgroups contend).
-      if (__hip_atomic_compare_exchange_strong(ticket, &t, next, __ATOMIC_RELAXED,
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-        break;
-    }
-    last = arrived == (unsigned)(S - 1);
-  }
+  if (threadIdx.x == 0) last = take_ticket(ticket, gen, S);
   __syncthreads();
   if (!last) return;
   if (wave < RT && b < B) {
@@ -877,9 +920,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_split(
       y[(size_t)b * M + orow] = f2h(sum);
     }
   }
-  if (threadIdx.x == 0)
-    __hip_atomic_store(ticket, (unsigned long long)gen << 32, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) release_ticket(ticket, gen);
 }
 
 }  // namespace dk

@@ -58,8 +58,8 @@ __global__ __launch_bounds__(W * kWave) void gate_up_silu_lds(
   const int b0 = blockIdx.y * NB;
 
   float acc[NB][2 * R];
-  lds_stream<2 * R, U, W, NB, kPrefetch, LayoutLogical, R>(xs, acc, rwg, rsg, rwu, rsu, rx, nck, G,
-                                                            H, b0, B, tid, lane);
+  lds_stream<2 * R, U, W, NB, kPrefetch, LayoutLogical, R>(xs, acc, rwg, rsg, rwu, rsu, rx, nck, nck,
+                                                            G, H, b0, B, tid, lane);
   if (!active) return;  // after the last barrier
 #pragma unroll
   for (int b = 0; b < NB; ++b)

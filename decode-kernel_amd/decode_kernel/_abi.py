@@ -30,6 +30,17 @@ class GemvConfig(ctypes.Structure):
     ]
 
 
+class LaunchInfo(ctypes.Structure):
+    """Mirror of dk_launch_info (dk_gemv_describe)."""
+
+    _fields_ = [
+        ("kernel", ctypes.c_char * 512),
+        ("grid", ctypes.c_uint * 3),
+        ("block", ctypes.c_uint * 3),
+        ("launches", ctypes.c_int),
+    ]
+
+
 # name -> (restype, argtypes); the export list checked against the header.
 _P = ctypes.c_void_p
 _SIGNATURES = {
@@ -46,6 +57,16 @@ _SIGNATURES = {
         ctypes.c_int,
         [_P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
          ctypes.POINTER(GemvConfig), _P, ctypes.c_size_t, _P],
+    ),
+    "dk_w4a16_gemv_ref_workspace": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+         ctypes.POINTER(GemvConfig), _P, _P],
+    ),
+    "dk_gemv_describe": (
+        ctypes.c_int,
+        [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(GemvConfig), ctypes.c_size_t,
+         ctypes.POINTER(LaunchInfo)],
     ),
     "dk_quantize_pack_f32": (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_int, _P, _P, _P]),
     "dk_repack_paired": (ctypes.c_int, [_P, _P, ctypes.c_int, ctypes.c_int, _P]),
@@ -99,6 +120,22 @@ def default_config(lib: ctypes.CDLL, **overrides) -> GemvConfig:
     for k, v in overrides.items():
         setattr(cfg, k, int(v))
     return cfg
+
+
+def describe(lib: ctypes.CDLL, m: int, k: int, b: int, workspace_bytes: int | None = None,
+             **config) -> dict:
+    """The kernel dk_w4a16_gemv would launch for this call (dk_gemv_describe):
+    demangled name, grid, workgroup size and number of launches. Needs no GPU.
+    By default the call passes dk_gemv_workspace_bytes(), as the torch binding
+    does."""
+    cfg = default_config(lib, **config)
+    if workspace_bytes is None:
+        workspace_bytes = lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(cfg))
+    info = LaunchInfo()
+    check(lib, lib.dk_gemv_describe(m, k, b, ctypes.byref(cfg), workspace_bytes,
+                                    ctypes.byref(info)))
+    return {"kernel": info.kernel.decode(), "grid": list(info.grid), "block": list(info.block),
+            "launches": info.launches}
 
 
 def check(lib: ctypes.CDLL, status: int) -> None:

@@ -1,0 +1,94 @@
+"""ctypes view of dk_bench/libdk_bench.so, the measurement-only kernels
+(csrc/bench/dk_bench_kernels.hip): read-floor probes, the load-only ablation
+of the streaming GEMV, one-stage GEMV variants and split-K shape instances.
+None of it is part of the product library or its C ABI."""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libdk_bench.so"
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_SIGNATURES = {
+    "dkb_read_probe": (_I, [_P, ctypes.c_size_t, _P, _I, _I, _I, _I, _P]),
+    "dkb_v5": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P]),
+    "dkb_onestage": (_I, [_I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P]),
+    "dkb_v4": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, ctypes.c_ulonglong, _I, _I,
+                    _P]),
+}
+EXPORTS = tuple(_SIGNATURES)
+
+_lib = None
+
+
+def load(path: Path | str = LIB_PATH) -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not Path(path).exists():
+            raise ImportError(f"{path} is not built; run `python decode-kernel_amd/build_ext.py`")
+        lib = ctypes.CDLL(str(path))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what}: status {rc}")
+
+
+def stream_handle():
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+def read_probe(src, partials, blocks: int, threads: int, loads: int, nt: bool) -> None:
+    check(load().dkb_read_probe(src.data_ptr(), src.numel() * src.element_size(),
+                                partials.data_ptr(), blocks, threads, loads, int(nt),
+                                stream_handle()), "read probe")
+
+
+def v5(math: int, shape: tuple, packed, scales, x, y) -> None:
+    """Streaming GEMV (B = 1) with shape (R, U, W, prefetch); math 0 product,
+    1 no decode, 2 loads only."""
+    r, u, w, pf = shape
+    m, k = packed.shape[0], packed.shape[1] * 8
+    check(load().dkb_v5(math, r, u, w, int(pf), packed.data_ptr(), scales.data_ptr(), x.data_ptr(),
+                        y.data_ptr(), m, k, stream_handle()), f"v5 {shape} math {math}")
+
+
+def onestage(w: int, s: int, lds: bool, weights_first: bool, packed, scales, x, y) -> None:
+    m, k = packed.shape[0], packed.shape[1] * 8
+    check(load().dkb_onestage(w, s, int(lds), int(weights_first), packed.data_ptr(),
+                              scales.data_ptr(), x.data_ptr(), y.data_ptr(), m, k,
+                              stream_handle()), f"onestage W{w} S{s}")
+
+
+def v4(shape: tuple, reduce: int, splits: int, packed, scales, x, y, ws, tickets, gen: int) -> None:
+    """Split-K GEMV (B = 1), shape (R, U, W, prefetch); reduce 0 tickets (the
+    product's), 2 partials only (no y)."""
+    r, u, w, pf = shape
+    m, k = packed.shape[0], packed.shape[1] * 8
+    check(load().dkb_v4(r, u, w, int(pf), reduce, splits, packed.data_ptr(), scales.data_ptr(),
+                        x.data_ptr(), y.data_ptr(), ws.data_ptr(), tickets.data_ptr(), gen, m, k,
+                        stream_handle()), f"v4 {shape} S{splits}")
+
+
+def parse_v5_shape(kernel_name: str) -> tuple | None:
+    """(R, U, W, prefetch) of a gemv_v5_lds kernel name at one batch row, as
+    dk_gemv_describe reports it; None for any other kernel."""
+    key = "gemv_v5_lds<"
+    if key not in kernel_name:
+        return None
+    args = [a.strip() for a in kernel_name.split(key, 1)[1].split(">", 1)[0].split(",")]
+    r, u, w, nb = (int(a) for a in args[:4])
+    if nb != 1:
+        return None
+    return (r, u, w, args[4] == "true")

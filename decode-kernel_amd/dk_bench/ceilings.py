@@ -71,18 +71,18 @@ def measure_write(nbytes: int = DEFAULT_STREAM_BYTES) -> dict:
     return out
 
 
-def measure_event_floor(steps: int = 500) -> dict:
+def measure_event_floor(steps: int = 500, preroll=None) -> dict:
     """An empty kernel: per launch when launches run back-to-back (graph
     replay; the floor under every per-step time here), and with events around
     a single call (the floor under the reference's protocol)."""
     from decode_kernel import _cuda
 
-    b2b, _ = time_graph_steps(lambda i: _cuda.empty_kernel(), steps=steps)
+    b2b, _ = time_graph_steps(lambda i: _cuda.empty_kernel(), steps=steps, preroll=preroll)
     call = time_gpu(lambda: _cuda.empty_kernel(), warmup=50, iters=500)
     return {"back_to_back": b2b, "call": call}
 
 
-def measure_read_same_size(packed_copies: list) -> dict:
+def measure_read_same_size(packed_copies: list, preroll=None) -> dict:
     """Read-only STREAM over the GEMV's own weight buffers, back-to-back over
     the copies: the best a kernel that only reads those bytes achieves."""
     from decode_kernel import _cuda
@@ -92,12 +92,51 @@ def measure_read_same_size(packed_copies: list) -> dict:
         partials = torch.empty(blocks, dtype=torch.float32, device="cuda")
         n = len(packed_copies)
         st, _ = time_graph_steps(lambda i: _cuda.stream_read(packed_copies[i % n], partials),
-                                 steps=4 * n)
+                                 steps=4 * n, preroll=preroll)
         nbytes = packed_copies[0].numel() * 4
         st.update({"blocks": blocks, "nbytes": nbytes, "gbps": nbytes / (st["median_us"] * 1e3)})
         if best is None or st["gbps"] > best["gbps"]:
             best = st
     return best
+
+
+def measure_read_floor(nbytes: int, preroll=None, grids=(256, 512, 1024, 2048, 4096),
+                       threads=(256, 512, 1024), loads=(1, 2, 4, 8), max_passes: int = 2,
+                       steps: int = 200) -> dict:
+    """The read floor at `nbytes`: the fastest per-launch time of a kernel that
+    only reads that many bytes, over launch shapes of the read probe
+    (dk_bench/libdk_bench.so): `grids` workgroups of `threads` lanes, `loads`
+    16-byte loads per lane all issued before the first wait, with and without
+    the non-temporal hint; shapes needing more than `max_passes` passes over
+    the buffer are skipped. Each shape is timed back-to-back over buffer
+    copies totalling > 640 MB (cold), `steps` launches per graph, p50 of 5
+    replays after a 1 GiB pre-roll. Returns the best shape and the sweep."""
+    from . import benchlib
+    from .common import COLD_WORKING_SET
+
+    nbytes = (nbytes + 15) // 16 * 16
+    n = max(2, -(-COLD_WORKING_SET // nbytes))
+    bufs = [torch.ones(nbytes // 4, dtype=torch.float32, device="cuda") for _ in range(n)]
+    pieces = nbytes // 16
+    sweep, best = [], None
+    for t in threads:
+        partials = torch.empty(max(grids) * t // 64, dtype=torch.float32, device="cuda")
+        for g in grids:
+            for ld in loads:
+                if -(-pieces // (g * t * ld)) > max_passes:
+                    continue
+                for nt in (False, True):
+                    st, _ = time_graph_steps(
+                        lambda i: benchlib.read_probe(bufs[i % n], partials, g, t, ld, nt),
+                        steps=steps, preroll=preroll)
+                    row = {"blocks": g, "threads": t, "loads": ld, "nt": nt,
+                           "median_us": st["median_us"], "gbps": nbytes / (st["median_us"] * 1e3)}
+                    sweep.append(row)
+                    if best is None or row["median_us"] < best["median_us"]:
+                        best = row
+    del bufs
+    return {"nbytes": nbytes, "copies": n, "best": best,
+            "sweep": sorted(sweep, key=lambda r: r["median_us"])}
 
 
 def measure_gemm_fp16(n: int = 8192, warmup: int = 10, iters: int = 30) -> dict:

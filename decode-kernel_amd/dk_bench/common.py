@@ -154,24 +154,28 @@ def weight_copies(packed: torch.Tensor, scales: torch.Tensor,
 
 
 def time_graph_steps(step: Callable[[int], object], steps: int, trials: int = 5,
-                     warmup: int = 1) -> dict:
+                     warmup: int = 1, preroll: Optional[Callable[[], None]] = None) -> dict:
     """Per-step time of exactly `steps` back-to-back steps, `step(i)` for
     i = 0..steps-1, captured in one HIP graph and replayed `trials` times.
-    Each replay is bracketed by events on the stream it runs on (after a
-    synchronize); the per-step time of a replay is its elapsed time / steps.
-    Host launch cost is outside the measurement, so the figure is what the
-    GPU spends per step when the steps run back-to-back, as in a decode pass."""
+
+    `warmup` untimed eager steps run first (at least one: allocator and code
+    objects), then one untimed replay loads the graph. Before each timed
+    replay `preroll` (a 1 GiB read, ~0.2 ms) is enqueued on the same stream
+    outside the events: the GPU is busy with it while the host enqueues the
+    start event and the graph's launches, so the timed span holds only the
+    steps back-to-back, whatever `steps` is, and every replay starts with
+    the L2s and the Infinity Cache flushed. Each replay is bracketed by
+    events on the stream it runs on; per-step time = elapsed / steps."""
     import time
 
-    for i in range(min(steps, 4)):  # eager warm-up: allocator and code objects
-        step(i)
+    for i in range(max(1, warmup)):
+        step(i % steps)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for i in range(steps):
             step(i)
-    for _ in range(warmup):
-        graph.replay()
+    graph.replay()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -179,6 +183,8 @@ def time_graph_steps(step: Callable[[int], object], steps: int, trials: int = 5,
     for _ in range(trials):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
+        if preroll is not None:
+            preroll()
         start.record()
         graph.replay()
         end.record()
@@ -186,7 +192,9 @@ def time_graph_steps(step: Callable[[int], object], steps: int, trials: int = 5,
         walls.append(time.perf_counter() - t0)
         per.append(start.elapsed_time(end) * 1000.0 / steps)
     out = _stats(per)
-    out.update({"steps": steps, "trials": trials, "timer": "events_around_graph_replay",
+    out.update({"steps": steps, "trials": trials, "warmup": max(1, warmup),
+                "timer": "events_around_graph_replay",
+                "preroll": "1 GiB read before each replay" if preroll is not None else None,
                 "wall_s_per_replay": statistics.fmean(walls)})
     return out, graph
 

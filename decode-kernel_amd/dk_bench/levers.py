@@ -1,0 +1,174 @@
+"""Launch-shape and kernel-variant sweeps behind the routing choices.
+
+    python -m dk_bench.levers floor|c0|v4|all [--steps 300] [--out PATH]
+    (from decode-kernel_amd/, after build_ext.py)
+
+  floor  read-probe launch shapes at the algorithmic bytes of c0, c1 and c2
+         (grid, lanes, loads per lane, non-temporal hint): the read floor;
+  c0     one-stage GEMV variants at M = K = 4096, B = 1 (activations through
+         LDS or in registers, weights issued first or last, one or two waves
+         per row, 4 to 16 waves per workgroup) and streaming-kernel shapes,
+         against the product;
+  v4     split-K shapes (rows, chunks per lane per stage, waves, prefetch;
+         2, 4 or 8 slices) at short and tall rows, each also without its
+         reduction (partials stored, no ticket, no y), against the product's
+         v5 and v4.
+
+Every variant that computes y is checked against the product's v5 output
+(bit-exact where the summation order is the same, else within 1e-3 plus one
+fp16 ulp) before it is timed. Timing as in bench.py: HIP graphs of `steps`
+launches over weight copies totalling > 640 MB (cold), a 1 GiB pre-roll
+before each of 5 replays, p50 microseconds per launch.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+from pathlib import Path
+
+import torch
+
+V4_SHAPES = [(1, 1, 4, True), (1, 2, 4, True), (1, 4, 4, True), (1, 1, 8, True), (1, 2, 8, True),
+             (1, 4, 8, True), (1, 2, 4, False), (1, 4, 4, False), (2, 1, 4, True), (2, 2, 4, True),
+             (1, 1, 16, True), (1, 2, 16, True)]
+V4_PROBLEMS = {"c0": (4096, 4096), "c2": (4096, 11008), "m1024_k28672": (1024, 28672),
+               "m2048_k11008": (2048, 11008), "m1024_k8192": (1024, 8192), "c4b": (8192, 28672)}
+V5_C0_SHAPES = [(1, 2, 8, True), (1, 2, 8, False), (1, 2, 16, True), (1, 2, 16, False),
+                (1, 2, 4, True), (1, 1, 16, True), (1, 1, 8, True)]
+
+
+def _close(a, b) -> bool:
+    a32, b32 = a.float(), b.float()
+    ulp = torch.clamp(b32.abs(), min=2.0 ** -14) * 2.0 ** -10
+    return bool(((a32 - b32).abs() <= 1e-3 + ulp).all())
+
+
+def _time(fn, steps, flush) -> float:
+    from .common import time_graph_steps
+
+    st, _ = time_graph_steps(fn, steps=steps, preroll=flush)
+    return st["median_us"]
+
+
+def sweep_floor(flush, steps: int) -> dict:
+    from .ceilings import measure_read_floor
+    from .common import bytes_moved_w4
+
+    out = {}
+    for name, (m, k) in {"c0": (4096, 4096), "c1": (11008, 4096), "c2": (4096, 11008)}.items():
+        fl = measure_read_floor(bytes_moved_w4(m, k, 1), preroll=flush, steps=steps)
+        out[name] = fl
+        b = fl["best"]
+        print(f"floor {name}: {b['median_us']:.3f} us ({b['gbps']:.0f} GB/s) at {b['blocks']} x "
+              f"{b['threads']} lanes, {b['loads']} loads, nt={b['nt']}; next: "
+              + ", ".join(f"{r['median_us']:.3f}" for r in fl["sweep"][1:6]), flush=True)
+    return out
+
+
+def sweep_c0(flush, steps: int) -> dict:
+    from decode_kernel import _cuda
+
+    from . import benchlib
+    from .ablation import gpu_case
+    from .common import weight_copies
+
+    packed, scales, x = gpu_case(4096, 4096, seed=1000)
+    pk, sc = weight_copies(packed, scales)
+    n = len(pk)
+    y_prod = _cuda.w4a16_gemv(pk[0], sc[0], x)
+    y = torch.empty_like(y_prod)
+    rows = {"product_v5": _time(lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x), steps, flush)}
+    print(f"c0 product v5 {rows['product_v5']:.3f} us", flush=True)
+    for shape in V5_C0_SHAPES:
+        benchlib.v5(0, shape, pk[0], sc[0], x, y)
+        torch.cuda.synchronize()
+        if not torch.equal(y, y_prod):
+            raise RuntimeError(f"v5 {shape} differs from the product at c0")
+        key = "v5_R{}_U{}_W{}_{}".format(*shape[:3], "pf" if shape[3] else "nopf")
+        rows[key] = _time(lambda i: benchlib.v5(0, shape, pk[i % n], sc[i % n], x, y), steps, flush)
+        print(f"c0 {key} {rows[key]:.3f} us", flush=True)
+    for w, s in ((4, 1), (8, 1), (16, 1), (8, 2), (16, 2)):
+        for lds in (True, False):
+            for wf in (False, True):
+                benchlib.onestage(w, s, lds, wf, pk[0], sc[0], x, y)
+                torch.cuda.synchronize()
+                ok = torch.equal(y, y_prod) if s == 1 else _close(y, y_prod)
+                if not ok:
+                    raise RuntimeError(f"onestage W{w} S{s} lds={lds} wf={wf} differs at c0")
+                key = f"onestage_W{w}_S{s}_{'lds' if lds else 'regs'}_{'wfirst' if wf else 'xfirst'}"
+                rows[key] = _time(lambda i: benchlib.onestage(w, s, lds, wf, pk[i % n], sc[i % n], x,
+                                                              y), steps, flush)
+                print(f"c0 {key} {rows[key]:.3f} us", flush=True)
+    return rows
+
+
+def sweep_v4(flush, steps: int) -> dict:
+    from decode_kernel import _cuda
+
+    from . import benchlib
+    from .ablation import gpu_case
+    from .common import weight_copies
+
+    out = {}
+    gen = 1 << 20
+    for name, (m, k) in V4_PROBLEMS.items():
+        packed, scales, x = gpu_case(m, k, seed=2000 + m + k)
+        pk, sc = weight_copies(packed, scales)
+        n = len(pk)
+        y_prod = _cuda.w4a16_gemv(pk[0], sc[0], x)
+        y = torch.empty_like(y_prod)
+        rows = {"product_v5": _time(lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x), steps, flush),
+                "product_v4_s4": _time(lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x, version=4,
+                                                                  split_k=4), steps, flush)}
+        print(f"v4 {name}: product v5 {rows['product_v5']:.3f}, product v4 s4 "
+              f"{rows['product_v4_s4']:.3f} us", flush=True)
+        for splits in (2, 4, 8):
+            ws = torch.empty(splits * m, dtype=torch.float32, device="cuda")
+            tickets = torch.zeros(m, dtype=torch.int64, device="cuda")
+            for shape in V4_SHAPES:
+                gen += 64
+                benchlib.v4(shape, 0, splits, pk[0], sc[0], x, y, ws, tickets, gen)
+                torch.cuda.synchronize()
+                if not _close(y, y_prod):
+                    raise RuntimeError(f"v4 {shape} S{splits} differs from v5 at {name}")
+                key = "S{}_R{}_U{}_W{}_{}".format(splits, *shape[:3], "pf" if shape[3] else "nopf")
+                g = gen + 64
+                gen += 128
+                full = _time(lambda i: benchlib.v4(shape, 0, splits, pk[i % n], sc[i % n], x, y, ws,
+                                                   tickets, g), steps, flush)
+                part = _time(lambda i: benchlib.v4(shape, 2, splits, pk[i % n], sc[i % n], x, y, ws,
+                                                   tickets, g), steps, flush)
+                rows[key] = {"us": full, "partials_only_us": part}
+                print(f"v4 {name} {key}: {full:.3f} us (partials only {part:.3f})", flush=True)
+        out[name] = rows
+        del pk, sc, packed, scales, x
+        torch.cuda.empty_cache()
+    return out
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("what", choices=["floor", "c0", "v4", "all"])
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--out", type=Path, default=None)
+    args = ap.parse_args()
+    if not torch.cuda.is_available():
+        raise SystemExit("a GPU is required")
+    from .common import Flush
+
+    flush = Flush()
+    res = {}
+    if args.what in ("floor", "all"):
+        res["floor"] = sweep_floor(flush, args.steps)
+    if args.what in ("c0", "all"):
+        res["c0"] = sweep_c0(flush, args.steps)
+    if args.what in ("v4", "all"):
+        res["v4"] = sweep_v4(flush, args.steps)
+    if args.out:
+        args.out.parent.mkdir(parents=True, exist_ok=True)
+        args.out.write_text(json.dumps(res, indent=2) + "\n")
+
+
+if __name__ == "__main__":
+    main()

@@ -38,7 +38,7 @@ typedef enum dk_kernel_version {
   DK_V1 = 1, /* one wave64 per row, 4-byte coalesced word loads */
   DK_V2 = 2, /* one wave64 per row, 16-byte coalesced loads */
   DK_V3 = 3, /* v2 with the row's group scales staged in LDS */
-  DK_V4 = 4, /* split-K over grid.y, deterministic single-launch reduction */
+  DK_V4 = 4, /* split-K over grid.z, deterministic single-launch reduction */
   DK_V5 = 5  /* tuned: raw buffer loads (activations first), shape-selected
                 rows per wave and activation rows per tile */
 } dk_kernel_version;
@@ -72,23 +72,22 @@ void dk_gemv_config_default(dk_gemv_config* cfg);
 
 /* Bytes of device workspace dk_w4a16_gemv takes for this call; 0 for every
  * variant but two:
- *  - split-K v4 (required): fp32 partials [split_k', B, M], split_k' =
- *    min(split_k, K/128), followed by one uint32 completion ticket per 4-row
- *    tile, ceil(M/4). The ticket area must be zero when a v4 call starts;
- *    every v4 call leaves it zero again, so a workspace zeroed once can be
- *    reused by later calls of the same shape that run one after another.
+ *  - split-K v4 (required, 8-byte aligned): one 8-byte completion ticket per
+ *    (4-row workgroup, batch tile), padded to 256 bytes, then fp32 partials
+ *    [split_k', B, M], split_k' = min(split_k, K/128);
  *  - the weight-reuse path when its MFMA tiles split K over workgroups
  *    (K > 8192 with M <= 2048, or with M <= 4096 and 32 or more batch
  *    rows; K = 8192 with M of 2049-4096 and 32 or more batch rows;
- *    optional): one 8-byte ticket per set of
- *    32 rows and 16 batch rows, padded to 256 bytes, then fp32 partials
- *    [4, B, M]. It needs no clearing: each ticket carries the call's
- *    generation. Without it (NULL or too small) the path runs its
- *    single-pass tiles, same results within rounding.
- * Calls that overlap in time need separate workspaces. No counterpart in the
+ *    optional, 8-byte aligned): one 8-byte ticket per set of 32 rows and 16
+ *    batch rows, padded to 256 bytes, then fp32 partials [4, B, M]. Without
+ *    it (NULL or too small) the path runs its single-pass tiles, same
+ *    results within rounding.
+ * Neither needs clearing: each ticket carries the call's generation. Calls
+ * that overlap in time need separate workspaces. No counterpart in the
  * reference, whose v4 took an fp32 [B, M] buffer zeroed per call
- * (include/decode_kernel/gemv_w4a16.h:33, csrc/bindings.cpp:65-68) and whose
- * reuse path took none. Returns 0 for invalid arguments. */
+ * (include/decode_kernel/gemv_w4a16.h:33, csrc/bindings.cpp:65-68: see
+ * dk_w4a16_gemv_ref_workspace) and whose reuse path took none. Returns 0
+ * for invalid arguments. */
 size_t dk_gemv_workspace_bytes(int M, int K, int B, const dk_gemv_config* cfg);
 
 /* Host-side argument check of dk_w4a16_gemv without launching anything
@@ -101,8 +100,8 @@ int dk_gemv_validate(int M, int K, int B, const dk_gemv_config* cfg);
  * (include/decode_kernel/gemv_w4a16.h:34-36, csrc/gemv_w4a16.cu:568-591).
  * M, K or B <= 0 is a no-op returning DK_OK (csrc/gemv_w4a16.cu:571).
  * `workspace` must hold dk_gemv_workspace_bytes() bytes for v4 (may be NULL
- * if 0); on the reuse path a workspace of that size is optional and 8-byte
- * aligned.
+ * if 0); on the reuse path a workspace of that size is optional; both are
+ * 8-byte aligned.
  * Differences from the reference: launch errors are returned (the reference
  * printed and continued, csrc/gemv_w4a16.cu:9-16), and split-K is one
  * launch with a deterministic reduction instead of memset+atomics+convert. */
@@ -110,6 +109,35 @@ int dk_w4a16_gemv(const uint32_t* packed, const uint16_t* scales,
                   const uint16_t* x, uint16_t* y, int M, int K, int B,
                   const dk_gemv_config* cfg, void* workspace,
                   size_t workspace_bytes, hipStream_t stream);
+
+/* dk_w4a16_gemv with the reference's workspace contract, for callers written
+ * against decode_kernel::w4a16_gemv (include/decode_kernel/gemv_w4a16.h:29-36,
+ * csrc/gemv_w4a16.cu:474-481): for v4, `workspace` is a caller-zeroed fp32
+ * [B, M] buffer; the K slices add their fp32 row sums into it with atomics
+ * and a second kernel converts it to y (it holds the fp32 result after the
+ * call, as in the reference; the order of the adds, and so the last bit of
+ * the fp32 sums, is not fixed, also as in the reference). Every other
+ * variant ignores `workspace` and runs as dk_w4a16_gemv with none. */
+int dk_w4a16_gemv_ref_workspace(const uint32_t* packed, const uint16_t* scales,
+                                const uint16_t* x, uint16_t* y, int M, int K, int B,
+                                const dk_gemv_config* cfg, float* workspace,
+                                hipStream_t stream);
+
+/* The kernel dk_w4a16_gemv would launch for this call, without launching
+ * anything or touching a device: its demangled name (as a rocprofv3 kernel
+ * trace prints it), grid and workgroup size, and the number of launches the
+ * call makes. `workspace_bytes` is what the call would pass (it selects the
+ * reuse path's split-K tiles). No counterpart in the reference; it lets a
+ * benchmark or profile name the kernel behind a measurement. */
+typedef struct dk_launch_info {
+  char kernel[512];
+  unsigned grid[3];
+  unsigned block[3];
+  int launches;
+} dk_launch_info;
+
+int dk_gemv_describe(int M, int K, int B, const dk_gemv_config* cfg, size_t workspace_bytes,
+                     dk_launch_info* info);
 
 /* Kernel-native "paired" weight layout: the same two's-complement int4
  * nibbles and scales, with each word's nibbles permuted so that q_{2j} is at
@@ -171,7 +199,7 @@ const char* dk_last_error(void);
 
 /* ABI version of this header, (major << 16) | minor. */
 int dk_abi_version(void);
-#define DK_ABI_VERSION ((1 << 16) | 1)
+#define DK_ABI_VERSION ((1 << 16) | 2)
 
 #ifdef __cplusplus
 } /* extern "C" */

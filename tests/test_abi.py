@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.dk_abi_version() == (1 << 16) | 1
+    assert lib.dk_abi_version() == (1 << 16) | 2
 
 
 def test_default_config_matches_reference(lib):
@@ -101,17 +101,71 @@ def test_null_and_misaligned_pointers_rejected(lib):
 
 def test_split_k_workspace_contract(lib):
     cfg = _abi.default_config(lib, version=4, split_k=4)
-    # [split_k, B, M] fp32 partials (split capped at the group count), then
-    # one uint32 ticket per 4-row tile.
-    assert lib.dk_gemv_workspace_bytes(4096, 4096, 2, ctypes.byref(cfg)) == 4 * 2 * 4096 * 4 + 1024 * 4
-    assert lib.dk_gemv_workspace_bytes(64, 256, 1, ctypes.byref(cfg)) == 2 * 1 * 64 * 4 + 16 * 4
-    assert lib.dk_gemv_workspace_bytes(65, 256, 1, ctypes.byref(cfg)) == 2 * 1 * 65 * 4 + 17 * 4
+    # One 8-byte ticket per (4-row workgroup, batch tile of 1, 2 or 4 rows),
+    # padded to 256 bytes, then [split_k, B, M] fp32 partials (split capped
+    # at the group count).
+    ws = lambda m, k, b, c=cfg: lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(c))
+    assert ws(4096, 4096, 2) == 1024 * 8 + 4 * 2 * 4096 * 4   # tiles of 2 batch rows
+    assert ws(4096, 4096, 1) == 1024 * 8 + 4 * 1 * 4096 * 4
+    assert ws(4096, 4096, 5) == 2048 * 8 + 4 * 5 * 4096 * 4   # tiles of 4: two of them
+    assert ws(64, 256, 1) == 256 + 2 * 1 * 64 * 4             # 16 tickets -> 256 bytes
+    assert ws(65, 256, 1) == 256 + 2 * 1 * 65 * 4
+    assert ws(4096, 4096, 1, _abi.default_config(lib, version=4, split_k=32)) == (
+        1024 * 8 + 32 * 4096 * 4)
     for v in (0, 1, 2, 3, 5):
         c = _abi.default_config(lib, version=v)
         assert lib.dk_gemv_workspace_bytes(4096, 4096, 1, ctypes.byref(c)) == 0
     fake = 0x10000
     rc = lib.dk_w4a16_gemv(fake, fake, fake, fake, 64, 256, 1, ctypes.byref(cfg), None, 0, None)
     assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "workspace" in lib.dk_last_error().decode()
+    rc = lib.dk_w4a16_gemv(fake, fake, fake, fake, 64, 256, 1, ctypes.byref(cfg), fake + 4,
+                           ws(64, 256, 1), None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "8-byte aligned" in lib.dk_last_error().decode()
+
+
+def test_reference_workspace_contract_checks(lib):
+    # dk_w4a16_gemv_ref_workspace keeps the reference's v4 contract (a
+    # caller-zeroed fp32 [B, M] buffer, include/decode_kernel/gemv_w4a16.h:33):
+    # v4 without it is rejected before any launch; the checks of
+    # dk_w4a16_gemv come first.
+    fake = 0x10000
+    cfg = _abi.default_config(lib, version=4)
+    rc = lib.dk_w4a16_gemv_ref_workspace(fake, fake, fake, fake, 64, 256, 1, ctypes.byref(cfg),
+                                         None, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "[B, M]" in lib.dk_last_error().decode()
+    rc = lib.dk_w4a16_gemv_ref_workspace(fake, fake, fake, fake, 64, 200, 1, ctypes.byref(cfg),
+                                         fake, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "group size" in lib.dk_last_error().decode()
+    rc = lib.dk_w4a16_gemv_ref_workspace(fake, fake, fake, fake, 64, 256, 1, ctypes.byref(cfg),
+                                         fake + 2, None)
+    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "4-byte aligned" in lib.dk_last_error().decode()
+    # M, K or B <= 0: no-op, as in the reference.
+    assert lib.dk_w4a16_gemv_ref_workspace(None, None, None, None, 0, 256, 1, ctypes.byref(cfg),
+                                           None, None) == _abi.DK_OK
+
+
+def test_describe_names_the_dispatched_kernel(lib):
+    # dk_gemv_describe runs the dispatch without launching (no GPU needed) and
+    # names the kernel as a rocprofv3 trace does.
+    d = _abi.describe(lib, 4096, 4096, 1)
+    assert d["kernel"].startswith("void dk::gemv_v5_lds<1, 2, 8, 1, true, dk::LayoutLogical, 5")
+    assert d["grid"] == [512, 1, 1] and d["block"] == [512, 1, 1] and d["launches"] == 1
+    d = _abi.describe(lib, 4096, 11008, 1, version=4, split_k=4)
+    assert d["kernel"].startswith("void dk::gemv_v4_lds<") and d["grid"][2] == 4
+    assert _abi.describe(lib, 4096, 4096, 16, reuse_weights=1)["kernel"].startswith(
+        "void dk::gemv_reuse<")
+    assert _abi.describe(lib, 4096, 4096, 2, reuse_weights=1)["kernel"].startswith(
+        "void dk::gemv_v5_lds<") and ", 15, " in _abi.describe(lib, 4096, 4096, 2,
+                                                              reuse_weights=1)["kernel"]
+    # With the optional workspace the reuse path splits K; without it, not.
+    assert "gemv_reuse_split<" in _abi.describe(lib, 2048, 16384, 16, reuse_weights=1)["kernel"]
+    assert "gemv_reuse<" in _abi.describe(lib, 2048, 16384, 16, workspace_bytes=0,
+                                          reuse_weights=1)["kernel"]
+    assert _abi.describe(lib, 4096, 4096, 1, version=1, warps_per_row=4)["kernel"].startswith(
+        "dk::gemv_v1_multiwave(")
+    # Invalid calls fail as dk_w4a16_gemv would.
+    with pytest.raises(_abi.DkError, match="group size"):
+        _abi.describe(lib, 64, 200, 1)
 
 
 def test_reuse_split_workspace_size(lib):
@@ -212,7 +266,7 @@ def test_torch_extension_surface():
     for pat in (r"version: [\w.]*Int = 5", r"split_k: [\w.]*Int = 4",
                 r"reuse_weights: bool = False", r"warps_per_row: [\w.]*Int = 1"):
         assert re.search(pat, doc), (pat, doc)
-    assert _cuda.ABI_VERSION == (1 << 16) | 1
+    assert _cuda.ABI_VERSION == (1 << 16) | 2
 
 
 def test_extension_rejects_cpu_tensors():
@@ -246,6 +300,25 @@ int main() {
   }
   GemvLaunchConfig v4;
   v4.version = KernelVersion::V4;
+  // The reference's signature with its v4 contract: a null [B, M] workspace
+  // is rejected on the host, before any launch (the reference would fault).
+  try {
+    w4a16_gemv(reinterpret_cast<const uint32_t*>(0x10000), reinterpret_cast<const __half*>(0x10000),
+               reinterpret_cast<const __half*>(0x10000), reinterpret_cast<__half*>(0x10000), 64,
+               256, 1, v4, static_cast<float*>(nullptr), nullptr);
+    return 4;
+  } catch (const std::runtime_error& e) {
+    std::printf("v4 threw: %s\n", e.what());
+  }
+  // The sized overload checks the size it is given.
+  try {
+    w4a16_gemv(reinterpret_cast<const uint32_t*>(0x10000), reinterpret_cast<const __half*>(0x10000),
+               reinterpret_cast<const __half*>(0x10000), reinterpret_cast<__half*>(0x10000), 64,
+               256, 1, v4, reinterpret_cast<void*>(0x10000), size_t{64}, nullptr);
+    return 5;
+  } catch (const std::runtime_error& e) {
+    std::printf("sized threw: %s\n", e.what());
+  }
   std::printf("ws %zu %zu\n", workspace_bytes(4096, 4096, 2, v4), workspace_bytes(4096, 4096, 2, cfg));
   return 0;
 }
@@ -272,4 +345,26 @@ def test_cpp_namespace_wrapper_compiles_and_validates(tmp_path):
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert out.returncode == 0, (out.returncode, out.stdout, out.stderr)
     assert "threw: w4a16_gemv: K must be divisible by group size 128" in out.stdout
-    assert f"ws {4 * 2 * 4096 * 4 + 1024 * 4} 0" in out.stdout
+    assert "v4 threw: w4a16_gemv: v4 needs the caller-zeroed fp32 [B, M] workspace" in out.stdout
+    assert "sized threw: w4a16_gemv: split-K needs a 768-byte workspace (got 64)" in out.stdout
+    assert f"ws {1024 * 8 + 4 * 2 * 4096 * 4} 0" in out.stdout
+
+
+def test_bench_library_loads_and_stays_out_of_the_product(lib):
+    # dk_bench/libdk_bench.so holds the measurement-only kernels (read-floor
+    # probes, the load-only ablation, shape variants); the product library
+    # exports none of its entry points, and it exports only those.
+    import subprocess
+
+    from dk_bench import benchlib
+
+    blib = benchlib.load()
+    for name in benchlib.EXPORTS:
+        assert hasattr(blib, name), name
+        assert not hasattr(lib, name), name
+    syms = subprocess.run(["nm", "-D", "--defined-only", str(benchlib.LIB_PATH)],
+                          capture_output=True, text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in syms.splitlines() if " T " in ln}
+    assert exported == set(benchlib.EXPORTS), exported
+    assert benchlib.parse_v5_shape(_abi.describe(lib, 4096, 4096, 1)["kernel"]) == (1, 2, 8, True)
+    assert benchlib.parse_v5_shape(_abi.describe(lib, 4096, 4096, 1, version=4)["kernel"]) is None

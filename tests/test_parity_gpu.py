@@ -99,8 +99,12 @@ def _config_case(name, batch=1):
         m, k = CONFIGS[name]
         w, x = oracle.make_case(m, k, batch, seed=1000 + list(CONFIGS).index(name))
         packed, scales, pd, sd, xd = _upload(w, x)
-        y_ref = oracle.linear_f64(x, packed, scales) if m * k <= 64 << 20 else \
-            oracle.linear_fp32(x, packed, scales).astype(np.float64)
+        del w
+        # float64 oracle, row blocks at a time (each output row depends only
+        # on its own weight row), so the 70B shapes need ~1 GB of host memory.
+        rows = max(1, (16 << 20) // k)
+        y_ref = np.concatenate([oracle.linear_f64(x, packed[r:r + rows], scales[r:r + rows])
+                                for r in range(0, m, rows)], axis=1)
         _CASES.clear()  # keep at most one large case resident
         _CASES[key] = (pd, sd, xd, y_ref, packed, scales)
     return _CASES[key]
@@ -109,8 +113,7 @@ def _config_case(name, batch=1):
 @pytest.mark.parametrize("name", list(CONFIGS))
 def test_configs_full_size(name):
     pd, sd, xd, y_ref, _, _ = _config_case(name)
-    paths = PATHS if CONFIGS[name][0] * CONFIGS[name][1] <= 64 << 20 else FAST_PATHS
-    for label, kw in paths:
+    for label, kw in PATHS:
         print(f"[{name}] {label}", flush=True)
         y = _gemv(pd, sd, xd, **kw)
         torch.cuda.synchronize()
@@ -303,6 +306,36 @@ def test_reuse_split_graph_replays():
         torch.cuda.synchronize()
         assert torch.equal(y_graph, y_eager)
         assert torch.equal(y_between, y_eager)
+
+
+@pytest.mark.parametrize("m,k,b,split", [(4096, 11008, 1, 4), (1000, 1024, 5, 8), (77, 384, 2, 32),
+                                         (4096, 4096, 16, 4)])
+def test_v4_split_k_workspace_needs_no_clearing(m, k, b, split):
+    # v4 through the C ABI with workspaces full of different garbage: each
+    # ticket carries the call's generation, so results are bit-identical to
+    # the extension's and to each other, and meet the oracle.
+    from decode_kernel import _abi
+
+    lib = _abi.load()
+    w, x = oracle.make_case(m, k, b, seed=7 * m + b)
+    packed, scales, pd, sd, xd = _upload(w, x)
+    y_ref = oracle.linear_f64(x, packed, scales)
+    cfg = _abi.default_config(lib, version=4, split_k=split)
+    need = lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(cfg))
+    stream = torch.cuda.current_stream().cuda_stream
+    gen = torch.Generator(device="cuda").manual_seed(m + k)
+    outs = []
+    for _ in range(3):
+        ws = torch.randint(-(2 ** 62), 2 ** 62, ((need + 7) // 8,), dtype=torch.int64,
+                           device="cuda", generator=gen)
+        y = torch.empty(b, m, dtype=torch.float16, device="cuda")
+        _abi.check(lib, lib.dk_w4a16_gemv(pd.data_ptr(), sd.data_ptr(), xd.data_ptr(), y.data_ptr(),
+                                          m, k, b, ctypes.byref(cfg), ws.data_ptr(), need, stream))
+        outs.append(y)
+    torch.cuda.synchronize()
+    _check_against_oracle(outs[0], y_ref, f"v4 {m}x{k} B={b} split {split}")
+    assert all(torch.equal(o, outs[0]) for o in outs)
+    assert torch.equal(_gemv(pd, sd, xd, version=4, split_k=split), outs[0])
 
 
 @pytest.mark.parametrize("name", ["c0_4096x4096", "c2_4096x11008", "c4b_8192x28672"])
