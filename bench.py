@@ -11,10 +11,12 @@ graph, step i reading weight copy i mod n where the n copies total more than
 640 MB, as in a decode pass over many layers. Before each of 5 timed replays
 a 1 GiB read is enqueued on the same stream, outside the events: it flushes
 the L2s and the 256 MB Infinity Cache, so every replay starts cold whatever
---steps is, and it keeps the GPU busy while the host enqueues the start
-event and the graph, so the timed span is the steps alone. Per-step time =
-elapsed / steps, p50 over the 5 replays. `value` = algorithmic bytes / p50
-per-step time.
+--steps is. The timing events are nodes of the graph itself, after one
+untimed lead-in step, so they bracket exactly the `--steps` steps and not
+the fixed start cost of a graph launch (reported as
+`graph_replay_overhead_us`, with the events around the whole replay as
+`p50_us_outer`). Per-step time = elapsed / steps, p50 over the 5 replays.
+`value` = algorithmic bytes / p50 per-step time.
 
 The reference's protocol (a cache flush, then events around one call,
 bench/common.py:64-108) is reported beside it: on MI355X the event markers
@@ -567,9 +569,13 @@ def main():
         "read_roof_gbps": roof["gbps"],
         "copy_roof_gbps": copy_roof["gbps"],
         "timer": ("`warmup` untimed steps, then exactly `steps` GEMV launches back-to-back in one "
-                  "HIP graph over weight copies totalling > 640 MB; a 1 GiB read before each "
-                  "replay outside the events (cold caches, host launch hidden); events around "
-                  "the replay on its stream; p50 over 5 replays of elapsed/steps"),
+                  "HIP graph over weight copies totalling > 640 MB, after one untimed lead-in "
+                  "step; a 1 GiB read before each replay outside the events (cold caches); "
+                  "timing events recorded as graph nodes around the `steps` launches; p50 over "
+                  "5 replays of elapsed/steps"),
+        "timer_kind": headline["timer"],
+        "p50_us_outer": headline["outer_median_us"],
+        "graph_replay_overhead_us": headline["replay_overhead_us"],
         "p50_us_1000_steps": (headline_long["median_us"] if headline_long is not None
                               else headline["median_us"]),
         "same_size_read_gbps": results["c0_B1"]["same_size_read"]["gbps"],

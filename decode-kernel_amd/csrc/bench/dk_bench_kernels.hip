@@ -233,6 +233,16 @@ __global__ __launch_bounds__(W * kWave) void gemv_onestage(const uint4* __restri
   }
 }
 
+// ---------------------------------------------------------------------------
+// Timestamp: one lane writes the GPU's constant-rate wall clock
+// (s_memrealtime, hipDeviceAttributeWallClockRate kHz) to dst[slot] with a
+// vector store. Two of them inside a captured graph bracket the launches
+// between them on the GPU's own clock.
+// ---------------------------------------------------------------------------
+__global__ void timestamp_kernel(unsigned long long* __restrict__ dst, int slot) {
+  if (threadIdx.x == 0) dst[slot] = __builtin_amdgcn_s_memrealtime();
+}
+
 }  // namespace dkb
 
 namespace {
@@ -399,4 +409,21 @@ DKB_API int dkb_v4(int R, int U, int W, int prefetch, int reduce, int S, const v
 #undef DKB_V4R
 #undef DKB_V4
   return 3;
+}
+
+// Writes the wall clock to ((uint64_t*)dst)[slot] on `stream`.
+DKB_API int dkb_timestamp(void* dst, int slot, hipStream_t stream) {
+  if (!dst || slot < 0) return 1;
+  hipLaunchKernelGGL(dkb::timestamp_kernel, dim3(1), dim3(64), 0, stream,
+                     static_cast<unsigned long long*>(dst), slot);
+  return launch_error("timestamp");
+}
+
+// Rate of the clock dkb_timestamp reads, in kHz, for the current device
+// (<= 0 on error).
+DKB_API int dkb_wall_clock_khz(void) {
+  int dev = 0, khz = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess) return -1;
+  return khz;
 }

@@ -18,6 +18,8 @@ _SIGNATURES = {
     "dkb_onestage": (_I, [_I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P]),
     "dkb_v4": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, ctypes.c_ulonglong, _I, _I,
                     _P]),
+    "dkb_timestamp": (_I, [_P, _I, _P]),
+    "dkb_wall_clock_khz": (_I, []),
 }
 EXPORTS = tuple(_SIGNATURES)
 
@@ -92,3 +94,12 @@ def parse_v5_shape(kernel_name: str) -> tuple | None:
     if nb != 1:
         return None
     return (r, u, w, args[4] == "true")
+
+
+def timestamp(buf, slot: int) -> None:
+    """Write the GPU wall clock to buf[slot] (int64 tensor) on the current stream."""
+    check(load().dkb_timestamp(buf.data_ptr(), slot, stream_handle()), "timestamp")
+
+
+def wall_clock_khz() -> int:
+    return int(load().dkb_wall_clock_khz())

@@ -153,33 +153,14 @@ def weight_copies(packed: torch.Tensor, scales: torch.Tensor,
     return [packed.clone() for _ in range(n)], [scales.clone() for _ in range(n)]
 
 
-def time_graph_steps(step: Callable[[int], object], steps: int, trials: int = 5,
-                     warmup: int = 1, preroll: Optional[Callable[[], None]] = None) -> dict:
-    """Per-step time of exactly `steps` back-to-back steps, `step(i)` for
-    i = 0..steps-1, captured in one HIP graph and replayed `trials` times.
-
-    `warmup` untimed eager steps run first (at least one: allocator and code
-    objects), then one untimed replay loads the graph. Before each timed
-    replay `preroll` (a 1 GiB read, ~0.2 ms) is enqueued on the same stream
-    outside the events: the GPU is busy with it while the host enqueues the
-    start event and the graph's launches, so the timed span holds only the
-    steps back-to-back, whatever `steps` is, and every replay starts with
-    the L2s and the Infinity Cache flushed. Each replay is bracketed by
-    events on the stream it runs on; per-step time = elapsed / steps."""
+def _replays(graph, trials, preroll, after=None):
+    """`trials` replays, each after `preroll` and bracketed by events on the
+    replay stream; returns the outer times in us and the `after()` values."""
     import time
 
-    for i in range(max(1, warmup)):
-        step(i % steps)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(steps):
-            step(i)
-    graph.replay()
-    torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    per, walls = [], []
+    outer, extra, walls = [], [], []
     for _ in range(trials):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -190,10 +171,89 @@ def time_graph_steps(step: Callable[[int], object], steps: int, trials: int = 5,
         end.record()
         torch.cuda.synchronize()
         walls.append(time.perf_counter() - t0)
-        per.append(start.elapsed_time(end) * 1000.0 / steps)
-    out = _stats(per)
+        outer.append(start.elapsed_time(end) * 1000.0)
+        if after is not None:
+            extra.append(after())
+    return outer, extra, walls
+
+
+_BRACKET = {}  # (trials) -> cost of the timestamp bracket itself, in clock ticks
+
+
+def time_graph_steps(step: Callable[[int], object], steps: int, trials: int = 5,
+                     warmup: int = 1, preroll: Optional[Callable[[], None]] = None) -> dict:
+    """Per-step time of exactly `steps` back-to-back steps, `step(i)` for
+    i = 0..steps-1, captured in one HIP graph and replayed `trials` times.
+
+    `warmup` untimed eager steps run first (at least one: allocator and code
+    objects), then one untimed replay loads the graph. Before each timed
+    replay `preroll` (a 1 GiB read, ~0.2 ms) is enqueued on the same stream
+    outside the timed span: every replay starts with the L2s and the
+    Infinity Cache flushed.
+
+    The timed span is bracketed on the GPU's own clock: the graph is [one
+    untimed lead-in step (`step(steps)`, the next weight copy), a timestamp
+    kernel, the `steps` steps, a timestamp kernel]; the two timestamps
+    (s_memrealtime, a vector store each) bracket exactly the timed steps,
+    and the cost of the bracket itself, measured by a graph of the two
+    timestamp kernels alone, is subtracted. A graph launch's fixed start
+    cost (about 10 us per replay on MI355X) thus falls outside the span,
+    as it does when a decode pass replays one graph over hundreds of kernels.
+    Events around the whole replay on the host's side are kept beside it
+    (`outer_median_us`, per step), and their difference per replay is
+    `replay_overhead_us`. Without the bench library the outer events are the
+    measurement. Per-step time = span / steps; p50 over the replays."""
+    try:
+        from . import benchlib
+
+        khz = benchlib.wall_clock_khz()
+        inner = khz > 0
+    except Exception:
+        inner, khz = False, 0
+    for i in range(max(1, warmup)):
+        step(i % steps)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    if inner:
+        ts = torch.zeros(2, dtype=torch.int64, device="cuda")
+        with torch.cuda.graph(graph):
+            step(steps)  # lead-in, untimed
+            benchlib.timestamp(ts, 0)
+            for i in range(steps):
+                step(i)
+            benchlib.timestamp(ts, 1)
+        if trials not in _BRACKET:
+            tb = torch.zeros(2, dtype=torch.int64, device="cuda")
+            bracket = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(bracket):
+                benchlib.timestamp(tb, 0)
+                benchlib.timestamp(tb, 1)
+            bracket.replay()
+            _, ticks, _ = _replays(bracket, 2 * trials, preroll,
+                                   lambda: int(tb[1].item()) - int(tb[0].item()))
+            _BRACKET[trials] = sorted(ticks)[len(ticks) // 2]
+    else:
+        with torch.cuda.graph(graph):
+            for i in range(steps):
+                step(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    if inner:
+        outer, ticks, walls = _replays(graph, trials, preroll,
+                                       lambda: int(ts[1].item()) - int(ts[0].item()))
+        per_in = [(t - _BRACKET[trials]) * 1e3 / khz / steps for t in ticks]
+        if not all(0.0 < a <= b / steps * 1.001 for a, b in zip(per_in, outer)):
+            inner = False  # implausible: the outer events bound the bracketed span
+    else:
+        outer, _, walls = _replays(graph, trials, preroll)
+    per_out = [o / steps for o in outer]
+    out = _stats(per_in if inner else per_out)
     out.update({"steps": steps, "trials": trials, "warmup": max(1, warmup),
-                "timer": "events_around_graph_replay",
+                "timer": "gpu_clock_bracket_in_graph" if inner else "events_around_graph_replay",
+                "outer_median_us": _stats(per_out)["median_us"],
+                "replay_overhead_us": ((_stats(per_out)["median_us"] - out["median_us"]) * steps
+                                       if inner else None),
+                "bracket_us": _BRACKET[trials] * 1e3 / khz if inner else None,
                 "preroll": "1 GiB read before each replay" if preroll is not None else None,
                 "wall_s_per_replay": statistics.fmean(walls)})
     return out, graph
