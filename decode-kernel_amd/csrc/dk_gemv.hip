@@ -19,6 +19,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <string>
 
 #include "dk_host.hpp"
@@ -702,6 +703,53 @@ int gemv_ref_workspace_impl(const uint32_t* packed, const uint16_t* scales, cons
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Library-owned scratch for dk_w4a16_gemv_noalloc: the workspace of the
+// split-K paths (v4, and the reuse path's split-K tiles) in a file-scope
+// device array, so that a call allocates nothing. Every GPU the library runs
+// on holds its own copy (DK_NOALLOC_SCRATCH_BYTES) until the process ends. Its
+// device address is taken once per device with hipGetSymbolAddress, with
+// that device current, and only that address is used from the host (the
+// array's name is a host-side stand-in). Nothing in it must start at zero:
+// the tickets carry each call's generation (take_ticket), and the partials
+// are written before they are read. Calls that overlap in time on one GPU
+// share it and race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[DK_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr size_t kNoallocScratchBytes = DK_NOALLOC_SCRATCH_BYTES;
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The current device's address of `scratch` (set up on the first call on
+// that device).
+int scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return dk::hip_error(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(DK_ERR_UNSUPPORTED, "device %d beyond the %d devices the scratch supports", dev,
+                kMaxDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return dk::hip_error(e, "hipGetSymbolAddress(scratch)");
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return DK_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 void dk_gemv_config_default(dk_gemv_config* cfg) {
@@ -747,6 +795,31 @@ int dk_w4a16_gemv(const uint32_t* packed, const uint16_t* scales, const uint16_t
                   int M, int K, int B, const dk_gemv_config* cfg, void* workspace,
                   size_t workspace_bytes, hipStream_t stream) {
   return gemv_impl(packed, scales, x, y, M, K, B, cfg, workspace, workspace_bytes, Launch{stream});
+}
+
+int dk_w4a16_gemv_noalloc(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
+                          uint16_t* y, int M, int K, int B, const dk_gemv_config* cfg,
+                          hipStream_t stream) {
+  int rc = dk_gemv_validate(M, K, B, cfg);
+  if (rc != DK_OK) return rc;
+  if (M <= 0 || K <= 0 || B <= 0) return DK_OK;
+  const size_t need = dk_gemv_workspace_bytes(M, K, B, cfg);
+  if (need == 0) return gemv_impl(packed, scales, x, y, M, K, B, cfg, nullptr, 0, Launch{stream});
+  if (need > kNoallocScratchBytes) {
+    // The reuse path's split-K tiles are optional: the single-pass tiles run.
+    if (cfg->reuse_weights)
+      return gemv_impl(packed, scales, x, y, M, K, B, cfg, nullptr, 0, Launch{stream});
+    return fail(DK_ERR_UNSUPPORTED,
+                "split-K needs %zu bytes of workspace; dk_w4a16_gemv_noalloc holds %zu (call "
+                "dk_w4a16_gemv with a workspace)",
+                need, kNoallocScratchBytes);
+  }
+  rc = check_io(packed, scales, x, y);
+  if (rc != DK_OK) return rc;
+  void* ws = nullptr;
+  rc = scratch_ptr(&ws);
+  if (rc != DK_OK) return rc;
+  return gemv_impl(packed, scales, x, y, M, K, B, cfg, ws, kNoallocScratchBytes, Launch{stream});
 }
 
 int dk_w4a16_gemv_ref_workspace(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,

@@ -17,6 +17,7 @@ DK_OK = 0
 DK_ERR_INVALID_ARGUMENT = 1
 DK_ERR_HIP = 2
 DK_ERR_UNSUPPORTED = 3
+DK_NOALLOC_SCRATCH_BYTES = 8 << 20  # include/decode_kernel/dk_gemv.h
 
 
 class GemvConfig(ctypes.Structure):
@@ -62,6 +63,11 @@ _SIGNATURES = {
         ctypes.c_int,
         [_P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
          ctypes.POINTER(GemvConfig), _P, _P],
+    ),
+    "dk_w4a16_gemv_noalloc": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+         ctypes.POINTER(GemvConfig), _P],
     ),
     "dk_gemv_describe": (
         ctypes.c_int,

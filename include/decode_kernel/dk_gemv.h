@@ -110,6 +110,24 @@ int dk_w4a16_gemv(const uint32_t* packed, const uint16_t* scales,
                   const dk_gemv_config* cfg, void* workspace,
                   size_t workspace_bytes, hipStream_t stream);
 
+/* Size of the per-GPU device array behind dk_w4a16_gemv_noalloc. */
+#define DK_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+
+/* dk_w4a16_gemv for callers that cannot allocate: code under HIP graph
+ * capture, tight serving loops, hosts that forbid hipMalloc. No counterpart
+ * in the reference. The split-K paths (v4, and the reuse path's split-K
+ * tiles) take their workspace from a library-owned device array of
+ * DK_NOALLOC_SCRATCH_BYTES (8 MiB) on each GPU, held until the process
+ * ends; nothing is allocated, cleared or freed by a call. A v4 call
+ * whose dk_gemv_workspace_bytes() exceeds it returns DK_ERR_UNSUPPORTED
+ * before any launch; the reuse path then runs its single-pass tiles. Every
+ * call on one GPU shares that GPU's array: calls that overlap in time on one
+ * GPU (different streams, or host threads) race and must not be issued.
+ * Arguments, checks and results otherwise as dk_w4a16_gemv. */
+int dk_w4a16_gemv_noalloc(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
+                          uint16_t* y, int M, int K, int B, const dk_gemv_config* cfg,
+                          hipStream_t stream);
+
 /* dk_w4a16_gemv with the reference's workspace contract, for callers written
  * against decode_kernel::w4a16_gemv (include/decode_kernel/gemv_w4a16.h:29-36,
  * csrc/gemv_w4a16.cu:474-481): for v4, `workspace` is a caller-zeroed fp32

@@ -1,0 +1,135 @@
+"""dk_w4a16_gemv_noalloc, the entry point that allocates nothing, through the
+C ABI against dk_w4a16_gemv with a caller workspace (same kernels, so the
+same bits), on two calls in a row per path, the second with a smaller input:
+split-K v4, the reuse path's split-K tiles, and a path without scratch. Also:
+a v4 call whose workspace exceeds the scratch is refused before any launch,
+the reuse path then runs its single-pass tiles, and a captured call replays
+with eager calls of other shapes between the replays.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _lib():
+    from decode_kernel import _abi
+
+    return _abi, _abi.load()
+
+
+def _case(m, k, b, seed):
+    w, x = oracle.make_case(m, k, b, seed=seed, w_std=0.05)
+    packed, scales = oracle.quantize_and_pack(w)
+    y_ref = oracle.linear_f64(x, packed, scales)
+    return (torch.from_numpy(packed).cuda(), torch.from_numpy(scales).cuda(),
+            torch.from_numpy(x).cuda(), y_ref)
+
+
+def _call_noalloc(lib, cfg, pd, sd, xd, y, m, k, b):
+    return lib.dk_w4a16_gemv_noalloc(pd.data_ptr(), sd.data_ptr(), xd.data_ptr(), y.data_ptr(),
+                                     m, k, b, ctypes.byref(cfg),
+                                     torch.cuda.current_stream().cuda_stream)
+
+
+def _call_ws(abi, lib, cfg, pd, sd, xd, m, k, b, with_ws=True):
+    need = lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(cfg)) if with_ws else 0
+    ws = (torch.randint(-(2 ** 62), 2 ** 62, ((need + 7) // 8,), dtype=torch.int64, device="cuda")
+          if need else None)
+    y = torch.empty(b, m, dtype=torch.float16, device="cuda")
+    abi.check(lib, lib.dk_w4a16_gemv(pd.data_ptr(), sd.data_ptr(), xd.data_ptr(), y.data_ptr(), m,
+                                     k, b, ctypes.byref(cfg), ws.data_ptr() if need else None,
+                                     need, torch.cuda.current_stream().cuda_stream))
+    return y
+
+
+def _tight(y, y_ref, label):
+    err = np.abs(y.float().cpu().numpy().astype(np.float64) - y_ref)
+    assert err.max() < 1e-2, f"{label}: {err.max():.3e}"
+    assert (err <= 0.5 * oracle.fp16_ulp(y_ref) + 1e-3).all(), label
+
+
+# (config, first call (M, K, B), second, smaller call)
+PATHS = [
+    (dict(version=4, split_k=4), (4096, 11008, 1), (1000, 1024, 3)),
+    (dict(version=4, split_k=32), (2048, 8192, 5), (77, 384, 2)),
+    (dict(version=5, reuse_weights=1), (2048, 16384, 16), (1024, 12416, 17)),
+    (dict(version=5), (4096, 4096, 1), (333, 640, 2)),
+]
+
+
+@pytest.mark.parametrize("cfg,first,second", PATHS)
+def test_noalloc_matches_the_workspace_entry(cfg, first, second):
+    abi, lib = _lib()
+    c = abi.default_config(lib, **cfg)
+    for (m, k, b), seed in ((first, 1), (second, 2)):
+        print(f"[noalloc] {cfg} M={m} K={k} B={b}", flush=True)
+        need = lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(c))
+        assert need <= abi.DK_NOALLOC_SCRATCH_BYTES
+        pd, sd, xd, y_ref = _case(m, k, b, seed=seed + m)
+        y = torch.empty(b, m, dtype=torch.float16, device="cuda")
+        abi.check(lib, _call_noalloc(lib, c, pd, sd, xd, y, m, k, b))
+        y_ws = _call_ws(abi, lib, c, pd, sd, xd, m, k, b)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ws), f"{cfg} M={m} K={k} B={b}: differs from dk_w4a16_gemv"
+        _tight(y, y_ref, f"noalloc {cfg} M={m} K={k} B={b}")
+
+
+def test_noalloc_refuses_v4_beyond_the_scratch():
+    abi, lib = _lib()
+    m, k, b = 28672, 8192, 16
+    c = abi.default_config(lib, version=4, split_k=32)
+    assert lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(c)) > abi.DK_NOALLOC_SCRATCH_BYTES
+    # Checked on the host before anything is launched: small stand-in buffers.
+    pd = torch.zeros(16, dtype=torch.int32, device="cuda")
+    y = torch.full((4,), 7.0, dtype=torch.float16, device="cuda")
+    rc = lib.dk_w4a16_gemv_noalloc(pd.data_ptr(), pd.data_ptr(), pd.data_ptr(), y.data_ptr(), m,
+                                   k, b, ctypes.byref(c), torch.cuda.current_stream().cuda_stream)
+    assert rc == abi.DK_ERR_UNSUPPORTED
+    assert "dk_w4a16_gemv_noalloc holds" in lib.dk_last_error().decode()
+    torch.cuda.synchronize()
+    assert bool((y == 7.0).all())
+
+
+def test_noalloc_reuse_beyond_the_scratch_runs_single_pass_tiles():
+    abi, lib = _lib()
+    m, k, b = 4096, 11008, 128
+    c = abi.default_config(lib, reuse_weights=1)
+    assert lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(c)) > abi.DK_NOALLOC_SCRATCH_BYTES
+    pd, sd, xd, _ = _case(m, k, b, seed=3)
+    y = torch.empty(b, m, dtype=torch.float16, device="cuda")
+    abi.check(lib, _call_noalloc(lib, c, pd, sd, xd, y, m, k, b))
+    y_single = _call_ws(abi, lib, c, pd, sd, xd, m, k, b, with_ws=False)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_single)
+
+
+def test_noalloc_graph_replays_with_eager_calls_between():
+    abi, lib = _lib()
+    c = abi.default_config(lib, version=4, split_k=8)
+    m, k, b = 2048, 8192, 3
+    pd, sd, xd, y_ref = _case(m, k, b, seed=4)
+    p2, s2, x2, y2_ref = _case(1000, 2048, 1, seed=5)
+    y_eager = torch.empty(b, m, dtype=torch.float16, device="cuda")
+    abi.check(lib, _call_noalloc(lib, c, pd, sd, xd, y_eager, m, k, b))
+    torch.cuda.synchronize()
+    y_graph = torch.empty(b, m, dtype=torch.float16, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        abi.check(lib, _call_noalloc(lib, c, pd, sd, xd, y_graph, m, k, b))
+    for rep in range(4):
+        graph.replay()
+        y_between = torch.empty(1, 1000, dtype=torch.float16, device="cuda")
+        abi.check(lib, _call_noalloc(lib, c, p2, s2, x2, y_between, 1000, 2048, 1))
+        torch.cuda.synchronize()
+        assert torch.equal(y_graph, y_eager), f"replay {rep}"
+        _tight(y_between, y2_ref, f"eager call between replays {rep}")
+    _tight(y_graph, y_ref, "graph")
