@@ -11,12 +11,14 @@ graph, step i reading weight copy i mod n where the n copies total more than
 640 MB, as in a decode pass over many layers. Before each of 5 timed replays
 a 1 GiB read is enqueued on the same stream, outside the events: it flushes
 the L2s and the 256 MB Infinity Cache, so every replay starts cold whatever
---steps is. The timing events are nodes of the graph itself, after one
-untimed lead-in step, so they bracket exactly the `--steps` steps and not
-the fixed start cost of a graph launch (reported as
-`graph_replay_overhead_us`, with the events around the whole replay as
-`p50_us_outer`). Per-step time = elapsed / steps, p50 over the 5 replays.
-`value` = algorithmic bytes / p50 per-step time.
+--steps is. The timed span is bracketed inside the graph on the GPU's own
+clock: after one untimed lead-in step, a timestamp kernel (s_memrealtime,
+100 MHz), the `--steps` steps, a second timestamp kernel; the bracket's own
+cost, measured by a graph of the two timestamps alone, is subtracted. So the
+span holds exactly the timed steps and not the fixed start cost of a graph
+launch, which is reported as `graph_replay_overhead_us` (events around the
+whole replay: `p50_us_outer`). Per-step time = span / steps, p50 over the 5
+replays. `value` = algorithmic bytes / p50 per-step time.
 
 The reference's protocol (a cache flush, then events around one call,
 bench/common.py:64-108) is reported beside it: on MI355X the event markers
@@ -570,9 +572,9 @@ def main():
         "copy_roof_gbps": copy_roof["gbps"],
         "timer": ("`warmup` untimed steps, then exactly `steps` GEMV launches back-to-back in one "
                   "HIP graph over weight copies totalling > 640 MB, after one untimed lead-in "
-                  "step; a 1 GiB read before each replay outside the events (cold caches); "
-                  "timing events recorded as graph nodes around the `steps` launches; p50 over "
-                  "5 replays of elapsed/steps"),
+                  "step; a 1 GiB read before each replay, outside the timed span (cold caches); "
+                  "the span bracketed inside the graph by two GPU wall-clock timestamp kernels, "
+                  "the bracket's own cost subtracted; p50 over 5 replays of span/steps"),
         "timer_kind": headline["timer"],
         "p50_us_outer": headline["outer_median_us"],
         "graph_replay_overhead_us": headline["replay_overhead_us"],
