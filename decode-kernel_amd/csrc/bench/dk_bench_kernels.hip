@@ -12,9 +12,11 @@
 //  * one-stage GEMV variants for short rows (K <= 4096): activations through
 //    LDS or per wave in registers, weights issued first or last, one or two
 //    waves per row;
-//  * every instance of the split-K kernel (gemv_v4_lds) that the v4 shape
-//    sweep times, including one that stores its partials and stops, which
-//    prices the cross-workgroup reduction.
+//  * split-K over workgroups with a ticket reduction (gemv_v4_lds, the form
+//    the product's v4 replaced), including an instance that stores its
+//    partials and stops, which prices the cross-workgroup reduction, and the
+//    product's split-over-waves v4 at every shape the v4 sweep times;
+//  * timestamps on the GPU's wall clock for the benchmark timer.
 // Outputs of the ablation kernels are meaningless by design; every other
 // kernel here computes the GEMV (checked against the product by the tools).
 #include <hip/hip_runtime.h>
@@ -234,6 +236,96 @@ __global__ __launch_bounds__(W * kWave) void gemv_onestage(const uint4* __restri
 }
 
 // ---------------------------------------------------------------------------
+// Split-K over workgroups, the form the product's v4 replaced (measured by
+// dk_bench.levers v4 beside it). grid = (row blocks of W R rows, batch tiles
+// of NB rows, S slices); workgroup (x, y, z) streams its rows over group
+// slice z with the stage loop of v5 (LDS-shared activations, buffer loads
+// through descriptors scoped to the slice). Each wave stores its fp32 row
+// sums to partials[z][b][row] with agent-scope stores (past the non-coherent
+// per-XCD L2s) and waits for them; thread 0 then takes the ticket of its
+// (row block, batch tile) (take_ticket). The last of the S workgroups adds
+// the S partials in slice order and writes y. kReduce 0: that reduction;
+// kReduce 2: store the partials and stop, without y (prices the reduction,
+// about 2 us on MI355X: the stores, the ticket and the reads each cross the
+// XCDs through memory).
+// ---------------------------------------------------------------------------
+constexpr int kV4Tickets = 0;
+
+template <int R, int U, int W, int NB, bool kPrefetch, int kReduce>
+__global__ __launch_bounds__(W * kWave) void gemv_v4_lds(const uint4* __restrict__ packed,
+                                                         const uint16_t* __restrict__ scales,
+                                                         const uint4* __restrict__ x4,
+                                                         uint16_t* __restrict__ y,
+                                                         float* __restrict__ ws,
+                                                         unsigned long long* __restrict__ tickets,
+                                                         unsigned long long gen, int M, int K,
+                                                         int B) {
+  write_stamp(4);
+  __shared__ LdsActs<U, NB> xs;
+  __shared__ int last;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nblk = (M + W * R - 1) / (W * R);
+  const int wg = xcd_contiguous_block(blockIdx.x, nblk);
+  const int row0 = (wg * W + wave) * R;
+  const bool active = row0 < M;  // wave-uniform
+  const int b0 = blockIdx.y * NB;
+  const int S = gridDim.z;
+  const int z = blockIdx.z;
+  const int nck = K >> 5;
+  const int G = K >> 7;
+  const int gps = (G + S - 1) / S;
+  const int gbeg = min(z * gps, G);
+  const int Gs = min(gbeg + gps, G) - gbeg;  // groups of this slice (0 if none)
+  const int rows = active ? min(R, M - row0) : 0;
+  const int rbase = active ? row0 : 0;
+  // The slice of row r is chunks [4 gbeg, 4 (gbeg + Gs)) at r * nck chunks
+  // from the descriptor base; the range ends after the last row's slice.
+  const auto rw = buffer_rsrc(packed + (size_t)rbase * nck + (size_t)gbeg * 4,
+                              rows > 0 ? (uint32_t)((rows - 1) * (K / 2) + Gs * 64) : 0u);
+  const auto rs = buffer_rsrc(scales + (size_t)rbase * G + gbeg,
+                              rows > 0 ? (uint32_t)(((rows - 1) * G + Gs) * 2) : 0u);
+  const auto rx = buffer_rsrc(x4 + (size_t)gbeg * 16, (uint32_t)((size_t)B * K * 2 - (size_t)gbeg * 256));
+
+  float acc[NB][R];
+  lds_stream<R, U, W, NB, kPrefetch, LayoutLogical, R>(xs, acc, rw, rs, rw, rs, rx, 4 * Gs, nck, G,
+                                                        K, b0, B, tid, lane);
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float t = wave_sum(acc[b][r]);
+      if (active && lane == 63 && row0 + r < M && b0 + b < B) {
+        const size_t o = (size_t)(b0 + b) * M + row0 + r;
+        __hip_atomic_store(&ws[(size_t)z * B * M + o], t, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  if constexpr (kReduce == kV4Tickets) {
+    // Every wave's partial stores are complete before the ticket is taken.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    unsigned long long* ticket = &tickets[(size_t)blockIdx.y * nblk + wg];
+    if (tid == 0) last = take_ticket(ticket, gen, S);
+    __syncthreads();
+    if (!last) return;
+    constexpr int kOut = W * R * NB;
+    for (int t = tid; t < kOut; t += W * kWave) {
+      const int row = wg * W * R + t % (W * R);
+      const int b = b0 + t / (W * R);
+      if (row >= M || b >= B) continue;
+      float sum = 0.f;
+      for (int s = 0; s < S; ++s)
+        sum += __hip_atomic_load(&ws[((size_t)s * B + b) * M + row], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      y[(size_t)b * M + row] = f2h(sum);
+    }
+    if (tid == 0) release_ticket(ticket, gen);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Timestamp: one lane writes the GPU's constant-rate wall clock
 // (s_memrealtime, hipDeviceAttributeWallClockRate kHz) to dst[slot] with a
 // vector store. Two of them inside a captured graph bracket the launches
@@ -389,7 +481,7 @@ DKB_API int dkb_v4(int R, int U, int W, int prefetch, int reduce, int S, const v
   if (S < 1 || S > 32) return 1;
 #define DKB_V4(r, u, w, pf, red)                                                                  \
   if (R == r && U == u && W == w && (prefetch != 0) == pf && reduce == red) {                    \
-    hipLaunchKernelGGL((dk::gemv_v4_lds<r, u, w, 1, pf, red>), dim3((M + w * r - 1) / (w * r), 1, S), \
+    hipLaunchKernelGGL((dkb::gemv_v4_lds<r, u, w, 1, pf, red>), dim3((M + w * r - 1) / (w * r), 1, S), \
                        dim3(w * 64), 0, stream, p, s, xx, yy, ws, t, gen, M, K, 1);              \
     return launch_error("v4");                                                                    \
   }
@@ -426,4 +518,27 @@ DKB_API int dkb_wall_clock_khz(void) {
   if (hipGetDevice(&dev) != hipSuccess) return -1;
   if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess) return -1;
   return khz;
+}
+
+// The split-over-waves v4 (gemv_v4_waves, B = 1) with R rows per workgroup,
+// U chunks per lane per stage and S slices. Returns 3 if not instantiated or
+// if the activation stage would exceed 64 KiB of LDS.
+DKB_API int dkb_v4_waves(int R, int U, int S, const void* packed, const void* scales, const void* x,
+                         void* y, int M, int K, hipStream_t stream) {
+  if (S < 1 || R * S > 16 || S * U > 16) return 3;
+  const auto* p = static_cast<const uint4*>(packed);
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* xx = static_cast<const uint4*>(x);
+  auto* yy = static_cast<uint16_t*>(y);
+  const size_t lds = (size_t)S * U * 4 * 64 * 16;
+#define DKB_V4W(r, u)                                                                          \
+  if (R == r && U == u) {                                                                      \
+    hipLaunchKernelGGL((dk::gemv_v4_waves<r, u, 1>), dim3((M + r - 1) / r), dim3(r * S * 64), lds, \
+                       stream, p, s, xx, yy, static_cast<float*>(nullptr), M, K, 1, S);        \
+    return launch_error("v4 waves");                                                           \
+  }
+  DKB_V4W(1, 1) DKB_V4W(1, 2) DKB_V4W(1, 4) DKB_V4W(2, 1) DKB_V4W(2, 2) DKB_V4W(2, 4)
+  DKB_V4W(4, 1) DKB_V4W(4, 2) DKB_V4W(4, 4) DKB_V4W(8, 1) DKB_V4W(8, 2)
+#undef DKB_V4W
+  return 3;
 }

@@ -7,9 +7,9 @@
 //     printed launch errors and returned garbage, csrc/gemv_w4a16.cu:9-16);
 //   * work is issued on the current HIP stream of the tensors' device under a
 //     device guard (the reference assumed the current device);
-//   * the split-K workspace comes from torch's caching allocator and needs
-//     no clearing (the reference zeroed a [B, M] fp32 buffer,
-//     csrc/bindings.cpp:65-68).
+//   * v4 needs no workspace (the reference zeroed a [B, M] fp32 buffer per
+//     call, csrc/bindings.cpp:65-68); the reuse path's split-K tiles take
+//     one from torch's caching allocator, with no clearing.
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
@@ -94,9 +94,10 @@ torch::Tensor gemv_common(torch::Tensor packed, torch::Tensor scales, torch::Ten
   cfg.reuse_weights = reuse_weights ? 1 : 0;
   cfg.warps_per_row = warps_per_row;
 
-  // v4 and the reuse path's split-K tiles take a workspace from the caching
+  // The reuse path's split-K tiles take a workspace from the caching
   // allocator: tickets that carry the call's generation, then fp32 partials,
-  // so it needs no clearing (8-byte words keep it 8-byte aligned).
+  // so it needs no clearing (8-byte words keep it 8-byte aligned). No other
+  // path, v4 included, takes one.
   const size_t ws_bytes = dk_gemv_workspace_bytes(M, K, B, &cfg);
   torch::Tensor workspace;
   void* ws_ptr = nullptr;

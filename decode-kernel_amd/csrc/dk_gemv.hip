@@ -545,53 +545,54 @@ int effective_split(int K, int split_k) {
   return std::max(1, std::min(split_k, G));
 }
 
-// v4 (split-K) launch plan: S slices of ceil(G / S) groups; four one-row
-// waves per workgroup; U 16-byte chunks per lane per stage, so that a slice
-// of up to 256 chunks is one stage; NB batch rows per stage.
-constexpr int kV4Rows = 4;  // rows per workgroup (W R) of every v4 instance
+// v4 (split-K) launch plan: S = min(split_k, K / 128, 16) slices of
+// ceil(G / S) groups, each on its own wave; R rows per workgroup (a power of
+// two, R S <= 16 waves); U 16-byte chunks per lane per stage; NB batch rows
+// per stage. The activation stage in LDS is S NB U 4 KiB, kept within
+// 64 KiB. From a sweep of R (1-8), U (1-4) and S (1-16) at eight shapes
+// (M from 512 to 8192, K from 4096 to 28672; dk_bench.levers v4), the best
+// shapes for a given S take R = 2 at M <= 512 and 4 above (8 at S <= 2 from
+// M = 4096), and stages that cover a slice once (M <= 1024) or twice.
 struct V4Plan {
-  int S, U, NB;
+  int S, R, U, NB;
 };
 
-V4Plan v4_plan(int K, int B, int split_k) {
+V4Plan v4_plan(int M, int K, int B, int split_k) {
   V4Plan p;
-  p.S = effective_split(K, split_k);
   const int G = K / DK_GROUP_SIZE;
-  const int slice_chunks = 4 * ((G + p.S - 1) / p.S);
-  p.U = slice_chunks <= 64 ? 1 : slice_chunks <= 128 ? 2 : 4;
+  p.S = std::max(1, std::min({split_k, G, 16}));
+  int r = M <= 512 ? 2 : (p.S <= 2 && M >= 4096) ? 8 : 4;
+  while (r > 1 && r * p.S > 16) r /= 2;
+  p.R = r;
   p.NB = B == 1 ? 1 : B == 2 ? 2 : 4;
+  while (p.NB > 1 && p.S * p.NB > 16) p.NB /= 2;
+  const int slice_chunks = 4 * ((G + p.S - 1) / p.S);
+  const int per_stage = M <= 1024 ? slice_chunks : (slice_chunks + 1) / 2;
+  p.U = per_stage <= 64 ? 1 : per_stage <= 128 ? 2 : 4;
+  while (p.U > 1 && p.S * p.NB * p.U > 16) p.U /= 2;
   return p;
 }
 
-// v4 workspace: one 8-byte ticket per (workgroup, batch tile), padded to 256
-// bytes, then fp32 partials [S, B, M].
-size_t v4_ticket_bytes(int M, int B, const V4Plan& p) {
-  const size_t n = (size_t)((M + kV4Rows - 1) / kV4Rows) * (size_t)((B + p.NB - 1) / p.NB);
-  return (n * 8 + 255) / 256 * 256;
-}
+size_t v4_lds_bytes(const V4Plan& p) { return (size_t)p.S * p.NB * p.U * 4 * 64 * 16; }
 
-size_t v4_workspace_bytes(int M, int K, int B, int split_k) {
-  const V4Plan p = v4_plan(K, B, split_k);
-  return v4_ticket_bytes(M, B, p) + (size_t)p.S * B * M * sizeof(float);
-}
-
-template <int U, int NB, int kReduce>
+template <int R, int U, int NB>
 int launch_v4_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
-                float* ws, unsigned long long* tickets, unsigned long long gen, int M, int K, int B,
-                int S) {
-  const dim3 grid((M + kV4Rows - 1) / kV4Rows, (B + NB - 1) / NB, S);
-  return L("v4 launch", dk::gemv_v4_lds<1, U, kV4Rows, NB, true, kReduce>, grid,
-           dim3(kV4Rows * 64), 0, p, s, x, y, ws, tickets, gen, M, K, B);
+                float* acc, int M, int K, int B, const V4Plan& plan) {
+  const dim3 grid((M + R - 1) / R, (B + NB - 1) / NB);
+  return L("v4 launch", dk::gemv_v4_waves<R, U, NB>, grid, dim3(R * plan.S * 64),
+           v4_lds_bytes(plan), p, s, x, y, acc, M, K, B, plan.S);
 }
 
-template <int kReduce>
+// acc: the reference's [B, M] fp32 buffer to receive the sums, or NULL.
 int launch_v4(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
-              float* ws, unsigned long long* tickets, int M, int K, int B, const V4Plan& plan) {
-  const unsigned long long gen = kReduce == dk::kV4Tickets ? next_gen() : 0ull;
-#define DK_V4(U, NB) launch_v4_t<U, NB, kReduce>(L, p, s, x, y, ws, tickets, gen, M, K, B, plan.S)
-#define DK_V4_NB(U) (plan.NB == 1 ? DK_V4(U, 1) : plan.NB == 2 ? DK_V4(U, 2) : DK_V4(U, 4))
-  return plan.U == 1 ? DK_V4_NB(1) : plan.U == 2 ? DK_V4_NB(2) : DK_V4_NB(4);
+              float* acc, int M, int K, int B, const V4Plan& plan) {
+#define DK_V4(R, U, NB) launch_v4_t<R, U, NB>(L, p, s, x, y, acc, M, K, B, plan)
+#define DK_V4_U(R, NB) (plan.U == 1 ? DK_V4(R, 1, NB) : plan.U == 2 ? DK_V4(R, 2, NB) : DK_V4(R, 4, NB))
+#define DK_V4_NB(R) (plan.NB == 1 ? DK_V4_U(R, 1) : plan.NB == 2 ? DK_V4_U(R, 2) : DK_V4_U(R, 4))
+  return plan.R == 1 ? DK_V4_NB(1) : plan.R == 2 ? DK_V4_NB(2) : plan.R == 4 ? DK_V4_NB(4)
+                                                                       : DK_V4_NB(8);
 #undef DK_V4_NB
+#undef DK_V4_U
 #undef DK_V4
 }
 
@@ -661,13 +662,8 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
     case DK_V3:
       return L("v3 launch", dk::gemv_v23<true>, rows4, block4, v3_lds_bytes(K), p4, scales, x4, y,
                M, K, B);
-    case DK_V4: {
-      const V4Plan plan = v4_plan(K, B, cfg->split_k);
-      auto* tickets = static_cast<unsigned long long*>(workspace);
-      auto* partials = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                v4_ticket_bytes(M, B, plan));
-      return launch_v4<dk::kV4Tickets>(L, p4, scales, x4, y, partials, tickets, M, K, B, plan);
-    }
+    case DK_V4:
+      return launch_v4(L, p4, scales, x4, y, nullptr, M, K, B, v4_plan(M, K, B, cfg->split_k));
     case DK_V5:
       return launch_v5(L, p4, scales, x4, y, M, K, B);
     default:
@@ -675,9 +671,10 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
   }
 }
 
-// The reference's workspace contract: v4 accumulates its slices into the
-// caller-zeroed fp32 [B, M] buffer `acc` and converts it to y in a second
-// kernel; every other variant runs as dk_w4a16_gemv without a workspace.
+// The reference's workspace contract: v4 leaves the fp32 sums in the
+// caller's [B, M] buffer `acc` (the reference accumulated them there and
+// converted them to y); every other variant runs as dk_w4a16_gemv without a
+// workspace.
 int gemv_ref_workspace_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
                             uint16_t* y, int M, int K, int B, const dk_gemv_config* cfg,
                             float* acc, const Launch& L) {
@@ -691,22 +688,17 @@ int gemv_ref_workspace_impl(const uint32_t* packed, const uint16_t* scales, cons
   if (!acc)
     return fail(DK_ERR_INVALID_ARGUMENT, "v4 needs the caller-zeroed fp32 [B, M] workspace");
   if (!aligned(acc, 4)) return fail(DK_ERR_INVALID_ARGUMENT, "workspace must be 4-byte aligned");
-  const V4Plan plan = v4_plan(K, B, cfg->split_k);
-  rc = launch_v4<dk::kV4Accumulate>(L, reinterpret_cast<const uint4*>(packed), scales,
-                                    reinterpret_cast<const uint4*>(x), y, acc, nullptr, M, K, B,
-                                    plan);
-  if (rc != DK_OK) return rc;
-  const long long n = (long long)B * M;
-  return L("v4 convert launch", dk::v4_to_fp16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-           acc, y, n);
+  return launch_v4(L, reinterpret_cast<const uint4*>(packed), scales,
+                   reinterpret_cast<const uint4*>(x), y, acc, M, K, B,
+                   v4_plan(M, K, B, cfg->split_k));
 }
 
 }  // namespace
 
 // ---------------------------------------------------------------------------
 // Library-owned scratch for dk_w4a16_gemv_noalloc: the workspace of the
-// split-K paths (v4, and the reuse path's split-K tiles) in a file-scope
-// device array, so that a call allocates nothing. Every GPU the library runs
+// reuse path's split-K tiles in a file-scope device array, so that a call
+// allocates nothing. Every GPU the library runs
 // on holds its own copy (DK_NOALLOC_SCRATCH_BYTES) until the process ends. Its
 // device address is taken once per device with hipGetSymbolAddress, with
 // that device current, and only that address is used from the host (the
@@ -787,8 +779,7 @@ size_t dk_gemv_workspace_bytes(int M, int K, int B, const dk_gemv_config* cfg) {
   if (dk_gemv_validate(M, K, B, cfg) != DK_OK) return 0;
   if (M <= 0 || K <= 0 || B <= 0) return 0;
   if (cfg->reuse_weights) return reuse_split(M, K, B) ? split_workspace_bytes(M, B) : 0;
-  if (cfg->version != DK_V4) return 0;
-  return v4_workspace_bytes(M, K, B, cfg->split_k);
+  return 0;
 }
 
 int dk_w4a16_gemv(const uint32_t* packed, const uint16_t* scales, const uint16_t* x, uint16_t* y,
@@ -805,15 +796,11 @@ int dk_w4a16_gemv_noalloc(const uint32_t* packed, const uint16_t* scales, const 
   if (M <= 0 || K <= 0 || B <= 0) return DK_OK;
   const size_t need = dk_gemv_workspace_bytes(M, K, B, cfg);
   if (need == 0) return gemv_impl(packed, scales, x, y, M, K, B, cfg, nullptr, 0, Launch{stream});
-  if (need > kNoallocScratchBytes) {
-    // The reuse path's split-K tiles are optional: the single-pass tiles run.
-    if (cfg->reuse_weights)
-      return gemv_impl(packed, scales, x, y, M, K, B, cfg, nullptr, 0, Launch{stream});
+  if (need > kNoallocScratchBytes)
     return fail(DK_ERR_UNSUPPORTED,
                 "split-K needs %zu bytes of workspace; dk_w4a16_gemv_noalloc holds %zu (call "
-                "dk_w4a16_gemv with a workspace)",
+                "dk_w4a16_gemv, with or without a workspace)",
                 need, kNoallocScratchBytes);
-  }
   rc = check_io(packed, scales, x, y);
   if (rc != DK_OK) return rc;
   void* ws = nullptr;

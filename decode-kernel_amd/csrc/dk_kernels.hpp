@@ -476,41 +476,15 @@ __global__ __launch_bounds__(W * kWave) void gemv_v5_lds(const uint4* __restrict
 }
 
 // ---------------------------------------------------------------------------
-// v4: split-K on the stage loop of v5 (stamp 4). grid = (row blocks of W R
-// rows, batch tiles of NB rows, S slices). Workgroup (x, y, z) streams its
-// rows over group slice z, groups [z ceil(G/S), +ceil(G/S)), with the same
-// LDS-shared activation stages, buffer loads through wave-uniform
-// descriptors (scoped to the slice, so chunks past it read zero) and decode
-// as v5; each slice reads only its share of the activations.
-// Reference: csrc/gemv_w4a16.cu:264-313, 415-419, 474-481 (a caller-zeroed
-// fp32 [B, M] buffer, fp32 atomicAdd of each slice's row sums, then a
-// separate fp32 -> fp16 kernel).
-//
-// Reductions (kReduce):
-//  * kV4Tickets: one launch, bit-reproducible. Each wave stores its fp32 row
-//    sums to partials[z][b][row] with agent-scope stores (past the
-//    non-coherent per-XCD L2s) and waits for them; thread 0 then takes the
-//    ticket of its (row block, batch tile). The last of the S workgroups to
-//    arrive adds the S partials in slice order z = 0..S-1 and writes fp16 y.
-//    A ticket is 64 bits, (generation << 6) | arrivals: the first arrival of
-//    a call replaces whatever the ticket held, so the workspace needs no
-//    clearing; the last resets it to (generation, 0), so graph replays of
-//    one captured call (same generation) start clean. Generations are 58
-//    bits and never repeat in a process, so only a ticket holding this
-//    call's exact generation before the call (2^-58 for arbitrary memory)
-//    would be miscounted. A fence-based version of the earlier v4 was ~35x
-//    slower: an agent-scope fence writes back and invalidates a whole L2.
-//  * kV4Accumulate: the reference's contract, kept for callers of its C++
-//    API: fp32 agent-scope atomic adds of each slice's row sums into the
-//    caller-zeroed fp32 [B, M] buffer `ws`; a second kernel (v4_to_fp16)
-//    converts it to y. The order of the adds, and so the last bit of the
-//    fp32 sums, is not fixed (as in the reference).
-// Any other kReduce stores the partials and stops, without y (the benchmark
-// tools time it to price the reduction).
+// Completion tickets of a split-K reduction across workgroups (the reuse
+// path's split-K tiles): 64 bits, (generation << 6) | arrivals. The first
+// arrival of a call replaces whatever the ticket held, so a workspace needs
+// no clearing; the last resets it to (generation, 0), so graph replays of
+// one captured call (same generation) start clean. Generations are 58 bits
+// and never repeat in a process, so only a ticket holding this call's exact
+// generation before the call (2^-58 for arbitrary memory) would be
+// miscounted.
 // ---------------------------------------------------------------------------
-constexpr int kV4Tickets = 0;
-constexpr int kV4Accumulate = 1;
-
 // Takes the ticket of a split reduction for generation `gen` (low 6 bits
 // zero); true for the last of `S` arrivals. One thread per workgroup.
 __device__ __forceinline__ bool take_ticket(unsigned long long* ticket, unsigned long long gen, int S) {
@@ -531,88 +505,137 @@ __device__ __forceinline__ void release_ticket(unsigned long long* ticket, unsig
   __hip_atomic_store(ticket, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int R, int U, int W, int NB, bool kPrefetch, int kReduce>
-__global__ __launch_bounds__(W * kWave) void gemv_v4_lds(const uint4* __restrict__ packed,
-                                                         const uint16_t* __restrict__ scales,
-                                                         const uint4* __restrict__ x4,
-                                                         uint16_t* __restrict__ y,
-                                                         float* __restrict__ ws,
-                                                         unsigned long long* __restrict__ tickets,
-                                                         unsigned long long gen, int M, int K,
-                                                         int B) {
+// ---------------------------------------------------------------------------
+// v4, split over the waves of a workgroup (stamp 4). A workgroup owns R rows
+// and splits K into S slices of ceil(G / S) groups; wave w takes row w % R
+// and slice w / R, so the S slices of a row run side by side on S waves
+// instead of one after another. Each stage holds U 16-byte chunks per lane
+// of every slice; the workgroup loads the activations of all S slices once
+// per stage, pairs them and shares them through LDS (slot ((s NB + b) U + u)
+// 4 + j) 64 + l); weights and scales are raw buffer loads through
+// descriptors scoped to the wave's slice, so chunks past it read zero. After
+// the last stage each wave's row sums go to LDS and wave (row, slice 0) adds
+// the S slices in slice order (deterministic) and writes y, and the fp32
+// sums to `acc` when one is given (the reference's workspace contract).
+// No workspace, no second launch: the slices meet inside one CU.
+// S is a launch parameter (the workgroup is R S waves); LDS is dynamic,
+// S NB U 4 KiB of activations, which the S NB R slice sums reuse at the end.
+// ---------------------------------------------------------------------------
+template <int R, int U, int NB>
+__global__ __launch_bounds__(1024) void gemv_v4_waves(const uint4* __restrict__ packed,
+                                                      const uint16_t* __restrict__ scales,
+                                                      const uint4* __restrict__ x4,
+                                                      uint16_t* __restrict__ y,
+                                                      float* __restrict__ acc_out, int M, int K,
+                                                      int B, int S) {
   write_stamp(4);
-  __shared__ LdsActs<U, NB> xs;
-  __shared__ int last;
+  extern __shared__ uint4 v4_lds[];
+  constexpr int kSlicePieces = NB * U * 4 * kWave;  // activation pieces of one slice per stage
+  constexpr int kPer = (4 * NB * U + R - 1) / R;     // pieces per lane: S kSlicePieces / (R S 64)
+  const int W = R * S;
+  const int kPieces = S * kSlicePieces;
+  uint4* xs = v4_lds;
+  // [S][NB][R] slice sums, over the activation stage once every wave has
+  // passed the last stage's closing barrier.
+  float* red = reinterpret_cast<float*>(v4_lds);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nblk = (M + W * R - 1) / (W * R);
-  const int wg = xcd_contiguous_block(blockIdx.x, nblk);
-  const int row0 = (wg * W + wave) * R;
-  const bool active = row0 < M;  // wave-uniform
+  const int r = wave % R;
+  const int sl = wave / R;
+  const int wg = xcd_contiguous_block(blockIdx.x, (M + R - 1) / R);
+  const int row = wg * R + r;
+  const bool active = row < M;
   const int b0 = blockIdx.y * NB;
-  const int S = gridDim.z;
-  const int z = blockIdx.z;
-  const int nck = K >> 5;
   const int G = K >> 7;
+  const int nck = K >> 5;
   const int gps = (G + S - 1) / S;
-  const int gbeg = min(z * gps, G);
-  const int Gs = min(gbeg + gps, G) - gbeg;  // groups of this slice (0 if none)
-  const int rows = active ? min(R, M - row0) : 0;
-  const int rbase = active ? row0 : 0;
-  // The slice of row r is chunks [4 gbeg, 4 (gbeg + Gs)) at r * nck chunks
-  // from the descriptor base; the range ends after the last row's slice.
-  const auto rw = buffer_rsrc(packed + (size_t)rbase * nck + (size_t)gbeg * 4,
-                              rows > 0 ? (uint32_t)((rows - 1) * (K / 2) + Gs * 64) : 0u);
-  const auto rs = buffer_rsrc(scales + (size_t)rbase * G + gbeg,
-                              rows > 0 ? (uint32_t)(((rows - 1) * G + Gs) * 2) : 0u);
-  const auto rx = buffer_rsrc(x4 + (size_t)gbeg * 16, (uint32_t)((size_t)B * K * 2 - (size_t)gbeg * 256));
+  const int gbeg = min(sl * gps, G);
+  const int ns = 4 * (min(gbeg + gps, G) - gbeg);  // chunks of this wave's slice
+  const int smax = 4 * gps;                         // chunks of the longest slice
+  const auto rw = buffer_rsrc(packed + (size_t)(active ? row : 0) * nck + (size_t)gbeg * 4,
+                              active ? (uint32_t)(ns * 16) : 0u);
+  const auto rs = buffer_rsrc(scales + (size_t)(active ? row : 0) * G + gbeg,
+                              active ? (uint32_t)(ns / 2) : 0u);
+  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
 
-  float acc[NB][R];
-  lds_stream<R, U, W, NB, kPrefetch, LayoutLogical, R>(xs, acc, rw, rs, rw, rs, rx, 4 * Gs, nck, G,
-                                                        K, b0, B, tid, lane);
+  float acc[NB];
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+  for (int b = 0; b < NB; ++b) acc[b] = 0.f;
+  for (int c0 = 0; c0 < smax; c0 += U * kWave) {
+    uint4 xv[kPer];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float t = wave_sum(acc[b][r]);
-      if (active && lane == 63 && row0 + r < M && b0 + b < B) {
-        const size_t o = (size_t)(b0 + b) * M + row0 + r;
-        if constexpr (kReduce == kV4Accumulate)
-          __hip_atomic_fetch_add(&ws[o], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else
-          __hip_atomic_store(&ws[(size_t)z * B * M + o], t, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = 0; i < kPer; ++i) {
+      const int p = tid + i * W * kWave;
+      const int sp = p / kSlicePieces;  // slice of this piece
+      const int q = p % kSlicePieces;
+      const int b = q / (U * 4 * kWave);
+      const int pr = q % (U * 4 * kWave);
+      const int cs = c0 + (pr >> 2);  // chunk within slice sp
+      const int gb = min(sp * gps, G);
+      const int nsp = 4 * (min(gb + gps, G) - gb);
+      const bool ok = p < kPieces && cs < nsp && b0 + b < B;
+      xv[i] = buffer_load16<0>(rx, ok ? (b0 + b) * K * 2 + (4 * gb + cs) * 64 + (pr & 3) * 16
+                                      : kOutOfRange);
+    }
+    uint4 w[U];
+    uint32_t sc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * kWave + lane;
+      const bool ok = c < ns;
+      sc[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (c >> 2) * 2 : kOutOfRange, 0, 0);
+      w[u] = buffer_load16<kLoadNonTemporal>(rw, ok ? c * 16 : kOutOfRange);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int p = tid + i * W * kWave;
+      if (p < kPieces) {
+        const int sp = p / kSlicePieces;
+        const int q = p % kSlicePieces;
+        const int b = q / (U * 4 * kWave);
+        const int pr = q % (U * 4 * kWave);
+        const int cr = pr >> 2;  // chunk within the stage: 64 u + l
+        h2_t pp[4];
+        pair_x(xv[i], pp);
+        xs[(((sp * NB + b) * U + cr / kWave) * 4 + (pr & 3)) * kWave + cr % kWave] =
+            make_uint4(__builtin_bit_cast(uint32_t, pp[0]), __builtin_bit_cast(uint32_t, pp[1]),
+                       __builtin_bit_cast(uint32_t, pp[2]), __builtin_bit_cast(uint32_t, pp[3]));
       }
     }
-  if constexpr (kReduce == kV4Tickets) {
-    // Every wave's partial stores are complete before the ticket is taken.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    unsigned long long* ticket = &tickets[(size_t)blockIdx.y * nblk + wg];
-    if (tid == 0) last = take_ticket(ticket, gen, S);
-    __syncthreads();
-    if (!last) return;
-    constexpr int kOut = W * R * NB;
-    for (int t = tid; t < kOut; t += W * kWave) {
-      const int row = wg * W * R + t % (W * R);
-      const int b = b0 + t / (W * R);
-      if (row >= M || b >= B) continue;
-      float sum = 0.f;
-      for (int s = 0; s < S; ++s)
-        sum += __hip_atomic_load(&ws[((size_t)s * B + b) * M + row], __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-      y[(size_t)b * M + row] = f2h(sum);
+    lds_barrier();
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t words[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+      const float scale = h2f((uint16_t)sc[u]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        float part = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint4 pv = xs[(((sl * NB + b) * U + u) * 4 + j) * kWave + lane];
+          const h2_t xp[4] = {as_h2(pv.x), as_h2(pv.y), as_h2(pv.z), as_h2(pv.w)};
+          part = dot_word(words[j], xp, part);
+        }
+        acc[b] = __builtin_fmaf(part, scale, acc[b]);
+      }
     }
-    if (tid == 0) release_ticket(ticket, gen);
+    lds_barrier();  // every wave's reads are done before the next stage's stores
   }
-}
-
-// The second kernel of the accumulate form: y = fp16(acc), n = B * M values.
-__global__ __launch_bounds__(256) void v4_to_fp16(const float* __restrict__ acc,
-                                                  uint16_t* __restrict__ y, long long n) {
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = f2h(acc[i]);
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float t = wave_sum(acc[b]);
+    if (lane == 63) red[(sl * NB + b) * R + r] = t;
+  }
+  __syncthreads();
+  if (sl == 0 && active && lane < NB && b0 + lane < B) {
+    float sum = 0.f;
+    for (int s2 = 0; s2 < S; ++s2) sum += red[(s2 * NB + lane) * R + r];
+    const size_t o = (size_t)(b0 + lane) * M + row;
+    y[o] = f2h(sum);
+    if (acc_out) acc_out[o] = sum;
+  }
 }
 
 // ---------------------------------------------------------------------------

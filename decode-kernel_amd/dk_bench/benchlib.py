@@ -18,6 +18,7 @@ _SIGNATURES = {
     "dkb_onestage": (_I, [_I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P]),
     "dkb_v4": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, ctypes.c_ulonglong, _I, _I,
                     _P]),
+    "dkb_v4_waves": (_I, [_I, _I, _I, _P, _P, _P, _P, _I, _I, _P]),
     "dkb_timestamp": (_I, [_P, _I, _P]),
     "dkb_wall_clock_khz": (_I, []),
 }
@@ -103,3 +104,15 @@ def timestamp(buf, slot: int) -> None:
 
 def wall_clock_khz() -> int:
     return int(load().dkb_wall_clock_khz())
+
+
+def v4_waves(r: int, u: int, s: int, packed, scales, x, y) -> int:
+    """The split-over-waves v4 (B = 1): R rows per workgroup, U chunks per
+    lane per stage, S slices. Returns 3 (nothing launched) for a shape not
+    instantiated or over the LDS bound."""
+    m, k = packed.shape[0], packed.shape[1] * 8
+    rc = load().dkb_v4_waves(r, u, s, packed.data_ptr(), scales.data_ptr(), x.data_ptr(),
+                             y.data_ptr(), m, k, stream_handle())
+    if rc not in (0, 3):
+        raise RuntimeError(f"v4 waves R{r} U{u} S{s}: status {rc}")
+    return rc

@@ -9,10 +9,10 @@
          LDS or in registers, weights issued first or last, one or two waves
          per row, 4 to 16 waves per workgroup) and streaming-kernel shapes,
          against the product;
-  v4     split-K shapes (rows, chunks per lane per stage, waves, prefetch;
-         2, 4 or 8 slices) at short and tall rows, each also without its
-         reduction (partials stored, no ticket, no y), against the product's
-         v5 and v4.
+  v4     split-K over the waves of one workgroup (rows per workgroup,
+         chunks per lane per stage, 1-16 slices; the product's v4) and over
+         workgroups with a ticket reduction (a sample, also without the
+         reduction), at short and tall rows, against the product's v5 and v4.
 
 Every variant that computes y is checked against the product's v5 output
 (bit-exact where the summation order is the same, else within 1e-3 plus one
@@ -33,6 +33,7 @@ V4_SHAPES = [(1, 1, 4, True), (1, 2, 4, True), (1, 4, 4, True), (1, 1, 8, True),
              (1, 4, 8, True), (1, 2, 4, False), (1, 4, 4, False), (2, 1, 4, True), (2, 2, 4, True),
              (1, 1, 16, True), (1, 2, 16, True)]
 V4_PROBLEMS = {"c0": (4096, 4096), "c2": (4096, 11008), "m1024_k28672": (1024, 28672),
+               "m512_k28672": (512, 28672), "m2048_k16384": (2048, 16384),
                "m2048_k11008": (2048, 11008), "m1024_k8192": (1024, 8192), "c4b": (8192, 28672)}
 V5_C0_SHAPES = [(1, 2, 8, True), (1, 2, 8, False), (1, 2, 16, True), (1, 2, 16, False),
                 (1, 2, 4, True), (1, 1, 16, True), (1, 1, 8, True)]
@@ -104,6 +105,10 @@ def sweep_c0(flush, steps: int) -> dict:
 
 
 def sweep_v4(flush, steps: int) -> dict:
+    """Split-K two ways, against the product's v5 and v4: over the waves of
+    one workgroup (gemv_v4_waves: R rows per workgroup, U chunks per lane per
+    stage, S slices; the product's v4) and over workgroups with a ticket
+    reduction (gemv_v4_lds, a sample of shapes, also without the reduction)."""
     from decode_kernel import _cuda
 
     from . import benchlib
@@ -118,21 +123,36 @@ def sweep_v4(flush, steps: int) -> dict:
         n = len(pk)
         y_prod = _cuda.w4a16_gemv(pk[0], sc[0], x)
         y = torch.empty_like(y_prod)
-        rows = {"product_v5": _time(lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x), steps, flush),
-                "product_v4_s4": _time(lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x, version=4,
-                                                                  split_k=4), steps, flush)}
-        print(f"v4 {name}: product v5 {rows['product_v5']:.3f}, product v4 s4 "
-              f"{rows['product_v4_s4']:.3f} us", flush=True)
-        for splits in (2, 4, 8):
+        rows = {"product_v5": _time(lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x), steps, flush)}
+        for sk in (2, 4, 8, 16):
+            rows[f"product_v4_s{sk}"] = _time(
+                lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x, version=4, split_k=sk), steps,
+                flush)
+        print(f"v4 {name}: product v5 {rows['product_v5']:.3f}; product v4 " + ", ".join(
+            f"s{sk} {rows[f'product_v4_s{sk}']:.3f}" for sk in (2, 4, 8, 16)), flush=True)
+        for r in (1, 2, 4, 8):
+            for u in (1, 2, 4):
+                for s_ in (1, 2, 4, 8, 16):
+                    if benchlib.v4_waves(r, u, s_, pk[0], sc[0], x, y) == 3:
+                        continue
+                    torch.cuda.synchronize()
+                    if not _close(y, y_prod):
+                        raise RuntimeError(f"v4 waves R{r} U{u} S{s_} differs from v5 at {name}")
+                    key = f"waves_R{r}_U{u}_S{s_}"
+                    rows[key] = _time(lambda i: benchlib.v4_waves(r, u, s_, pk[i % n], sc[i % n], x,
+                                                                  y), steps, flush)
+                    print(f"v4 {name} {key}: {rows[key]:.3f} us", flush=True)
+        for splits in (2, 4):
             ws = torch.empty(splits * m, dtype=torch.float32, device="cuda")
             tickets = torch.zeros(m, dtype=torch.int64, device="cuda")
-            for shape in V4_SHAPES:
+            for shape in ((1, 1, 16, True), (1, 4, 8, True), (2, 1, 4, True)):
                 gen += 64
                 benchlib.v4(shape, 0, splits, pk[0], sc[0], x, y, ws, tickets, gen)
                 torch.cuda.synchronize()
                 if not _close(y, y_prod):
                     raise RuntimeError(f"v4 {shape} S{splits} differs from v5 at {name}")
-                key = "S{}_R{}_U{}_W{}_{}".format(splits, *shape[:3], "pf" if shape[3] else "nopf")
+                key = "groups_S{}_R{}_U{}_W{}_{}".format(splits, *shape[:3],
+                                                         "pf" if shape[3] else "nopf")
                 g = gen + 64
                 gen += 128
                 full = _time(lambda i: benchlib.v4(shape, 0, splits, pk[i % n], sc[i % n], x, y, ws,

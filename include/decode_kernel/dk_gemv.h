@@ -38,7 +38,9 @@ typedef enum dk_kernel_version {
   DK_V1 = 1, /* one wave64 per row, 4-byte coalesced word loads */
   DK_V2 = 2, /* one wave64 per row, 16-byte coalesced loads */
   DK_V3 = 3, /* v2 with the row's group scales staged in LDS */
-  DK_V4 = 4, /* split-K over grid.z, deterministic single-launch reduction */
+  DK_V4 = 4, /* split-K: the slices of a row on the waves of one workgroup,
+                added in slice order through LDS (one launch, deterministic,
+                no workspace) */
   DK_V5 = 5  /* tuned: raw buffer loads (activations first), shape-selected
                 rows per wave and activation rows per tile */
 } dk_kernel_version;
@@ -50,7 +52,8 @@ typedef enum dk_kernel_version {
  * (GemvLaunchConfig); defaults are the same (v5, split_k 4, no reuse, 1). */
 typedef struct dk_gemv_config {
   int version;       /* dk_kernel_version, 0..5 */
-  int split_k;       /* v4 only, 1..32; ignored otherwise */
+  int split_k;       /* v4 only, 1..32 (slices: min(split_k, K/128, 16));
+                        ignored otherwise */
   int reuse_weights; /* nonzero: weight-reuse path, ignores version: MFMA tiles
                         from 5 batch rows (3 at M * K >= 2^27 or with
                         4096 < K < 8192 and M >= 3072, 4 at M >= 3072; 9 at
@@ -70,24 +73,19 @@ typedef enum dk_status {
 /* Fill *cfg with the reference defaults (v5, split_k 4, reuse 0, 1 wave/row). */
 void dk_gemv_config_default(dk_gemv_config* cfg);
 
-/* Bytes of device workspace dk_w4a16_gemv takes for this call; 0 for every
- * variant but two:
- *  - split-K v4 (required, 8-byte aligned): one 8-byte completion ticket per
- *    (4-row workgroup, batch tile), padded to 256 bytes, then fp32 partials
- *    [split_k', B, M], split_k' = min(split_k, K/128);
- *  - the weight-reuse path when its MFMA tiles split K over workgroups
- *    (K > 8192 with M <= 2048, or with M <= 4096 and 32 or more batch
- *    rows; K = 8192 with M of 2049-4096 and 32 or more batch rows;
- *    optional, 8-byte aligned): one 8-byte ticket per set of 32 rows and 16
- *    batch rows, padded to 256 bytes, then fp32 partials [4, B, M]. Without
- *    it (NULL or too small) the path runs its single-pass tiles, same
- *    results within rounding.
- * Neither needs clearing: each ticket carries the call's generation. Calls
- * that overlap in time need separate workspaces. No counterpart in the
- * reference, whose v4 took an fp32 [B, M] buffer zeroed per call
- * (include/decode_kernel/gemv_w4a16.h:33, csrc/bindings.cpp:65-68: see
- * dk_w4a16_gemv_ref_workspace) and whose reuse path took none. Returns 0
- * for invalid arguments. */
+/* Bytes of device workspace dk_w4a16_gemv takes for this call: 0 for every
+ * variant (v4 included) but the weight-reuse path when its MFMA tiles split
+ * K over workgroups (K > 8192 with M <= 2048, or with M <= 4096 and 32 or
+ * more batch rows; K = 8192 with M of 2049-4096 and 32 or more batch rows).
+ * There it is optional and 8-byte aligned: one 8-byte ticket per set of 32
+ * rows and 16 batch rows, padded to 256 bytes, then fp32 partials [4, B, M];
+ * without it (NULL or too small) the path runs its single-pass tiles, same
+ * results within rounding. It needs no clearing: each ticket carries the
+ * call's generation. Calls that overlap in time need separate workspaces.
+ * No counterpart in the reference, whose v4 took an fp32 [B, M] buffer
+ * zeroed per call (include/decode_kernel/gemv_w4a16.h:33,
+ * csrc/bindings.cpp:65-68: see dk_w4a16_gemv_ref_workspace) and whose reuse
+ * path took none. Returns 0 for invalid arguments. */
 size_t dk_gemv_workspace_bytes(int M, int K, int B, const dk_gemv_config* cfg);
 
 /* Host-side argument check of dk_w4a16_gemv without launching anything
@@ -99,12 +97,13 @@ int dk_gemv_validate(int M, int K, int B, const dk_gemv_config* cfg);
  * `stream`. Replaces decode_kernel::w4a16_gemv
  * (include/decode_kernel/gemv_w4a16.h:34-36, csrc/gemv_w4a16.cu:568-591).
  * M, K or B <= 0 is a no-op returning DK_OK (csrc/gemv_w4a16.cu:571).
- * `workspace` must hold dk_gemv_workspace_bytes() bytes for v4 (may be NULL
- * if 0); on the reuse path a workspace of that size is optional; both are
- * 8-byte aligned.
+ * `workspace` (8-byte aligned) is optional: only the reuse path's split-K
+ * tiles use one, of dk_gemv_workspace_bytes() bytes; NULL with 0 is always
+ * valid.
  * Differences from the reference: launch errors are returned (the reference
  * printed and continued, csrc/gemv_w4a16.cu:9-16), and split-K is one
- * launch with a deterministic reduction instead of memset+atomics+convert. */
+ * launch with a deterministic reduction inside the workgroup instead of
+ * memset + atomics + convert. */
 int dk_w4a16_gemv(const uint32_t* packed, const uint16_t* scales,
                   const uint16_t* x, uint16_t* y, int M, int K, int B,
                   const dk_gemv_config* cfg, void* workspace,
@@ -115,27 +114,25 @@ int dk_w4a16_gemv(const uint32_t* packed, const uint16_t* scales,
 
 /* dk_w4a16_gemv for callers that cannot allocate: code under HIP graph
  * capture, tight serving loops, hosts that forbid hipMalloc. No counterpart
- * in the reference. The split-K paths (v4, and the reuse path's split-K
- * tiles) take their workspace from a library-owned device array of
- * DK_NOALLOC_SCRATCH_BYTES (8 MiB) on each GPU, held until the process
- * ends; nothing is allocated, cleared or freed by a call. A v4 call
- * whose dk_gemv_workspace_bytes() exceeds it returns DK_ERR_UNSUPPORTED
- * before any launch; the reuse path then runs its single-pass tiles. Every
- * call on one GPU shares that GPU's array: calls that overlap in time on one
- * GPU (different streams, or host threads) race and must not be issued.
- * Arguments, checks and results otherwise as dk_w4a16_gemv. */
+ * in the reference. The reuse path's split-K tiles take their workspace from
+ * a library-owned device array of DK_NOALLOC_SCRATCH_BYTES (8 MiB) on each
+ * GPU, held until the process ends; nothing is allocated, cleared or freed
+ * by a call. A call whose dk_gemv_workspace_bytes() exceeds the array
+ * returns DK_ERR_UNSUPPORTED before any launch. Every call on one GPU shares
+ * that GPU's array: calls that overlap in time on one GPU (different
+ * streams, or host threads) race and must not be issued. Arguments, checks
+ * and results otherwise as dk_w4a16_gemv. */
 int dk_w4a16_gemv_noalloc(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
                           uint16_t* y, int M, int K, int B, const dk_gemv_config* cfg,
                           hipStream_t stream);
 
 /* dk_w4a16_gemv with the reference's workspace contract, for callers written
  * against decode_kernel::w4a16_gemv (include/decode_kernel/gemv_w4a16.h:29-36,
- * csrc/gemv_w4a16.cu:474-481): for v4, `workspace` is a caller-zeroed fp32
- * [B, M] buffer; the K slices add their fp32 row sums into it with atomics
- * and a second kernel converts it to y (it holds the fp32 result after the
- * call, as in the reference; the order of the adds, and so the last bit of
- * the fp32 sums, is not fixed, also as in the reference). Every other
- * variant ignores `workspace` and runs as dk_w4a16_gemv with none. */
+ * csrc/gemv_w4a16.cu:474-481): for v4, `workspace` is the caller's fp32
+ * [B, M] buffer (required, as in the reference), which holds the fp32 sums
+ * of y after the call, as the reference's did; nothing past it is touched.
+ * Every other variant ignores `workspace` and runs as dk_w4a16_gemv with
+ * none. */
 int dk_w4a16_gemv_ref_workspace(const uint32_t* packed, const uint16_t* scales,
                                 const uint16_t* x, uint16_t* y, int M, int K, int B,
                                 const dk_gemv_config* cfg, float* workspace,
@@ -217,7 +214,7 @@ const char* dk_last_error(void);
 
 /* ABI version of this header, (major << 16) | minor. */
 int dk_abi_version(void);
-#define DK_ABI_VERSION ((1 << 16) | 2)
+#define DK_ABI_VERSION ((1 << 16) | 3)
 
 #ifdef __cplusplus
 } /* extern "C" */

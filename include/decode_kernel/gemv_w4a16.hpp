@@ -6,14 +6,12 @@
 //   * failures throw std::runtime_error carrying dk_last_error() (the
 //     reference printed launch errors and continued, csrc/gemv_w4a16.cu:9-16);
 //   * w4a16_gemv(..., float* workspace, stream) keeps the reference's
-//     workspace contract (gemv_w4a16.h:33): for v4 a caller-zeroed fp32
-//     [B, M] buffer that the K slices accumulate into with atomics before a
-//     second kernel converts it to y; other versions ignore it
+//     workspace contract (gemv_w4a16.h:33): v4 requires the fp32 [B, M]
+//     buffer and leaves the fp32 sums of y in it; other versions ignore it
 //     (dk_w4a16_gemv_ref_workspace);
-//   * w4a16_gemv(..., void* workspace, size_t workspace_bytes, stream) is the
-//     single-launch, bit-reproducible form: workspace_bytes() bytes for v4
-//     (8-byte tickets, then fp32 partials [split_k, B, M]; no clearing), and
-//     optionally for the reuse path's split-K tiles (dk_w4a16_gemv).
+//   * w4a16_gemv(..., void* workspace, size_t workspace_bytes, stream) is
+//     dk_w4a16_gemv: no version needs a workspace; workspace_bytes() bytes
+//     optionally enable the reuse path's split-K tiles.
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -65,8 +63,8 @@ inline void check(int rc, const char* what) {
 
 }  // namespace detail
 
-// Device workspace bytes the sized w4a16_gemv overload takes for this call:
-// required for v4, optional for the reuse path's split-K tiles, 0 otherwise.
+// Device workspace bytes the sized w4a16_gemv overload can take for this
+// call: optional, for the reuse path's split-K tiles; 0 otherwise.
 inline size_t workspace_bytes(int M, int K, int B, const GemvLaunchConfig& cfg) {
   const dk_gemv_config c = detail::to_c(cfg);
   return dk_gemv_workspace_bytes(M, K, B, &c);
@@ -76,8 +74,8 @@ inline size_t workspace_bytes(int M, int K, int B, const GemvLaunchConfig& cfg) 
 // scales:  [M, K/128] fp16, symmetric group scale
 // x:       [B, K] fp16
 // y:       [B, M] fp16
-// workspace: fp32 [B, M], zeroed by the caller, required for v4 (as in the
-//            reference); ignored by every other version
+// workspace: fp32 [B, M], required for v4 (as in the reference), which leaves
+//            the fp32 sums of y in it; ignored by every other version
 inline void w4a16_gemv(const uint32_t* packed, const __half* scales, const __half* x, __half* y,
                        int M, int K, int B, const GemvLaunchConfig& cfg, float* workspace,
                        hipStream_t stream) {
@@ -89,9 +87,9 @@ inline void w4a16_gemv(const uint32_t* packed, const __half* scales, const __hal
                 "w4a16_gemv");
 }
 
-// Single-launch form: `workspace` holds `bytes` >= workspace_bytes() bytes,
-// 8-byte aligned, no clearing needed (null if workspace_bytes() is 0; for the
-// reuse path null runs the single-pass tiles).
+// The C ABI's form: `workspace` holds `bytes` >= workspace_bytes() bytes,
+// 8-byte aligned, no clearing needed, or is null (for the reuse path null
+// runs the single-pass tiles).
 inline void w4a16_gemv(const uint32_t* packed, const __half* scales, const __half* x, __half* y,
                        int M, int K, int B, const GemvLaunchConfig& cfg, void* workspace,
                        size_t bytes, hipStream_t stream) {

@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.dk_abi_version() == (1 << 16) | 2
+    assert lib.dk_abi_version() == (1 << 16) | 3
 
 
 def test_default_config_matches_reference(lib):
@@ -99,28 +99,19 @@ def test_null_and_misaligned_pointers_rejected(lib):
     assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "16-byte aligned" in lib.dk_last_error().decode()
 
 
-def test_split_k_workspace_contract(lib):
-    cfg = _abi.default_config(lib, version=4, split_k=4)
-    # One 8-byte ticket per (4-row workgroup, batch tile of 1, 2 or 4 rows),
-    # padded to 256 bytes, then [split_k, B, M] fp32 partials (split capped
-    # at the group count).
-    ws = lambda m, k, b, c=cfg: lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(c))
-    assert ws(4096, 4096, 2) == 1024 * 8 + 4 * 2 * 4096 * 4   # tiles of 2 batch rows
-    assert ws(4096, 4096, 1) == 1024 * 8 + 4 * 1 * 4096 * 4
-    assert ws(4096, 4096, 5) == 2048 * 8 + 4 * 5 * 4096 * 4   # tiles of 4: two of them
-    assert ws(64, 256, 1) == 256 + 2 * 1 * 64 * 4             # 16 tickets -> 256 bytes
-    assert ws(65, 256, 1) == 256 + 2 * 1 * 65 * 4
-    assert ws(4096, 4096, 1, _abi.default_config(lib, version=4, split_k=32)) == (
-        1024 * 8 + 32 * 4096 * 4)
-    for v in (0, 1, 2, 3, 5):
-        c = _abi.default_config(lib, version=v)
-        assert lib.dk_gemv_workspace_bytes(4096, 4096, 1, ctypes.byref(c)) == 0
-    fake = 0x10000
-    rc = lib.dk_w4a16_gemv(fake, fake, fake, fake, 64, 256, 1, ctypes.byref(cfg), None, 0, None)
-    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "workspace" in lib.dk_last_error().decode()
-    rc = lib.dk_w4a16_gemv(fake, fake, fake, fake, 64, 256, 1, ctypes.byref(cfg), fake + 4,
-                           ws(64, 256, 1), None)
-    assert rc == _abi.DK_ERR_INVALID_ARGUMENT and "8-byte aligned" in lib.dk_last_error().decode()
+def test_split_k_needs_no_workspace(lib):
+    # v4 splits K over the waves of one workgroup and adds the slices through
+    # LDS: no workspace for any version (only the reuse path's optional
+    # split-K tiles take one), so a NULL workspace is accepted.
+    for v in range(6):
+        for sk in (1, 4, 32):
+            c = _abi.default_config(lib, version=v, split_k=sk)
+            for m, k, b in ((4096, 4096, 1), (4096, 11008, 5), (64, 256, 2)):
+                assert lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(c)) == 0, (v, sk, m, k, b)
+    d = _abi.describe(lib, 4096, 11008, 1, version=4, split_k=4)
+    assert d["kernel"].startswith("void dk::gemv_v4_waves<4, 1, 1>") and d["block"] == [1024, 1, 1]
+    d = _abi.describe(lib, 1024, 28672, 1, version=4, split_k=32)  # 16 slices at most
+    assert d["kernel"].startswith("void dk::gemv_v4_waves<1, 1, 1>") and d["block"] == [1024, 1, 1]
 
 
 def test_reference_workspace_contract_checks(lib):
@@ -151,7 +142,7 @@ def test_describe_names_the_dispatched_kernel(lib):
     assert d["kernel"].startswith("void dk::gemv_v5_lds<1, 2, 8, 1, true, dk::LayoutLogical, 5")
     assert d["grid"] == [512, 1, 1] and d["block"] == [512, 1, 1] and d["launches"] == 1
     d = _abi.describe(lib, 4096, 11008, 1, version=4, split_k=4)
-    assert d["kernel"].startswith("void dk::gemv_v4_lds<") and d["grid"][2] == 4
+    assert d["kernel"].startswith("void dk::gemv_v4_waves<") and d["grid"] == [1024, 1, 1]
     assert _abi.describe(lib, 4096, 4096, 16, reuse_weights=1)["kernel"].startswith(
         "void dk::gemv_reuse<")
     assert _abi.describe(lib, 4096, 4096, 2, reuse_weights=1)["kernel"].startswith(
@@ -266,7 +257,7 @@ def test_torch_extension_surface():
     for pat in (r"version: [\w.]*Int = 5", r"split_k: [\w.]*Int = 4",
                 r"reuse_weights: bool = False", r"warps_per_row: [\w.]*Int = 1"):
         assert re.search(pat, doc), (pat, doc)
-    assert _cuda.ABI_VERSION == (1 << 16) | 2
+    assert _cuda.ABI_VERSION == (1 << 16) | 3
 
 
 def test_extension_rejects_cpu_tensors():
@@ -310,11 +301,11 @@ int main() {
   } catch (const std::runtime_error& e) {
     std::printf("v4 threw: %s\n", e.what());
   }
-  // The sized overload checks the size it is given.
+  // The sized overload checks its arguments on the host too.
   try {
-    w4a16_gemv(reinterpret_cast<const uint32_t*>(0x10000), reinterpret_cast<const __half*>(0x10000),
+    w4a16_gemv(reinterpret_cast<const uint32_t*>(0x10004), reinterpret_cast<const __half*>(0x10000),
                reinterpret_cast<const __half*>(0x10000), reinterpret_cast<__half*>(0x10000), 64,
-               256, 1, v4, reinterpret_cast<void*>(0x10000), size_t{64}, nullptr);
+               256, 1, v4, nullptr, size_t{0}, nullptr);
     return 5;
   } catch (const std::runtime_error& e) {
     std::printf("sized threw: %s\n", e.what());
@@ -346,8 +337,8 @@ def test_cpp_namespace_wrapper_compiles_and_validates(tmp_path):
     assert out.returncode == 0, (out.returncode, out.stdout, out.stderr)
     assert "threw: w4a16_gemv: K must be divisible by group size 128" in out.stdout
     assert "v4 threw: w4a16_gemv: v4 needs the caller-zeroed fp32 [B, M] workspace" in out.stdout
-    assert "sized threw: w4a16_gemv: split-K needs a 768-byte workspace (got 64)" in out.stdout
-    assert f"ws {1024 * 8 + 4 * 2 * 4096 * 4} 0" in out.stdout
+    assert "sized threw: w4a16_gemv: packed and x must be 16-byte aligned" in out.stdout
+    assert "ws 0 0" in out.stdout
 
 
 def test_bench_library_loads_and_stays_out_of_the_product(lib):

@@ -1,10 +1,10 @@
 """dk_w4a16_gemv_noalloc, the entry point that allocates nothing, through the
 C ABI against dk_w4a16_gemv with a caller workspace (same kernels, so the
 same bits), on two calls in a row per path, the second with a smaller input:
-split-K v4, the reuse path's split-K tiles, and a path without scratch. Also:
-a v4 call whose workspace exceeds the scratch is refused before any launch,
-the reuse path then runs its single-pass tiles, and a captured call replays
-with eager calls of other shapes between the replays.
+the reuse path's split-K tiles (the scratch's user) and paths without
+scratch. Also: a call whose workspace would exceed the scratch is refused
+before any launch, and a captured call replays with eager calls of another
+shape between the replays.
 """
 
 from __future__ import annotations
@@ -57,11 +57,12 @@ def _tight(y, y_ref, label):
     assert (err <= 0.5 * oracle.fp16_ulp(y_ref) + 1e-3).all(), label
 
 
-# (config, first call (M, K, B), second, smaller call)
+# (config, first call (M, K, B), second, smaller call); the reuse path's
+# split-K tiles take the scratch, the others none.
 PATHS = [
-    (dict(version=4, split_k=4), (4096, 11008, 1), (1000, 1024, 3)),
-    (dict(version=4, split_k=32), (2048, 8192, 5), (77, 384, 2)),
     (dict(version=5, reuse_weights=1), (2048, 16384, 16), (1024, 12416, 17)),
+    (dict(version=5, reuse_weights=1), (4096, 11008, 64), (2048, 9216, 33)),
+    (dict(version=4, split_k=4), (4096, 11008, 1), (1000, 1024, 3)),
     (dict(version=5), (4096, 4096, 1), (333, 640, 2)),
 ]
 
@@ -83,12 +84,14 @@ def test_noalloc_matches_the_workspace_entry(cfg, first, second):
         _tight(y, y_ref, f"noalloc {cfg} M={m} K={k} B={b}")
 
 
-def test_noalloc_refuses_v4_beyond_the_scratch():
+def test_noalloc_refuses_a_workspace_beyond_the_scratch():
+    # The reuse path's split-K tiles at B = 128 need more than the scratch:
+    # refused on the host, before anything is launched (small stand-in
+    # buffers), and y is untouched.
     abi, lib = _lib()
-    m, k, b = 28672, 8192, 16
-    c = abi.default_config(lib, version=4, split_k=32)
+    m, k, b = 4096, 11008, 128
+    c = abi.default_config(lib, reuse_weights=1)
     assert lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(c)) > abi.DK_NOALLOC_SCRATCH_BYTES
-    # Checked on the host before anything is launched: small stand-in buffers.
     pd = torch.zeros(16, dtype=torch.int32, device="cuda")
     y = torch.full((4,), 7.0, dtype=torch.float16, device="cuda")
     rc = lib.dk_w4a16_gemv_noalloc(pd.data_ptr(), pd.data_ptr(), pd.data_ptr(), y.data_ptr(), m,
@@ -99,25 +102,13 @@ def test_noalloc_refuses_v4_beyond_the_scratch():
     assert bool((y == 7.0).all())
 
 
-def test_noalloc_reuse_beyond_the_scratch_runs_single_pass_tiles():
-    abi, lib = _lib()
-    m, k, b = 4096, 11008, 128
-    c = abi.default_config(lib, reuse_weights=1)
-    assert lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(c)) > abi.DK_NOALLOC_SCRATCH_BYTES
-    pd, sd, xd, _ = _case(m, k, b, seed=3)
-    y = torch.empty(b, m, dtype=torch.float16, device="cuda")
-    abi.check(lib, _call_noalloc(lib, c, pd, sd, xd, y, m, k, b))
-    y_single = _call_ws(abi, lib, c, pd, sd, xd, m, k, b, with_ws=False)
-    torch.cuda.synchronize()
-    assert torch.equal(y, y_single)
-
-
 def test_noalloc_graph_replays_with_eager_calls_between():
     abi, lib = _lib()
-    c = abi.default_config(lib, version=4, split_k=8)
-    m, k, b = 2048, 8192, 3
+    c = abi.default_config(lib, reuse_weights=1)
+    m, k, b = 2048, 16384, 16
     pd, sd, xd, y_ref = _case(m, k, b, seed=4)
-    p2, s2, x2, y2_ref = _case(1000, 2048, 1, seed=5)
+    assert lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(c)) > 0  # uses the scratch
+    p2, s2, x2, y2_ref = _case(1024, 12416, 17, seed=5)
     y_eager = torch.empty(b, m, dtype=torch.float16, device="cuda")
     abi.check(lib, _call_noalloc(lib, c, pd, sd, xd, y_eager, m, k, b))
     torch.cuda.synchronize()
@@ -127,8 +118,8 @@ def test_noalloc_graph_replays_with_eager_calls_between():
         abi.check(lib, _call_noalloc(lib, c, pd, sd, xd, y_graph, m, k, b))
     for rep in range(4):
         graph.replay()
-        y_between = torch.empty(1, 1000, dtype=torch.float16, device="cuda")
-        abi.check(lib, _call_noalloc(lib, c, p2, s2, x2, y_between, 1000, 2048, 1))
+        y_between = torch.empty(17, 1024, dtype=torch.float16, device="cuda")
+        abi.check(lib, _call_noalloc(lib, c, p2, s2, x2, y_between, 1024, 12416, 17))
         torch.cuda.synchronize()
         assert torch.equal(y_graph, y_eager), f"replay {rep}"
         _tight(y_between, y2_ref, f"eager call between replays {rep}")
