@@ -68,10 +68,10 @@ __global__ __launch_bounds__(1024) void read_probe(const uint4* __restrict__ src
 //  LoadsOnly: folds only the weight words and scales (no LDS reads).
 // ---------------------------------------------------------------------------
 struct MathNoDecode {
-  template <int R, int U, int W, int NB, typename Layout>
-  static __device__ __forceinline__ void compute(const LdsStage<R, U, W, NB>& st,
-                                                 const uint4 (&xs)[LdsActsT<U, NB>::kSlots],
-                                                 float (&acc)[NB][R], int lane) {
+  template <int R, int U, int W, int NB, typename Layout, int kS>
+  static __device__ __forceinline__ void compute(const LdsStage<R, U, W, NB, kS>& st,
+                                                 const uint4 (&xs)[LdsActsT<kS * U, NB>::kSlots],
+                                                 float (&acc)[NB][R], int lane, int sl) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -81,7 +81,7 @@ struct MathNoDecode {
         for (int r = 0; r < R; ++r) h[r] = 0u;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint4 pv = xs[((b * U + u) * 4 + j) * kWave + lane];
+          const uint4 pv = xs[((b * kS * U + sl * U + u) * 4 + j) * kWave + lane];
           const uint32_t xw = pv.x ^ pv.y ^ pv.z ^ pv.w;
 #pragma unroll
           for (int r = 0; r < R; ++r) {
@@ -97,10 +97,10 @@ struct MathNoDecode {
 };
 
 struct MathLoadsOnly {
-  template <int R, int U, int W, int NB, typename Layout>
-  static __device__ __forceinline__ void compute(const LdsStage<R, U, W, NB>& st,
-                                                 const uint4 (&)[LdsActsT<U, NB>::kSlots],
-                                                 float (&acc)[NB][R], int) {
+  template <int R, int U, int W, int NB, typename Layout, int kS>
+  static __device__ __forceinline__ void compute(const LdsStage<R, U, W, NB, kS>& st,
+                                                 const uint4 (&)[LdsActsT<kS * U, NB>::kSlots],
+                                                 float (&acc)[NB][R], int, int) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -520,25 +520,40 @@ DKB_API int dkb_wall_clock_khz(void) {
   return khz;
 }
 
-// The split-over-waves v4 (gemv_v4_waves, B = 1) with R rows per workgroup,
-// U chunks per lane per stage and S slices. Returns 3 if not instantiated or
-// if the activation stage would exceed 64 KiB of LDS.
-DKB_API int dkb_v4_waves(int R, int U, int S, const void* packed, const void* scales, const void* x,
-                         void* y, int M, int K, hipStream_t stream) {
-  if (S < 1 || R * S > 16 || S * U > 16) return 3;
+// The product's split-K kernel (gemv_v4_split, B = 1) at shape R rows per
+// wave, U chunks per lane per stage, W waves, S slices per row, prefetch on
+// or off; math 0 is the product's, 1 no decode and 2 loads only (as for
+// dkb_v5; those at the shapes the v5 dispatch takes it for). Returns 3
+// (nothing launched) for a shape not instantiated here.
+DKB_API int dkb_v4s(int math, int R, int U, int W, int S, int pf, const void* packed,
+                    const void* scales, const void* x, void* y, int M, int K, hipStream_t stream) {
   const auto* p = static_cast<const uint4*>(packed);
   const auto* s = static_cast<const uint16_t*>(scales);
   const auto* xx = static_cast<const uint4*>(x);
   auto* yy = static_cast<uint16_t*>(y);
-  const size_t lds = (size_t)S * U * 4 * 64 * 16;
-#define DKB_V4W(r, u)                                                                          \
-  if (R == r && U == u) {                                                                      \
-    hipLaunchKernelGGL((dk::gemv_v4_waves<r, u, 1>), dim3((M + r - 1) / r), dim3(r * S * 64), lds, \
-                       stream, p, s, xx, yy, static_cast<float*>(nullptr), M, K, 1, S);        \
-    return launch_error("v4 waves");                                                           \
+#define DKB_V4S_M(mi, Mt, r, u, w, k, f)                                                        \
+  if (math == mi && R == r && U == u && W == w && S == k && pf == (int)f) {                     \
+    const int rows = w / k * r;                                                                 \
+    hipLaunchKernelGGL((dk::gemv_v4_split<r, u, w, k, 1, f, Mt>), dim3((M + rows - 1) / rows),   \
+                       dim3(w * 64), 0, stream, p, s, xx, yy, static_cast<float*>(nullptr), M, K, \
+                       1, 4);                                                                   \
+    return launch_error("v4 split");                                                            \
   }
-  DKB_V4W(1, 1) DKB_V4W(1, 2) DKB_V4W(1, 4) DKB_V4W(2, 1) DKB_V4W(2, 2) DKB_V4W(2, 4)
-  DKB_V4W(4, 1) DKB_V4W(4, 2) DKB_V4W(4, 4) DKB_V4W(8, 1) DKB_V4W(8, 2)
-#undef DKB_V4W
+#define DKB_V4S_PF(r, u, w, k, f) DKB_V4S_M(0, dk::StageMath, r, u, w, k, f)
+#define DKB_V4S(r, u, w, k) DKB_V4S_PF(r, u, w, k, true) DKB_V4S_PF(r, u, w, k, false)
+#define DKB_V4S_W(r, u, k) DKB_V4S(r, u, 4, k) DKB_V4S(r, u, 8, k) DKB_V4S(r, u, 16, k)
+  DKB_V4S_W(1, 1, 2) DKB_V4S_W(1, 2, 2) DKB_V4S_W(1, 4, 2) DKB_V4S_W(2, 1, 2) DKB_V4S_W(2, 2, 2)
+  DKB_V4S_W(1, 1, 4) DKB_V4S_W(1, 2, 4) DKB_V4S_W(2, 1, 4) DKB_V4S_W(2, 2, 4)
+  DKB_V4S(1, 1, 8, 8) DKB_V4S(1, 1, 16, 8) DKB_V4S(2, 1, 8, 8) DKB_V4S(2, 1, 16, 8)
+#define DKB_V4S_ABL(r, u, w, k, f) \
+  DKB_V4S_M(1, dkb::MathNoDecode, r, u, w, k, f) DKB_V4S_M(2, dkb::MathLoadsOnly, r, u, w, k, f)
+  DKB_V4S_ABL(1, 1, 4, 2, true) DKB_V4S_ABL(1, 2, 8, 4, true) DKB_V4S_ABL(1, 2, 8, 4, false)
+  DKB_V4S_ABL(2, 2, 8, 4, false) DKB_V4S_ABL(1, 1, 16, 2, true) DKB_V4S_ABL(2, 1, 16, 2, true)
+  DKB_V4S_ABL(2, 2, 8, 2, false)
+#undef DKB_V4S_ABL
+#undef DKB_V4S_W
+#undef DKB_V4S
+#undef DKB_V4S_PF
+#undef DKB_V4S_M
   return 3;
 }

@@ -21,6 +21,7 @@
 #include <cstdlib>
 #include <mutex>
 #include <string>
+#include <type_traits>
 
 #include "dk_host.hpp"
 #include "dk_kernels.hpp"
@@ -117,6 +118,123 @@ struct Launch {
   }
 };
 
+// The split-K kernel (gemv_v4_split): S waves per row, W waves per
+// workgroup, R rows per wave, U chunks per lane per stage and slice, NB
+// batch rows per stage, prefetch on or off. The activation stage (two
+// buffers of NB S U 4 KiB) stays within 64 KiB.
+struct SplitShape {
+  int R, U, W, S, NB;
+  bool pf;
+};
+
+template <int R, int U, int W, int S, int NB, bool PF>
+int launch_split_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
+                   float* acc, int M, int K, int B, int stamp) {
+  constexpr int kRows = W / S * R;
+  const dim3 grid((M + kRows - 1) / kRows, (B + NB - 1) / NB);
+  return L("split-K launch", dk::gemv_v4_split<R, U, W, S, NB, PF>, grid, dim3(W * 64), 0, p, s, x,
+           y, acc, M, K, B, stamp);
+}
+
+// acc: the reference's [B, M] fp32 buffer to receive the sums, or NULL.
+int launch_split(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
+                 float* acc, int M, int K, int B, const SplitShape& sh, int stamp) {
+#define DK_SPLIT(r, u, w, k, nb, f)                                                          \
+  if (sh.R == r && sh.U == u && sh.W == w && sh.S == k && sh.NB == nb && sh.pf == f)        \
+    return launch_split_t<r, u, w, k, nb, f>(L, p, s, x, y, acc, M, K, B, stamp);
+  DK_SPLIT(1, 2, 8, 1, 1, true) DK_SPLIT(1, 2, 8, 4, 1, false) DK_SPLIT(1, 4, 4, 2, 1, false)
+  DK_SPLIT(1, 1, 4, 2, 1, true) DK_SPLIT(1, 2, 8, 4, 1, true) DK_SPLIT(1, 4, 4, 2, 1, true)
+  DK_SPLIT(2, 2, 8, 4, 1, false) DK_SPLIT(1, 4, 8, 2, 1, false) DK_SPLIT(1, 2, 4, 2, 1, true)
+  DK_SPLIT(1, 1, 8, 2, 1, true) DK_SPLIT(1, 1, 16, 2, 1, true) DK_SPLIT(2, 1, 4, 2, 1, false)
+  DK_SPLIT(2, 2, 4, 2, 1, true) DK_SPLIT(2, 2, 8, 2, 1, false) DK_SPLIT(2, 1, 16, 2, 1, true)
+  DK_SPLIT(2, 1, 16, 2, 1, false)
+  DK_SPLIT(1, 2, 8, 1, 2, true) DK_SPLIT(1, 2, 8, 1, 4, true) DK_SPLIT(1, 1, 8, 2, 2, true)
+  DK_SPLIT(1, 1, 8, 2, 4, true)
+#undef DK_SPLIT
+  return dk::set_error(DK_ERR_UNSUPPORTED, "split-K: no kernel for R%d U%d W%d S%d NB%d", sh.R,
+                       sh.U, sh.W, sh.S, sh.NB);
+}
+
+// v4 launch plan. split_k caps the waves per row (S, a power of two, also at
+// most K / 128 and 8). Set from a sweep of 62 shapes (R 1-2, U 1-4, W 4-16,
+// S 2-8, prefetch on and off) at 24 shapes of M and K (dk_bench.levers v4 and
+// split), us per launch, the choice against the best:
+//   M = K = 4096:         R1 U1 W8  S2 pf    3.62 (3.60)
+//   M = 4096, K = 11008:  R1 U1 W16 S2 pf    6.10 (6.10)
+//   M = 4096, K = 28672:  R2 U1 W16 S2 pf   11.53 (11.53)
+//   M = 8192, K = 28672:  R2 U1 W16 S2      20.45 (20.45)
+//   M = 8192, K = 8192:   R2 U2 W8  S2       7.84 (7.84)
+//   M = 2048, K = 11008:  R1 U1 W16 S2 pf    4.64 (4.64)
+//   M = 1024, K = 28672:  R2 U2 W8  S4       5.85 (5.85)
+//   M = 512,  K = 28672:  R1 U2 W8  S4       4.60 (4.60)
+//   M = 512,  K = 4096:   R1 U1 W4  S2 pf    2.16 (2.16)
+// Eight waves per row (S = 8) were never the best (M = 512, K = 28672: 4.63
+// against 4.58 for S = 4; M = K = 4096: 8.43 against 3.60 for S = 2); S = 1
+// is the GEMV. Batches: S <= 2 with NB = 2 or 4 batch rows per stage.
+SplitShape v4_plan(int M, int K, int B, int split_k) {
+  const int G = K / DK_GROUP_SIZE;
+  const int cap = std::max(1, std::min({split_k, G, 8}));
+  const int s_max = cap >= 4 ? 4 : cap >= 2 ? 2 : 1;
+  if (B > 1) {
+    const int nb = B == 2 ? 2 : 4;
+    return s_max == 1 ? SplitShape{1, 2, 8, 1, nb, true} : SplitShape{1, 1, 8, 2, nb, true};
+  }
+  if (s_max == 1) return {1, 2, 8, 1, 1, true};
+  const bool tall = K >= 16384;
+  const bool four = s_max >= 4;
+  if (M <= 512) {
+    if (tall) return four ? SplitShape{1, 2, 8, 4, 1, false} : SplitShape{1, 4, 4, 2, 1, false};
+    if (K <= 4096) return {1, 1, 4, 2, 1, true};
+    return four ? SplitShape{1, 2, 8, 4, 1, true} : SplitShape{1, 4, 4, 2, 1, true};
+  }
+  if (M <= 1024) {
+    if (tall) return four ? SplitShape{2, 2, 8, 4, 1, false} : SplitShape{1, 4, 8, 2, 1, false};
+    return K <= 8192 ? SplitShape{1, 2, 4, 2, 1, true} : SplitShape{1, 4, 4, 2, 1, true};
+  }
+  if (M <= 2048) return K <= 4096 ? SplitShape{1, 1, 8, 2, 1, true} : SplitShape{1, 1, 16, 2, 1, true};
+  if (K <= 4096) return M <= 8192 ? SplitShape{1, 1, 8, 2, 1, true} : SplitShape{2, 1, 4, 2, 1, false};
+  if (K <= 8192) return M <= 4096 ? SplitShape{2, 2, 4, 2, 1, true} : SplitShape{2, 2, 8, 2, 1, false};
+  if (K <= 12288) return {1, 1, 16, 2, 1, true};
+  return M <= 4096 ? SplitShape{2, 1, 16, 2, 1, true} : SplitShape{2, 1, 16, 2, 1, false};
+}
+
+int launch_v4(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
+              float* acc, int M, int K, int B, int split_k) {
+  return launch_split(L, p, s, x, y, acc, M, K, B, v4_plan(M, K, B, split_k), 4);
+}
+
+// One batch row at the shapes where the split-K kernel beats gemv_v5_lds by
+// 5% or more in the same sweep (us, split-K against gemv_v5_lds):
+//   M = 4096, K = 11008:  6.12 (6.44)     M = 4096, K = 14336:  7.64 (8.19)
+//   M = 4096, K = 28672: 11.53 (12.67)    M = 5120, K = 8192:   5.94 (6.28)
+//   M = 8192, K = 8192:   7.84 (8.13)     M = 1024, K = 28672:  5.85 (6.74)
+//   M = 512,  K = 28672:  4.60 (6.21)     M = 512,  K = 8320:   2.91 (3.05)
+//   M = 512,  K = 4096:   2.16 (2.28)
+// Elsewhere it is level or slower (M = K = 4096: 3.62 against 3.54; M =
+// 11008, K = 5120: 9.34 against 8.48; M = 1024, K = 11008: 3.63 against
+// 3.31).
+bool v5_takes_split(int M, int K, SplitShape* sh) {
+  if (M <= 512 && K > 2048) {
+    *sh = K >= 16384 ? SplitShape{1, 2, 8, 4, 1, false}
+          : K <= 4096 ? SplitShape{1, 1, 4, 2, 1, true}
+                      : SplitShape{1, 2, 8, 4, 1, true};
+    return true;
+  }
+  if (M <= 1024 && K >= 16384) {
+    *sh = {2, 2, 8, 4, 1, false};
+    return true;
+  }
+  if (M > 3072 && M <= 4096 && K > 8192) {
+    *sh = K <= 12288 ? SplitShape{1, 1, 16, 2, 1, true} : SplitShape{2, 1, 16, 2, 1, true};
+    return true;
+  }
+  if (M > 4096 && M <= 8192 && K == 8192) {
+    *sh = {2, 2, 8, 2, 1, false};
+    return true;
+  }
+  return false;
+}
+
 // One activation row: the streaming kernel with activations shared through
 // LDS (R rows per wave, U 16-byte chunks per lane per stage, W waves per
 // workgroup, next stage prefetched or not). Timed on MI355X as the bench
@@ -177,6 +295,9 @@ int launch_lds_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4
 template <typename Layout, int kStamp>
 int launch_lds(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                int M, int K) {
+  SplitShape sh;
+  if (std::is_same<Layout, dk::LayoutLogical>::value && v5_takes_split(M, K, &sh))
+    return launch_split(L, p, s, x, y, nullptr, M, K, 1, sh, kStamp);
   if (K <= 2048) return launch_lds_t<1, 1, 16, true, Layout, kStamp>(L, p, s, x, y, M, K);
   if (M <= 3072) {
     if (K <= 4096) return launch_lds_t<1, 2, 4, true, Layout, kStamp>(L, p, s, x, y, M, K);
@@ -545,57 +666,6 @@ int effective_split(int K, int split_k) {
   return std::max(1, std::min(split_k, G));
 }
 
-// v4 (split-K) launch plan: S = min(split_k, K / 128, 16) slices of
-// ceil(G / S) groups, each on its own wave; R rows per workgroup (a power of
-// two, R S <= 16 waves); U 16-byte chunks per lane per stage; NB batch rows
-// per stage. The activation stage in LDS is S NB U 4 KiB, kept within
-// 64 KiB. From a sweep of R (1-8), U (1-4) and S (1-16) at eight shapes
-// (M from 512 to 8192, K from 4096 to 28672; dk_bench.levers v4), the best
-// shapes for a given S take R = 2 at M <= 512 and 4 above (8 at S <= 2 from
-// M = 4096), and stages that cover a slice once (M <= 1024) or twice.
-struct V4Plan {
-  int S, R, U, NB;
-};
-
-V4Plan v4_plan(int M, int K, int B, int split_k) {
-  V4Plan p;
-  const int G = K / DK_GROUP_SIZE;
-  p.S = std::max(1, std::min({split_k, G, 16}));
-  int r = M <= 512 ? 2 : (p.S <= 2 && M >= 4096) ? 8 : 4;
-  while (r > 1 && r * p.S > 16) r /= 2;
-  p.R = r;
-  p.NB = B == 1 ? 1 : B == 2 ? 2 : 4;
-  while (p.NB > 1 && p.S * p.NB > 16) p.NB /= 2;
-  const int slice_chunks = 4 * ((G + p.S - 1) / p.S);
-  const int per_stage = M <= 1024 ? slice_chunks : (slice_chunks + 1) / 2;
-  p.U = per_stage <= 64 ? 1 : per_stage <= 128 ? 2 : 4;
-  while (p.U > 1 && p.S * p.NB * p.U > 16) p.U /= 2;
-  return p;
-}
-
-size_t v4_lds_bytes(const V4Plan& p) { return (size_t)p.S * p.NB * p.U * 4 * 64 * 16; }
-
-template <int R, int U, int NB>
-int launch_v4_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
-                float* acc, int M, int K, int B, const V4Plan& plan) {
-  const dim3 grid((M + R - 1) / R, (B + NB - 1) / NB);
-  return L("v4 launch", dk::gemv_v4_waves<R, U, NB>, grid, dim3(R * plan.S * 64),
-           v4_lds_bytes(plan), p, s, x, y, acc, M, K, B, plan.S);
-}
-
-// acc: the reference's [B, M] fp32 buffer to receive the sums, or NULL.
-int launch_v4(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
-              float* acc, int M, int K, int B, const V4Plan& plan) {
-#define DK_V4(R, U, NB) launch_v4_t<R, U, NB>(L, p, s, x, y, acc, M, K, B, plan)
-#define DK_V4_U(R, NB) (plan.U == 1 ? DK_V4(R, 1, NB) : plan.U == 2 ? DK_V4(R, 2, NB) : DK_V4(R, 4, NB))
-#define DK_V4_NB(R) (plan.NB == 1 ? DK_V4_U(R, 1) : plan.NB == 2 ? DK_V4_U(R, 2) : DK_V4_U(R, 4))
-  return plan.R == 1 ? DK_V4_NB(1) : plan.R == 2 ? DK_V4_NB(2) : plan.R == 4 ? DK_V4_NB(4)
-                                                                       : DK_V4_NB(8);
-#undef DK_V4_NB
-#undef DK_V4_U
-#undef DK_V4
-}
-
 int check_io(const uint32_t* packed, const uint16_t* scales, const uint16_t* x, const uint16_t* y) {
   if (!packed || !scales || !x || !y)
     return fail(DK_ERR_INVALID_ARGUMENT, "packed, scales, x and y must not be NULL");
@@ -663,7 +733,7 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
       return L("v3 launch", dk::gemv_v23<true>, rows4, block4, v3_lds_bytes(K), p4, scales, x4, y,
                M, K, B);
     case DK_V4:
-      return launch_v4(L, p4, scales, x4, y, nullptr, M, K, B, v4_plan(M, K, B, cfg->split_k));
+      return launch_v4(L, p4, scales, x4, y, nullptr, M, K, B, cfg->split_k);
     case DK_V5:
       return launch_v5(L, p4, scales, x4, y, M, K, B);
     default:
@@ -689,8 +759,7 @@ int gemv_ref_workspace_impl(const uint32_t* packed, const uint16_t* scales, cons
     return fail(DK_ERR_INVALID_ARGUMENT, "v4 needs the caller-zeroed fp32 [B, M] workspace");
   if (!aligned(acc, 4)) return fail(DK_ERR_INVALID_ARGUMENT, "workspace must be 4-byte aligned");
   return launch_v4(L, reinterpret_cast<const uint4*>(packed), scales,
-                   reinterpret_cast<const uint4*>(x), y, acc, M, K, B,
-                   v4_plan(M, K, B, cfg->split_k));
+                   reinterpret_cast<const uint4*>(x), y, acc, M, K, B, cfg->split_k);
 }
 
 }  // namespace

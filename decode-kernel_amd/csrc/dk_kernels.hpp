@@ -223,9 +223,12 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, int off
 // overlap gains.
 // grid.y covers the batch in tiles of NB rows.
 // ---------------------------------------------------------------------------
-template <int R, int U, int W, int NB>
+// kS > 1 (split-K, v4): the stage holds kS U chunks per lane of activations
+// and the kS waves of a row take U of them each (wave slice sl: stage chunks
+// 64 (sl U + u) + l), so a row's chunks are dealt to its waves stage by stage.
+template <int R, int U, int W, int NB, int kS = 1>
 struct LdsStage {
-  static constexpr int kPiecesPerRow = U * 4 * kWave;  // 16-byte pieces of one batch row
+  static constexpr int kPiecesPerRow = kS * U * 4 * kWave;  // 16-byte pieces of one batch row
   static constexpr int kPieces = NB * kPiecesPerRow;
   static constexpr int kPer = (kPieces + W * kWave - 1) / (W * kWave);
   uint4 xv[kPer];
@@ -247,14 +250,15 @@ using LdsActs = typename LdsActsT<U, NB>::type;
 // Rows r < kSplit come from (rw, rs), rows r >= kSplit from (rw2, rs2) as
 // their row r - kSplit (the fused gate/up kernel streams two matrices
 // against one activation stage; the GEMV has kSplit = R).
-template <int R, int U, int W, int NB, int kSplit>
-__device__ __forceinline__ void lds_stage_load(LdsStage<R, U, W, NB>& st, __amdgpu_buffer_rsrc_t rw,
-                                               __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rw2,
+template <int R, int U, int W, int NB, int kSplit, int kS = 1>
+__device__ __forceinline__ void lds_stage_load(LdsStage<R, U, W, NB, kS>& st,
+                                               __amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs,
+                                               __amdgpu_buffer_rsrc_t rw2,
                                                __amdgpu_buffer_rsrc_t rs2, __amdgpu_buffer_rsrc_t rx,
                                                int c0, int nck, int wstride, int G, int K, int b0,
-                                               int B, int tid, int lane) {
-  using S = LdsStage<R, U, W, NB>;
-  // Activations of chunks [c0, c0 + 64U) of batch row b0 + b: piece p of
+                                               int B, int tid, int lane, int sl = 0) {
+  using S = LdsStage<R, U, W, NB, kS>;
+  // Activations of chunks [c0, c0 + 64 kS U) of batch row b0 + b: piece p of
   // that row is bytes [16p, 16p + 16) of the range, so consecutive lanes
   // read consecutive 16 bytes.
 #pragma unroll
@@ -268,7 +272,7 @@ __device__ __forceinline__ void lds_stage_load(LdsStage<R, U, W, NB>& st, __amdg
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int c = c0 + u * kWave + lane;
+    const int c = c0 + (sl * U + u) * kWave + lane;
     const bool ok = c < nck;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -289,11 +293,11 @@ __device__ __forceinline__ void lds_stage_load(LdsStage<R, U, W, NB>& st, __amdg
 // the lane that owns the chunk reads them (slot layout above). Lanes past
 // the stage's pieces (workgroups of more than 4U * NB waves) have none; the
 // test is uniform per wave, so those waves skip the store.
-template <int R, int U, int W, int NB, typename Layout>
-__device__ __forceinline__ void lds_stage_publish(const LdsStage<R, U, W, NB>& st,
-                                                  uint4 (&xs)[LdsActsT<U, NB>::kSlots],
+template <int R, int U, int W, int NB, typename Layout, int kS = 1>
+__device__ __forceinline__ void lds_stage_publish(const LdsStage<R, U, W, NB, kS>& st,
+                                                  uint4 (&xs)[LdsActsT<kS * U, NB>::kSlots],
                                                   int tid) {
-  using S = LdsStage<R, U, W, NB>;
+  using S = LdsStage<R, U, W, NB, kS>;
 #pragma unroll
   for (int i = 0; i < S::kPer; ++i) {
     const int piece = tid + i * W * kWave;
@@ -302,17 +306,17 @@ __device__ __forceinline__ void lds_stage_publish(const LdsStage<R, U, W, NB>& s
       const int cr = (piece % S::kPiecesPerRow) >> 2;  // chunk within the stage: 64 u + l
       h2_t p[4];
       Layout::pair(st.xv[i], p);
-      xs[((b * U + cr / kWave) * 4 + (piece & 3)) * kWave + cr % kWave] =
+      xs[((b * kS * U + cr / kWave) * 4 + (piece & 3)) * kWave + cr % kWave] =
           make_uint4(__builtin_bit_cast(uint32_t, p[0]), __builtin_bit_cast(uint32_t, p[1]),
                      __builtin_bit_cast(uint32_t, p[2]), __builtin_bit_cast(uint32_t, p[3]));
     }
   }
 }
 
-template <int R, int U, int W, int NB, typename Layout>
-__device__ __forceinline__ void lds_stage_compute(const LdsStage<R, U, W, NB>& st,
-                                                  const uint4 (&xs)[LdsActsT<U, NB>::kSlots],
-                                                  float (&acc)[NB][R], int lane) {
+template <int R, int U, int W, int NB, typename Layout, int kS = 1>
+__device__ __forceinline__ void lds_stage_compute(const LdsStage<R, U, W, NB, kS>& st,
+                                                  const uint4 (&xs)[LdsActsT<kS * U, NB>::kSlots],
+                                                  float (&acc)[NB][R], int lane, int sl = 0) {
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     h2_t xp[NB][4][4];
@@ -320,7 +324,7 @@ __device__ __forceinline__ void lds_stage_compute(const LdsStage<R, U, W, NB>& s
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint4 pv = xs[((b * U + u) * 4 + j) * kWave + lane];
+        const uint4 pv = xs[((b * kS * U + sl * U + u) * 4 + j) * kWave + lane];
         xp[b][j][0] = as_h2(pv.x);
         xp[b][j][1] = as_h2(pv.y);
         xp[b][j][2] = as_h2(pv.z);
@@ -363,31 +367,32 @@ __device__ __forceinline__ void lds_barrier() {
 
 // The decode and products of one stage (the default math of the stage loop).
 struct StageMath {
-  template <int R, int U, int W, int NB, typename Layout>
-  static __device__ __forceinline__ void compute(const LdsStage<R, U, W, NB>& st,
-                                                 const uint4 (&xs)[LdsActsT<U, NB>::kSlots],
-                                                 float (&acc)[NB][R], int lane) {
-    lds_stage_compute<R, U, W, NB, Layout>(st, xs, acc, lane);
+  template <int R, int U, int W, int NB, typename Layout, int kS>
+  static __device__ __forceinline__ void compute(const LdsStage<R, U, W, NB, kS>& st,
+                                                 const uint4 (&xs)[LdsActsT<kS * U, NB>::kSlots],
+                                                 float (&acc)[NB][R], int lane, int sl) {
+    lds_stage_compute<R, U, W, NB, Layout, kS>(st, xs, acc, lane, sl);
   }
 };
 
 // The stage loop shared by the GEMV, split-K and the fused gate/up kernel:
 // acc[b][r] is row r's fp32 sum for batch row b0 + b over this lane's chunks
-// of [0, nck) (a whole row, or one K slice of it). Weight row r starts
-// wstride chunks after row r - 1 in its descriptor; scales G entries; batch
-// rows of x K elements.
+// of [0, nck) (a whole row, or one K slice of it), or with kS > 1 over the
+// chunks of slice sl (the U of every kS U per lane that are this wave's).
+// Weight row r starts wstride chunks after row r - 1 in its descriptor;
+// scales G entries; batch rows of x K elements.
 template <int R, int U, int W, int NB, bool kPrefetch, typename Layout, int kSplit,
-          typename Math = StageMath>
-__device__ __forceinline__ void lds_stream(LdsActs<U, NB>& xs, float (&acc)[NB][R],
+          typename Math = StageMath, int kS = 1>
+__device__ __forceinline__ void lds_stream(LdsActs<kS * U, NB>& xs, float (&acc)[NB][R],
                                            __amdgpu_buffer_rsrc_t rw, __amdgpu_buffer_rsrc_t rs,
                                            __amdgpu_buffer_rsrc_t rw2, __amdgpu_buffer_rsrc_t rs2,
                                            __amdgpu_buffer_rsrc_t rx, int nck, int wstride, int G,
-                                           int K, int b0, int B, int tid, int lane) {
+                                           int K, int b0, int B, int tid, int lane, int sl = 0) {
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[b][r] = 0.f;
-  constexpr int kStep = U * kWave;
+  constexpr int kStep = kS * U * kWave;
   if constexpr (kPrefetch) {
     // Two register sets, the loop unrolled by two so that no register copy
     // waits on a load; the prefetch loads are unconditional (zeros past the
@@ -398,40 +403,40 @@ __device__ __forceinline__ void lds_stream(LdsActs<U, NB>& xs, float (&acc)[NB][
     // faster at 14 (M = 8192, K = 28672). Workgroups with more lanes than
     // activation pieces keep the publish test: giving the spare lanes
     // padding slots instead (so every lane loads and stores) cost 11-17%.
-    LdsStage<R, U, W, NB> sa, sb;
-    lds_stage_load<R, U, W, NB, kSplit>(sa, rw, rs, rw2, rs2, rx, 0, nck, wstride, G, K, b0, B, tid,
-                                        lane);
+    LdsStage<R, U, W, NB, kS> sa, sb;
+    lds_stage_load<R, U, W, NB, kSplit, kS>(sa, rw, rs, rw2, rs2, rx, 0, nck, wstride, G, K, b0,
+                                            B, tid, lane, sl);
     for (int c0 = 0;;) {
-      lds_stage_publish<R, U, W, NB, Layout>(sa, xs[0], tid);
+      lds_stage_publish<R, U, W, NB, Layout, kS>(sa, xs[0], tid);
       __syncthreads();
-      lds_stage_load<R, U, W, NB, kSplit>(sb, rw, rs, rw2, rs2, rx, c0 + kStep, nck, wstride, G, K,
-                                          b0, B, tid, lane);
+      lds_stage_load<R, U, W, NB, kSplit, kS>(sb, rw, rs, rw2, rs2, rx, c0 + kStep, nck, wstride,
+                                              G, K, b0, B, tid, lane, sl);
       __builtin_amdgcn_sched_barrier(0);
-      Math::template compute<R, U, W, NB, Layout>(sa, xs[0], acc, lane);
+      Math::template compute<R, U, W, NB, Layout, kS>(sa, xs[0], acc, lane, sl);
       c0 += kStep;
       if (c0 >= nck) break;
-      lds_stage_publish<R, U, W, NB, Layout>(sb, xs[1], tid);
+      lds_stage_publish<R, U, W, NB, Layout, kS>(sb, xs[1], tid);
       __syncthreads();
-      lds_stage_load<R, U, W, NB, kSplit>(sa, rw, rs, rw2, rs2, rx, c0 + kStep, nck, wstride, G, K,
-                                          b0, B, tid, lane);
+      lds_stage_load<R, U, W, NB, kSplit, kS>(sa, rw, rs, rw2, rs2, rx, c0 + kStep, nck, wstride,
+                                              G, K, b0, B, tid, lane, sl);
       __builtin_amdgcn_sched_barrier(0);
-      Math::template compute<R, U, W, NB, Layout>(sb, xs[1], acc, lane);
+      Math::template compute<R, U, W, NB, Layout, kS>(sb, xs[1], acc, lane, sl);
       c0 += kStep;
       if (c0 >= nck) break;
     }
   } else {
-    LdsStage<R, U, W, NB> st;
+    LdsStage<R, U, W, NB, kS> st;
     int buf = 0;
     for (int c0 = 0; c0 < nck; c0 += kStep, buf ^= 1) {
-      lds_stage_load<R, U, W, NB, kSplit>(st, rw, rs, rw2, rs2, rx, c0, nck, wstride, G, K, b0, B,
-                                          tid, lane);
+      lds_stage_load<R, U, W, NB, kSplit, kS>(st, rw, rs, rw2, rs2, rx, c0, nck, wstride, G, K,
+                                              b0, B, tid, lane, sl);
       // Every load of the stage issues before the publish waits on the
       // activation pieces (left alone, the scheduler can put that wait
       // between the loads).
       __builtin_amdgcn_sched_barrier(0);
-      lds_stage_publish<R, U, W, NB, Layout>(st, xs[buf], tid);
+      lds_stage_publish<R, U, W, NB, Layout, kS>(st, xs[buf], tid);
       lds_barrier();
-      Math::template compute<R, U, W, NB, Layout>(st, xs[buf], acc, lane);
+      Math::template compute<R, U, W, NB, Layout, kS>(st, xs[buf], acc, lane, sl);
     }
   }
 }
@@ -506,135 +511,90 @@ __device__ __forceinline__ void release_ticket(unsigned long long* ticket, unsig
 }
 
 // ---------------------------------------------------------------------------
-// v4, split over the waves of a workgroup (stamp 4). A workgroup owns R rows
-// and splits K into S slices of ceil(G / S) groups; wave w takes row w % R
-// and slice w / R, so the S slices of a row run side by side on S waves
-// instead of one after another. Each stage holds U 16-byte chunks per lane
-// of every slice; the workgroup loads the activations of all S slices once
-// per stage, pairs them and shares them through LDS (slot ((s NB + b) U + u)
-// 4 + j) 64 + l); weights and scales are raw buffer loads through
-// descriptors scoped to the wave's slice, so chunks past it read zero. After
-// the last stage each wave's row sums go to LDS and wave (row, slice 0) adds
-// the S slices in slice order (deterministic) and writes y, and the fp32
-// sums to `acc` when one is given (the reference's workspace contract).
-// No workspace, no second launch: the slices meet inside one CU.
-// S is a launch parameter (the workgroup is R S waves); LDS is dynamic,
-// S NB U 4 KiB of activations, which the S NB R slice sums reuse at the end.
+// v4, split-K (stamp 4): the streaming kernel with each row taken by kS
+// waves of its workgroup. The workgroup's W waves are W / kS row waves of R
+// rows times kS slices (wave w: slice w / (W / kS), rows of row wave
+// w % (W / kS)); each stage holds kS U chunks per lane of activations, and
+// the wave of slice sl takes U of them (stage chunks 64 (sl U + u) + l), so
+// the kS waves of a row share its stages' loads and the stage loop,
+// prefetch and single barrier per stage are the GEMV's. After the last stage
+// each wave's row sums go to LDS and the slice-0 wave of each row adds the
+// kS of them in slice order (deterministic; fixed for a launch shape) and
+// writes y, and the fp32 sums to `acc` when one is given (the reference's
+// workspace contract). One launch, no workspace: the slices meet inside one
+// CU. kS = 1 is the GEMV. The stamp is an argument: 4 for v4, 5 where the
+// v5 dispatch takes this kernel (it is faster than gemv_v5_lds at some
+// shapes).
 // ---------------------------------------------------------------------------
-template <int R, int U, int NB>
-__global__ __launch_bounds__(1024) void gemv_v4_waves(const uint4* __restrict__ packed,
-                                                      const uint16_t* __restrict__ scales,
-                                                      const uint4* __restrict__ x4,
-                                                      uint16_t* __restrict__ y,
-                                                      float* __restrict__ acc_out, int M, int K,
-                                                      int B, int S) {
-  write_stamp(4);
-  extern __shared__ uint4 v4_lds[];
-  constexpr int kSlicePieces = NB * U * 4 * kWave;  // activation pieces of one slice per stage
-  constexpr int kPer = (4 * NB * U + R - 1) / R;     // pieces per lane: S kSlicePieces / (R S 64)
-  const int W = R * S;
-  const int kPieces = S * kSlicePieces;
-  uint4* xs = v4_lds;
-  // [S][NB][R] slice sums, over the activation stage once every wave has
-  // passed the last stage's closing barrier.
-  float* red = reinterpret_cast<float*>(v4_lds);
+template <int R, int U, int W, int kS, int NB, bool kPrefetch, typename Math = StageMath>
+__global__ __launch_bounds__(W * kWave) void gemv_v4_split(const uint4* __restrict__ packed,
+                                                           const uint16_t* __restrict__ scales,
+                                                           const uint4* __restrict__ x4,
+                                                           uint16_t* __restrict__ y,
+                                                           float* __restrict__ acc_out, int M,
+                                                           int K, int B, int stamp) {
+  static_assert(W % kS == 0, "a workgroup holds whole rows");
+  constexpr int kRowWaves = W / kS;
+  constexpr int kRows = kRowWaves * R;  // rows per workgroup
+  write_stamp(stamp);
+  __shared__ LdsActs<kS * U, NB> xs;
+  __shared__ float red[kS > 1 ? kS * NB * kRows : 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = wave % R;
-  const int sl = wave / R;
-  const int wg = xcd_contiguous_block(blockIdx.x, (M + R - 1) / R);
-  const int row = wg * R + r;
-  const bool active = row < M;
+  const int sl = wave / kRowWaves;
+  const int rwave = wave % kRowWaves;
+  const int wg = xcd_contiguous_block(blockIdx.x, (M + kRows - 1) / kRows);
+  const int row0 = wg * kRows + rwave * R;
+  const bool active = row0 < M;  // wave-uniform
   const int b0 = blockIdx.y * NB;
-  const int G = K >> 7;
   const int nck = K >> 5;
-  const int gps = (G + S - 1) / S;
-  const int gbeg = min(sl * gps, G);
-  const int ns = 4 * (min(gbeg + gps, G) - gbeg);  // chunks of this wave's slice
-  const int smax = 4 * gps;                         // chunks of the longest slice
-  const auto rw = buffer_rsrc(packed + (size_t)(active ? row : 0) * nck + (size_t)gbeg * 4,
-                              active ? (uint32_t)(ns * 16) : 0u);
-  const auto rs = buffer_rsrc(scales + (size_t)(active ? row : 0) * G + gbeg,
-                              active ? (uint32_t)(ns / 2) : 0u);
+  const int G = K >> 7;
+  const int rows = active ? min(R, M - row0) : 0;
+  const int rbase = active ? row0 : 0;
+  const auto rw = buffer_rsrc(packed + (size_t)rbase * nck, (uint32_t)(rows * (K / 2)));
+  const auto rs = buffer_rsrc(scales + (size_t)rbase * G, (uint32_t)(rows * G * 2));
   const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
 
-  float acc[NB];
+  float acc[NB][R];
+  lds_stream<R, U, W, NB, kPrefetch, LayoutLogical, R, Math, kS>(
+      xs, acc, rw, rs, rw, rs, rx, nck, nck, G, K, b0, B, tid, lane, sl);
+  if constexpr (kS == 1) {
+    if (!active) return;  // after the last barrier
 #pragma unroll
-  for (int b = 0; b < NB; ++b) acc[b] = 0.f;
-  for (int c0 = 0; c0 < smax; c0 += U * kWave) {
-    uint4 xv[kPer];
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int p = tid + i * W * kWave;
-      const int sp = p / kSlicePieces;  // slice of this piece
-      const int q = p % kSlicePieces;
-      const int b = q / (U * 4 * kWave);
-      const int pr = q % (U * 4 * kWave);
-      const int cs = c0 + (pr >> 2);  // chunk within slice sp
-      const int gb = min(sp * gps, G);
-      const int nsp = 4 * (min(gb + gps, G) - gb);
-      const bool ok = p < kPieces && cs < nsp && b0 + b < B;
-      xv[i] = buffer_load16<0>(rx, ok ? (b0 + b) * K * 2 + (4 * gb + cs) * 64 + (pr & 3) * 16
-                                      : kOutOfRange);
-    }
-    uint4 w[U];
-    uint32_t sc[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = c0 + u * kWave + lane;
-      const bool ok = c < ns;
-      sc[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (c >> 2) * 2 : kOutOfRange, 0, 0);
-      w[u] = buffer_load16<kLoadNonTemporal>(rw, ok ? c * 16 : kOutOfRange);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int p = tid + i * W * kWave;
-      if (p < kPieces) {
-        const int sp = p / kSlicePieces;
-        const int q = p % kSlicePieces;
-        const int b = q / (U * 4 * kWave);
-        const int pr = q % (U * 4 * kWave);
-        const int cr = pr >> 2;  // chunk within the stage: 64 u + l
-        h2_t pp[4];
-        pair_x(xv[i], pp);
-        xs[(((sp * NB + b) * U + cr / kWave) * 4 + (pr & 3)) * kWave + cr % kWave] =
-            make_uint4(__builtin_bit_cast(uint32_t, pp[0]), __builtin_bit_cast(uint32_t, pp[1]),
-                       __builtin_bit_cast(uint32_t, pp[2]), __builtin_bit_cast(uint32_t, pp[3]));
-      }
-    }
-    lds_barrier();
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t words[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-      const float scale = h2f((uint16_t)sc[u]);
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        float part = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint4 pv = xs[(((sl * NB + b) * U + u) * 4 + j) * kWave + lane];
-          const h2_t xp[4] = {as_h2(pv.x), as_h2(pv.y), as_h2(pv.z), as_h2(pv.w)};
-          part = dot_word(words[j], xp, part);
+      for (int r = 0; r < R; ++r) {
+        const float t = wave_sum(acc[b][r]);
+        if (lane == 63 && row0 + r < M && b0 + b < B) {
+          const size_t o = (size_t)(b0 + b) * M + row0 + r;
+          y[o] = f2h(t);
+          if (acc_out) acc_out[o] = t;
         }
-        acc[b] = __builtin_fmaf(part, scale, acc[b]);
+      }
+  } else {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float t = wave_sum(acc[b][r]);
+        if (lane == 63) red[(sl * NB + b) * kRows + rwave * R + r] = t;
+      }
+    __syncthreads();
+    // Lane b R + r of the slice-0 wave adds row row0 + r's sums for batch
+    // row b0 + b.
+    if (sl == 0 && active && lane < NB * R) {
+      const int b = lane / R;
+      const int r = lane % R;
+      if (row0 + r < M && b0 + b < B) {
+        float sum = 0.f;
+#pragma unroll
+        for (int s2 = 0; s2 < kS; ++s2) sum += red[(s2 * NB + b) * kRows + rwave * R + r];
+        const size_t o = (size_t)(b0 + b) * M + row0 + r;
+        y[o] = f2h(sum);
+        if (acc_out) acc_out[o] = sum;
       }
     }
-    lds_barrier();  // every wave's reads are done before the next stage's stores
-  }
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    const float t = wave_sum(acc[b]);
-    if (lane == 63) red[(sl * NB + b) * R + r] = t;
-  }
-  __syncthreads();
-  if (sl == 0 && active && lane < NB && b0 + lane < B) {
-    float sum = 0.f;
-    for (int s2 = 0; s2 < S; ++s2) sum += red[(s2 * NB + lane) * R + r];
-    const size_t o = (size_t)(b0 + lane) * M + row;
-    y[o] = f2h(sum);
-    if (acc_out) acc_out[o] = sum;
   }
 }
 

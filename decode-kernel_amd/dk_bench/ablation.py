@@ -57,23 +57,23 @@ def run(configs, steps: int) -> dict:
         m, k = SHAPES[name]
         packed, scales, x = gpu_case(m, k, seed=1000 + list(SHAPES).index(name))
         desc = _abi.describe(lib, m, k, 1)
-        shape = benchlib.parse_v5_shape(desc["kernel"])
-        if shape is None:
-            raise RuntimeError(f"{name}: the product runs {desc['kernel']}, not a v5 stage kernel")
+        kern = benchlib.parse_kernel(desc["kernel"])
+        if kern is None:
+            raise RuntimeError(f"{name}: the product runs {desc['kernel']}, not a stage-loop kernel")
         pk, sc = weight_copies(packed, scales)
         n = len(pk)
         y_prod = _cuda.w4a16_gemv(pk[0], sc[0], x)
         y = torch.empty_like(y_prod)
-        benchlib.v5(0, shape, pk[0], sc[0], x, y)
+        benchlib.run_kernel(kern, 0, pk[0], sc[0], x, y)
         torch.cuda.synchronize()
         if not torch.equal(y, y_prod):
-            raise RuntimeError(f"{name}: bench-library instance {shape} differs from the product")
-        row = {"M": m, "K": k, "kernel": desc["kernel"], "shape_RUWP": list(shape),
+            raise RuntimeError(f"{name}: bench-library instance {kern} differs from the product")
+        row = {"M": m, "K": k, "kernel": desc["kernel"], "shape": [kern[0], *kern[1]],
                "bytes_moved": bytes_moved_w4(m, k, 1)}
         timings = {
             "product": lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x),
-            "no_decode": lambda i: benchlib.v5(1, shape, pk[i % n], sc[i % n], x, y),
-            "loads_only": lambda i: benchlib.v5(2, shape, pk[i % n], sc[i % n], x, y),
+            "no_decode": lambda i: benchlib.run_kernel(kern, 1, pk[i % n], sc[i % n], x, y),
+            "loads_only": lambda i: benchlib.run_kernel(kern, 2, pk[i % n], sc[i % n], x, y),
         }
         for key, fn in timings.items():
             st, _ = time_graph_steps(fn, steps=steps, preroll=flush)

@@ -18,7 +18,7 @@ _SIGNATURES = {
     "dkb_onestage": (_I, [_I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P]),
     "dkb_v4": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, ctypes.c_ulonglong, _I, _I,
                     _P]),
-    "dkb_v4_waves": (_I, [_I, _I, _I, _P, _P, _P, _P, _I, _I, _P]),
+    "dkb_v4s": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P]),
     "dkb_timestamp": (_I, [_P, _I, _P]),
     "dkb_wall_clock_khz": (_I, []),
 }
@@ -106,13 +106,43 @@ def wall_clock_khz() -> int:
     return int(load().dkb_wall_clock_khz())
 
 
-def v4_waves(r: int, u: int, s: int, packed, scales, x, y) -> int:
-    """The split-over-waves v4 (B = 1): R rows per workgroup, U chunks per
-    lane per stage, S slices. Returns 3 (nothing launched) for a shape not
-    instantiated or over the LDS bound."""
+def v4s(shape: tuple, packed, scales, x, y, math: int = 0) -> int:
+    """The product's split-K kernel (B = 1) at shape (R, U, W, S, prefetch):
+    R rows per wave, U chunks per lane per stage and slice, W waves per
+    workgroup, S waves per row; math 0 product, 1 no decode, 2 loads only.
+    Returns 3 (nothing launched) for a shape not instantiated in the
+    measurement library."""
+    r, u, w, s_, pf = shape
     m, k = packed.shape[0], packed.shape[1] * 8
-    rc = load().dkb_v4_waves(r, u, s, packed.data_ptr(), scales.data_ptr(), x.data_ptr(),
-                             y.data_ptr(), m, k, stream_handle())
+    rc = load().dkb_v4s(math, r, u, w, s_, int(pf), packed.data_ptr(), scales.data_ptr(),
+                        x.data_ptr(), y.data_ptr(), m, k, stream_handle())
     if rc not in (0, 3):
-        raise RuntimeError(f"v4 waves R{r} U{u} S{s}: status {rc}")
+        raise RuntimeError(f"v4 split {shape} math {math}: status {rc}")
     return rc
+
+
+def parse_kernel(kernel_name: str) -> tuple | None:
+    """("v5", (R, U, W, prefetch)) for a gemv_v5_lds kernel name at one batch
+    row, ("split", (R, U, W, S, prefetch)) for a gemv_v4_split one, as
+    dk_gemv_describe reports them; None for any other kernel."""
+    v5 = parse_v5_shape(kernel_name)
+    if v5 is not None:
+        return ("v5", v5)
+    key = "gemv_v4_split<"
+    if key not in kernel_name:
+        return None
+    args = [a.strip() for a in kernel_name.split(key, 1)[1].split(">", 1)[0].split(",")]
+    r, u, w, s_, nb = (int(a) for a in args[:5])
+    if nb != 1:
+        return None
+    return ("split", (r, u, w, s_, args[5] == "true"))
+
+
+def run_kernel(kernel: tuple, math: int, packed, scales, x, y) -> None:
+    """Launches a kernel parsed by parse_kernel with the given math (0
+    product, 1 no decode, 2 loads only)."""
+    kind, shape = kernel
+    if kind == "v5":
+        v5(math, shape, packed, scales, x, y)
+    elif v4s(shape, packed, scales, x, y, math) == 3:
+        raise RuntimeError(f"split {shape} math {math} is not in the measurement library")

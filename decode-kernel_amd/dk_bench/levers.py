@@ -1,6 +1,6 @@
 """Launch-shape and kernel-variant sweeps behind the routing choices.
 
-    python -m dk_bench.levers floor|c0|v4|all [--steps 300] [--out PATH]
+    python -m dk_bench.levers floor|c0|v4|split|all [--steps 300] [--out PATH]
     (from decode-kernel_amd/, after build_ext.py)
 
   floor  read-probe launch shapes at the algorithmic bytes of c0, c1 and c2
@@ -9,11 +9,13 @@
          LDS or in registers, weights issued first or last, one or two waves
          per row, 4 to 16 waves per workgroup) and streaming-kernel shapes,
          against the product;
-  v4     split-K over the waves of one workgroup (rows per workgroup,
-         chunks per lane per stage, 1-16 slices; the product's v4) and over
-         workgroups with a ticket reduction (a sample, also without the
-         reduction), at short and tall rows, against the product's v5 and v4.
-
+  v4     the product's split-K kernel at every instantiated shape (rows per
+         wave, chunks per lane per stage, waves per workgroup, 2-8 waves per
+         row, prefetch) and the cross-workgroup ticket form (a sample, also
+         without the reduction), at short and tall rows, against the
+         product's v5 and v4;
+  split  the split-K kernel's shapes against the product's v5 (B = 1) over
+         the shapes the streaming kernel's launch rules were set on.
 Every variant that computes y is checked against the product's v5 output
 (bit-exact where the summation order is the same, else within 1e-3 plus one
 fp16 ulp) before it is timed. Timing as in bench.py: HIP graphs of `steps`
@@ -29,9 +31,6 @@ from pathlib import Path
 
 import torch
 
-V4_SHAPES = [(1, 1, 4, True), (1, 2, 4, True), (1, 4, 4, True), (1, 1, 8, True), (1, 2, 8, True),
-             (1, 4, 8, True), (1, 2, 4, False), (1, 4, 4, False), (2, 1, 4, True), (2, 2, 4, True),
-             (1, 1, 16, True), (1, 2, 16, True)]
 V4_PROBLEMS = {"c0": (4096, 4096), "c2": (4096, 11008), "m1024_k28672": (1024, 28672),
                "m512_k28672": (512, 28672), "m2048_k16384": (2048, 16384),
                "m2048_k11008": (2048, 11008), "m1024_k8192": (1024, 8192), "c4b": (8192, 28672)}
@@ -104,11 +103,22 @@ def sweep_c0(flush, steps: int) -> dict:
     return rows
 
 
+SPLIT_PROBLEMS = [(4096, 4096), (4096, 11008), (4096, 5120), (4096, 6144), (3328, 5120),
+                  (8192, 5120), (11008, 5120), (13824, 5120), (4096, 8192), (5120, 8192),
+                  (8192, 8192), (4096, 14336), (4096, 28672), (8192, 28672), (28672, 8192),
+                  (11008, 4096), (14336, 4096), (2048, 16384), (2048, 4096), (1024, 28672),
+                  (1024, 11008), (512, 28672), (512, 4096), (512, 8320)]
+V4S_SHAPES = [(r, u, w, k, pf) for k, us in ((2, (1, 2, 4)), (4, (1, 2)), (8, (1,)))
+              for r in (1, 2) for u in us for w in (4, 8, 16) for pf in (True, False)
+              if w >= k and (r, u) != (2, 4)]
+
+
 def sweep_v4(flush, steps: int) -> dict:
-    """Split-K two ways, against the product's v5 and v4: over the waves of
-    one workgroup (gemv_v4_waves: R rows per workgroup, U chunks per lane per
-    stage, S slices; the product's v4) and over workgroups with a ticket
-    reduction (gemv_v4_lds, a sample of shapes, also without the reduction)."""
+    """Split-K two ways, against the product's v5 and v4: the product's
+    kernel (gemv_v4_split: S waves per row inside the streaming kernel's
+    stage loop) at every shape the measurement library instantiates, and
+    across workgroups with a ticket reduction (gemv_v4_lds, a sample of
+    shapes, also without the reduction)."""
     from decode_kernel import _cuda
 
     from . import benchlib
@@ -130,18 +140,16 @@ def sweep_v4(flush, steps: int) -> dict:
                 flush)
         print(f"v4 {name}: product v5 {rows['product_v5']:.3f}; product v4 " + ", ".join(
             f"s{sk} {rows[f'product_v4_s{sk}']:.3f}" for sk in (2, 4, 8, 16)), flush=True)
-        for r in (1, 2, 4, 8):
-            for u in (1, 2, 4):
-                for s_ in (1, 2, 4, 8, 16):
-                    if benchlib.v4_waves(r, u, s_, pk[0], sc[0], x, y) == 3:
-                        continue
-                    torch.cuda.synchronize()
-                    if not _close(y, y_prod):
-                        raise RuntimeError(f"v4 waves R{r} U{u} S{s_} differs from v5 at {name}")
-                    key = f"waves_R{r}_U{u}_S{s_}"
-                    rows[key] = _time(lambda i: benchlib.v4_waves(r, u, s_, pk[i % n], sc[i % n], x,
-                                                                  y), steps, flush)
-                    print(f"v4 {name} {key}: {rows[key]:.3f} us", flush=True)
+        for shape in V4S_SHAPES:
+            if benchlib.v4s(shape, pk[0], sc[0], x, y) == 3:
+                raise RuntimeError(f"v4 split {shape} is not instantiated")
+            torch.cuda.synchronize()
+            if not _close(y, y_prod):
+                raise RuntimeError(f"v4 split {shape} differs from v5 at {name}")
+            key = "split_R{}_U{}_W{}_S{}_{}".format(*shape[:4], "pf" if shape[4] else "nopf")
+            rows[key] = _time(lambda i: benchlib.v4s(shape, pk[i % n], sc[i % n], x, y), steps,
+                              flush)
+            print(f"v4 {name} {key}: {rows[key]:.3f} us", flush=True)
         for splits in (2, 4):
             ws = torch.empty(splits * m, dtype=torch.float32, device="cuda")
             tickets = torch.zeros(m, dtype=torch.int64, device="cuda")
@@ -167,9 +175,44 @@ def sweep_v4(flush, steps: int) -> dict:
     return out
 
 
+def sweep_split(flush, steps: int) -> dict:
+    """The split-K kernel at every instantiated shape against the product's
+    v5 at B = 1, over SPLIT_PROBLEMS."""
+    from decode_kernel import _cuda
+
+    from . import benchlib
+    from .ablation import gpu_case
+    from .common import weight_copies
+
+    out = {}
+    for m, k in SPLIT_PROBLEMS:
+        name = f"m{m}_k{k}"
+        packed, scales, x = gpu_case(m, k, seed=3000 + m + k)
+        pk, sc = weight_copies(packed, scales)
+        n = len(pk)
+        y_prod = _cuda.w4a16_gemv(pk[0], sc[0], x)
+        y = torch.empty_like(y_prod)
+        rows = {"product_v5": _time(lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x), steps, flush)}
+        for shape in V4S_SHAPES:
+            benchlib.v4s(shape, pk[0], sc[0], x, y)
+            torch.cuda.synchronize()
+            if not _close(y, y_prod):
+                raise RuntimeError(f"v4 split {shape} differs from v5 at {name}")
+            key = "R{}_U{}_W{}_S{}_{}".format(*shape[:4], "pf" if shape[4] else "nopf")
+            rows[key] = _time(lambda i: benchlib.v4s(shape, pk[i % n], sc[i % n], x, y), steps,
+                              flush)
+        best = min((v, kk) for kk, v in rows.items() if kk != "product_v5")
+        print(f"split {name}: product v5 {rows['product_v5']:.3f}; best {best[1]} {best[0]:.3f}",
+              flush=True)
+        out[name] = rows
+        del pk, sc, packed, scales, x
+        torch.cuda.empty_cache()
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("what", choices=["floor", "c0", "v4", "all"])
+    ap.add_argument("what", choices=["floor", "c0", "v4", "split", "all"])
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--out", type=Path, default=None)
     args = ap.parse_args()
@@ -185,6 +228,8 @@ def main() -> None:
         res["c0"] = sweep_c0(flush, args.steps)
     if args.what in ("v4", "all"):
         res["v4"] = sweep_v4(flush, args.steps)
+    if args.what in ("split", "all"):
+        res["split"] = sweep_split(flush, args.steps)
     if args.out:
         args.out.parent.mkdir(parents=True, exist_ok=True)
         args.out.write_text(json.dumps(res, indent=2) + "\n")

@@ -108,10 +108,16 @@ def test_split_k_needs_no_workspace(lib):
             c = _abi.default_config(lib, version=v, split_k=sk)
             for m, k, b in ((4096, 4096, 1), (4096, 11008, 5), (64, 256, 2)):
                 assert lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(c)) == 0, (v, sk, m, k, b)
-    d = _abi.describe(lib, 4096, 11008, 1, version=4, split_k=4)
-    assert d["kernel"].startswith("void dk::gemv_v4_waves<4, 1, 1>") and d["block"] == [1024, 1, 1]
-    d = _abi.describe(lib, 1024, 28672, 1, version=4, split_k=32)  # 16 slices at most
-    assert d["kernel"].startswith("void dk::gemv_v4_waves<1, 1, 1>") and d["block"] == [1024, 1, 1]
+    # The launch is one gemv_v4_split<R, U, W, S, NB, prefetch>: S waves per
+    # row (at most split_k, K / 128 and 8), W / S * R rows per workgroup.
+    for m, k, b, sk in ((4096, 11008, 1, 4), (1024, 28672, 1, 32), (512, 28672, 1, 8),
+                        (333, 8192, 3, 7), (64, 128, 2, 4)):
+        d = _abi.describe(lib, m, k, b, version=4, split_k=sk)
+        assert d["kernel"].startswith("void dk::gemv_v4_split<"), d["kernel"]
+        r, u, w, s, nb = (int(a) for a in d["kernel"].split("<", 1)[1].split(">", 1)[0].split(",")[:5])
+        assert 1 <= s <= min(sk, k // 128, 8) and w % s == 0, (m, k, b, sk, d["kernel"])
+        assert d["block"] == [64 * w, 1, 1] and d["launches"] == 1
+        assert d["grid"] == [-(-m // (w // s * r)), -(-b // nb), 1], (m, k, b, sk, d)
 
 
 def test_reference_workspace_contract_checks(lib):
@@ -142,7 +148,7 @@ def test_describe_names_the_dispatched_kernel(lib):
     assert d["kernel"].startswith("void dk::gemv_v5_lds<1, 2, 8, 1, true, dk::LayoutLogical, 5")
     assert d["grid"] == [512, 1, 1] and d["block"] == [512, 1, 1] and d["launches"] == 1
     d = _abi.describe(lib, 4096, 11008, 1, version=4, split_k=4)
-    assert d["kernel"].startswith("void dk::gemv_v4_waves<") and d["grid"] == [1024, 1, 1]
+    assert d["kernel"].startswith("void dk::gemv_v4_split<")
     assert _abi.describe(lib, 4096, 4096, 16, reuse_weights=1)["kernel"].startswith(
         "void dk::gemv_reuse<")
     assert _abi.describe(lib, 4096, 4096, 2, reuse_weights=1)["kernel"].startswith(
@@ -359,3 +365,7 @@ def test_bench_library_loads_and_stays_out_of_the_product(lib):
     assert exported == set(benchlib.EXPORTS), exported
     assert benchlib.parse_v5_shape(_abi.describe(lib, 4096, 4096, 1)["kernel"]) == (1, 2, 8, True)
     assert benchlib.parse_v5_shape(_abi.describe(lib, 4096, 4096, 1, version=4)["kernel"]) is None
+    assert benchlib.parse_kernel(_abi.describe(lib, 4096, 4096, 1)["kernel"]) == ("v5", (1, 2, 8, True))
+    assert benchlib.parse_kernel(_abi.describe(lib, 4096, 11008, 1)["kernel"]) == \
+        ("split", (1, 1, 16, 2, True))
+    assert benchlib.parse_kernel(_abi.describe(lib, 4096, 11008, 2)["kernel"]) is None

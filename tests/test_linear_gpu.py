@@ -243,10 +243,14 @@ def test_bench_library_variants_compute_the_gemv():
         _, _, _, pd, sd, xd = _upload(m, k, 1, seed=77 + m)
         y_prod = _cuda.w4a16_gemv(pd, sd, xd)
         y = torch.empty_like(y_prod)
-        shape = benchlib.parse_v5_shape(_abi.describe(lib, m, k, 1)["kernel"])
-        benchlib.v5(0, shape, pd, sd, xd, y)
+        kern = benchlib.parse_kernel(_abi.describe(lib, m, k, 1)["kernel"])
+        for math in (0, 1, 2):
+            # The ablation maths run the product's loads (their outputs are
+            # not the GEMV); the product math is bit-equal to the product.
+            benchlib.run_kernel(kern, math, pd, sd, xd, y)
+        benchlib.run_kernel(kern, 0, pd, sd, xd, y)
         torch.cuda.synchronize()
-        assert torch.equal(y, y_prod), (m, k, shape)
+        assert torch.equal(y, y_prod), (m, k, kern)
         if k <= 4096:
             for w, s in ((8, 1), (16, 2)):
                 for lds in (True, False):

@@ -312,8 +312,8 @@ def test_reuse_split_graph_replays():
                                          (4096, 4096, 16, 4), (1024, 28672, 1, 16),
                                          (333, 8192, 3, 7), (64, 128, 2, 4)])
 def test_v4_split_over_waves(m, k, b, split):
-    # v4 splits K into min(split_k, K/128, 16) slices on the waves of one
-    # workgroup and adds them in slice order through LDS: against the
+    # v4 takes each row on up to min(split_k, K/128, 8) waves of one
+    # workgroup and adds their sums in slice order through LDS: against the
     # oracle, bit-identical over repeated calls and through the C ABI with no
     # workspace, and every split count in range meets the oracle.
     from decode_kernel import _abi
@@ -397,26 +397,37 @@ def test_large_batches_all_paths(batch):
 
 
 # One shape per kernel the streaming path can choose (rows per wave, chunks
-# per stage, waves per workgroup, prefetch, batch rows per stage), each with M
-# not a multiple of the workgroup's rows so the last workgroup has idle waves.
-# For one batch row:
+# per stage, waves per workgroup, waves per row, prefetch, batch rows per
+# stage), each with M not a multiple of the workgroup's rows so the last
+# workgroup has idle waves. For one batch row, gemv_v4_split (S waves per
+# row) where it is the faster kernel:
+#   M <= 512, 2048 < K <= 4096             -> R1 U1 W4 S2 prefetch
+#   M <= 512, 4096 < K < 16384             -> R1 U2 W8 S4 prefetch
+#   M <= 512, K >= 16384                   -> R1 U2 W8 S4
+#   512 < M <= 1024, K >= 16384            -> R2 U2 W8 S4
+#   3072 < M <= 4096, 8192 < K <= 12288    -> R1 U1 W16 S2 prefetch
+#   3072 < M <= 4096, K > 12288            -> R2 U1 W16 S2 prefetch
+#   4096 < M <= 8192, K = 8192             -> R2 U2 W8 S2
+# and gemv_v5_lds otherwise:
 #   K <= 2048                              -> R1 U1 W16 prefetch
 #   M <= 3072: K <= 4096 / 8192 / 12288    -> R1 U2 / U4 / U6 W4 prefetch
 #              longer rows                 -> R1 U4 W4 (M <= 1024) or W8
-#   M > 8192, K <= 8192                    -> R2 U2 W4
-#   M > 8192, K > 8192                     -> R2 U1 W8
-#   M <= 4096, K > 8192                    -> R1 U2 W16 prefetch
-#   4096 < M <= 8192, K >= 8192            -> R2 U1 W16 prefetch
+#   3072 < M <= 8192, 4096 < K < 8192      -> R1 U1 W16 prefetch
+#   M <= 5120, K = 8192                    -> R1 U4 W4 prefetch
+#   M > 8192: 4096 < K < 8192 / K <= 8192 / longer -> R2 U1 W8 prefetch /
+#                                             R2 U2 W4 / R2 U1 W8
+#   4096 < M <= 8192, K > 8192             -> R2 U1 W16 prefetch
 #   otherwise                              -> R1 U2 W8 prefetch
 # and batches of 2-8 rows: tiles of 2, 3 or 4 rows per stage, the tile
 # choice depending on M and K ranges (the dispatch comments in dk_gemv.hip).
 # The shapes are ragged and fall in every M range (<= 512, 1024, 2048, 3072,
-# 4096, 8192, above) and K range (<= 2048, 4096, 8192, 12288, above) the
-# dispatch tells apart.
+# 4096, 8192, above) and K range (<= 2048, 4096, 8192, 12288, 16384, above)
+# the dispatch tells apart.
 DISPATCH_SHAPES = [(5000, 1920), (9001, 4224), (8197, 8320), (3000, 8320), (6001, 8320),
                    (2500, 4224), (500, 8320), (1000, 4224), (2000, 12416), (4000, 12416),
                    (700, 3968), (1500, 6144), (900, 16512), (3072, 2048), (400, 5120),
-                   (5000, 6144), (3200, 5248), (4500, 8192)]
+                   (5000, 6144), (3200, 5248), (4500, 8192), (300, 3968), (450, 20480),
+                   (3500, 11008), (7000, 16512)]
 
 
 @pytest.mark.parametrize("m,k", DISPATCH_SHAPES)
@@ -529,9 +540,10 @@ def test_stream_probes():
 
 
 
-def test_v4_concurrent_streams_do_not_share_tickets():
-    # Two split-K GEMVs with the same tile count run at the same time on two
-    # streams: each uses its own workspace tickets, so both must be exact.
+def test_v4_concurrent_streams_are_independent():
+    # Two split-K GEMVs of the same shape run at the same time on two
+    # streams: they share no memory but their inputs and outputs, so both
+    # must match their serial results bit for bit.
     from decode_kernel import gemv
 
     cases = []
