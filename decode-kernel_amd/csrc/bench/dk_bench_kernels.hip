@@ -520,6 +520,39 @@ DKB_API int dkb_wall_clock_khz(void) {
   return khz;
 }
 
+// The reuse path's tile kernels at any instantiated shape (B rows in tiles of
+// 16): kind 0 gemv_reuse<KS, RT, SG, pairs> (MFMA operands loaded directly),
+// kind 1 gemv_reuse_lds<KS, RT, pairs> (both operands staged in LDS by the
+// buffer-load-to-LDS path; SG must be 2). Returns 3 (nothing launched) for a
+// shape not instantiated here.
+DKB_API int dkb_reuse(int kind, int KS, int RT, int SG, int pairs, const void* packed,
+                      const void* scales, const void* x, void* y, int M, int K, int B,
+                      hipStream_t stream) {
+  const auto* p = static_cast<const uint4*>(packed);
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* xx = static_cast<const uint4*>(x);
+  auto* yy = static_cast<uint16_t*>(y);
+#define DKB_R0(ks, rt, sg, pr)                                                                 \
+  if (kind == 0 && KS == ks && RT == rt && SG == sg && pairs == (int)pr) {                     \
+    hipLaunchKernelGGL((dk::gemv_reuse<ks, rt, sg, pr>), dim3((M + 16 * rt - 1) / (16 * rt),     \
+                       (B + 15) / 16), dim3(ks * 64), 0, stream, p, s, xx, yy, M, K, B);        \
+    return launch_error("reuse");                                                              \
+  }
+#define DKB_R1(ks, rt, pr)                                                                     \
+  if (kind == 1 && KS == ks && RT == rt && SG == 2 && pairs == (int)pr) {                      \
+    hipLaunchKernelGGL((dk::gemv_reuse_lds<ks, rt, pr>), dim3((M + 16 * rt - 1) / (16 * rt),     \
+                       (B + 15) / 16), dim3(ks * 64), 0, stream, p, s, xx, yy, M, K, B);        \
+    return launch_error("reuse lds");                                                          \
+  }
+  DKB_R0(8, 1, 2, true) DKB_R0(8, 1, 2, false) DKB_R0(8, 1, 4, false) DKB_R0(16, 1, 4, false)
+  DKB_R0(16, 1, 2, false) DKB_R0(8, 2, 2, true) DKB_R0(8, 2, 2, false) DKB_R0(8, 2, 4, false)
+  DKB_R1(8, 1, true) DKB_R1(8, 1, false) DKB_R1(16, 1, true) DKB_R1(16, 1, false)
+  DKB_R1(8, 2, true) DKB_R1(8, 2, false) DKB_R1(4, 1, true) DKB_R1(4, 2, true)
+#undef DKB_R1
+#undef DKB_R0
+  return 3;
+}
+
 // The product's split-K kernel (gemv_v4_split, B = 1) at shape R rows per
 // wave, U chunks per lane per stage, W waves, S slices per row, prefetch on
 // or off; math 0 is the product's, 1 no decode and 2 loads only (as for

@@ -587,6 +587,56 @@ int launch_reuse(const Launch& L, const uint4* p, const uint16_t* s, const uint4
            K, B);
 }
 
+template <int KS, int RT>
+int launch_reuse_lds(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x,
+                     uint16_t* y, int M, int K, int B) {
+  const dim3 grid((M + 16 * RT - 1) / (16 * RT), (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
+  if ((K / DK_GROUP_SIZE) % 2 == 0 && aligned(s, 4))
+    return L("reuse launch", dk::gemv_reuse_lds<KS, RT, true>, grid, dim3(KS * 64), 0, p, s, x, y,
+             M, K, B);
+  return L("reuse launch", dk::gemv_reuse_lds<KS, RT, false>, grid, dim3(KS * 64), 0, p, s, x, y, M,
+           K, B);
+}
+
+// The single-pass tiles. The LDS-staged kernel (gemv_reuse_lds) against the
+// tiles that load the MFMA operands directly (gemv_reuse, the earlier rule's
+// shape) in brackets, us per launch, from the same sweep:
+//                        B = 4          B = 8          B = 16         B = 32
+//   M = K = 4096:        4.65 (4.62)    4.94 (5.01)    5.58 (6.78)    6.37 (7.82)
+//   M = 4096, K = 11008: 7.84 (8.40)    8.85 (10.65)   10.97 (15.20)  13.24 (16.92)
+//   M = 3072, K = 8192:  6.60 (6.74)    7.36 (7.69)    8.56 (11.30)   10.58 (13.17)
+//   M = 2048, K = 8192:                 7.12 (7.52)    8.25 (11.09)   8.08 (11.08)
+//   M = 5120, K = 5120:  6.43 (6.55)    7.04 (7.75)    7.83 (10.03)   11.76 (16.51)
+//   M = 6144, K = 8192:  9.20 (9.15)    10.10 (11.14)  11.58 (14.69)  18.98 (23.78)
+//   M = 8192, K = 28672: 25.70 (26.18)  29.02 (32.87)  34.79 (41.08)  64.65 (77.98)
+//   M = 11008, K = 4096: 8.42 (8.84)    9.42 (10.12)   11.21 (13.05)  15.25 (18.63)
+//   M = 28672, K = 8192: 30.64 (28.43)  34.18 (34.22)  39.05 (44.75)  66.82 (77.26)
+// Up to 4096 rows (256 tiles) one tile per wave, 16 waves (8 up to 8 batch
+// rows of up to 8192 weights: M = K = 4096, B = 8 4.94 against 5.09), two
+// per wave above 16 batch rows (the grid then has two batch tiles); to 8192
+// rows two tiles per wave, 8 waves (4 above 16 batch rows: M = 6144,
+// K = 8192, B = 32 18.98 against 20.24); above, 4 waves (two tiles per wave
+// from 9 batch rows). The direct tiles stay at M = 28672, K = 8192 up to 8
+// batch rows (B = 3: 27.79 against 29.80) and on rows of up to 4096 weights
+// at 2049-4096 rows up to 5 batch rows (M = K = 4096: B = 3 4.53 against
+// 4.60, B = 5 4.61 against 4.77).
+int launch_reuse_tiles(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x,
+                       uint16_t* y, int M, int K, int B) {
+  if (M > 2048 && M <= 4096 && K <= 4096 && B <= 5)
+    return launch_reuse<8, 1, 2>(L, p, s, x, y, M, K, B);
+  if (M > 8192) {
+    if (B <= 8 && K > 4096) return launch_reuse<8, 2, 2>(L, p, s, x, y, M, K, B);
+    return B <= 8 ? launch_reuse_lds<4, 1>(L, p, s, x, y, M, K, B)
+                  : launch_reuse_lds<4, 2>(L, p, s, x, y, M, K, B);
+  }
+  if (M > 4096)
+    return B <= 16 ? launch_reuse_lds<8, 2>(L, p, s, x, y, M, K, B)
+                   : launch_reuse_lds<4, 2>(L, p, s, x, y, M, K, B);
+  if (M > 2048 && B > 16) return launch_reuse_lds<8, 2>(L, p, s, x, y, M, K, B);
+  if (M > 2048 && B <= 8 && K <= 8192) return launch_reuse_lds<8, 1>(L, p, s, x, y, M, K, B);
+  return launch_reuse_lds<16, 1>(L, p, s, x, y, M, K, B);
+}
+
 // h of the MLP step at the start of its workspace, padded to 256 bytes so
 // that the down projection's split-K workspace after it stays aligned.
 size_t mlp_h_bytes(int I, int B) { return ((size_t)B * (size_t)I * sizeof(uint16_t) + 255) / 256 * 256; }
@@ -628,43 +678,47 @@ int launch_reuse_split(const Launch& L, const uint4* p, const uint16_t* s, const
 
 enum class ReuseShape { kStream, kTiles };
 
+// Which kernel the reuse path takes, from a sweep of the tile kernels (both
+// forms, 4-16 waves, one or two tiles per wave) against the streaming
+// kernel at 3-32 batch rows on 11 shapes (dk_bench.levers reuse), us:
+//   M = 2048, K = 16384: B = 4 stream 9.02 (tiles 9.37), B = 5 tiles 9.97 (stream 10.80)
+//   M = 2048, K = 8192:  B = 4 stream 5.74 (6.19), B = 8 tiles 7.12 (7.66)
+//   M = 1024, K = 4096:  B = 8 stream 3.73 (4.64), B = 12 tiles 4.87 (4.99)
+//   M = 4096, K = 11008, B = 3: tiles 7.50 (stream 9.63)
+//   M = 3072, K = 8192,  B = 3: tiles 6.40 (stream 7.11)
+//   M = K = 4096,        B = 3: stream 4.55 (tiles 4.60)
+//   M = 6144, K = 8192,  B = 3: tiles 9.14 (stream 10.45)
+// Up to 512 rows the streaming kernel keeps every batch up to 32 rows (M =
+// 512, K = 8320, B = 32: 11.67 against 11.47 for the earlier tiles); it also
+// keeps four batch rows below 3072 rows and up to eight at M <= 2048 on rows
+// shorter than 8192 weights, where the earlier tiles lost and no sweep point
+// says otherwise.
 ReuseShape reuse_shape(int M, int K, int B) {
-  // Three batch rows take the tiles on large matrices and, from 3072 rows,
-  // on rows of 4097-8191 weights.
-  const bool three_rows_tiles =
-      (size_t)M * (size_t)K >= ((size_t)1 << 27) || (M >= 3072 && K > 4096 && K < 8192);
-  if (B <= 2 || (B == 3 && !three_rows_tiles) ||
-      (B == 4 && M < 3072) ||
-      (B <= 8 && M <= 2048) || (B <= 16 && M <= 1024) || (B <= 32 && M <= 512) || M <= 128)
-    return ReuseShape::kStream;
+  if (B <= 2 || M <= 128) return ReuseShape::kStream;
+  if (M <= 512) return B <= 32 ? ReuseShape::kStream : ReuseShape::kTiles;
+  if (M <= 1024) return B < 12 ? ReuseShape::kStream : ReuseShape::kTiles;
+  if (M <= 2048 && (B <= 4 || (B <= 8 && K < 8192))) return ReuseShape::kStream;
+  if (B == 4 && M < 3072) return ReuseShape::kStream;
+  if (B == 3) {
+    const bool tiles = K >= 8192 || (size_t)M * (size_t)K >= ((size_t)1 << 27) ||
+                       (M >= 3072 && K > 4096 && K < 8192);
+    return tiles ? ReuseShape::kTiles : ReuseShape::kStream;
+  }
   return ReuseShape::kTiles;
 }
 
-// The tiles split K over workgroups, given a workspace, where that measured
-// faster: rows longer than 8192 weights with few tiles (M <= 2048) or 32 or
-// more batch rows (M <= 4096), and rows of 8192 at 2049-4096 rows with 32 or
-// more batch rows. Each split reads a quarter of the activations, which
-// bound the tiles at these batches, but the reduction across workgroups
-// costs several microseconds on this 8-XCD part: the partials and tickets
-// pass the non-coherent L2s (agent-scope atomics). Measured (us, single-pass
-// tiles in brackets): M = 2048, K = 16384, B = 16 16.26 (20.05);
-// M = 4096, K = 11008: B = 32 24.67 (29.31), B = 64 43.41 (56.23);
-// M = 3072, K = 12288, B = 32 22.77 (32.17); M = 4096, K = 14336, B = 64
-// 52.00 (71.88); M = 4096, K = 8192: B = 32 21.29 (22.35), B = 64 36.94
-// (42.59); and slower or level elsewhere: M = 2048, K = 8192: B = 16 12.39
-// (11.41), B = 32 15.29 (11.38); M = 1024, K = 8192, B = 32 12.05 (11.29);
-// M = 4096, K = 11008, B = 16 15.77 (15.72).
+// The tiles split K over workgroups, given a workspace, only for rows longer
+// than 8192 weights at M <= 1024 (M / 16 tiles cover too few CUs); the
+// reduction across workgroups costs several microseconds on this 8-XCD part
+// (the partials and tickets pass the non-coherent L2s), and the LDS-staged
+// tiles beat it wherever else it ran (us, split-K in brackets): M = 2048,
+// K = 16384: B = 16 13.65 (16.30), B = 32 13.31 (19.75); M = 4096,
+// K = 11008, B = 32 13.24 (24.79); M = 3072, K = 8192, B = 32 10.58 (21.07).
 bool reuse_split(int M, int K, int B) {
-  if (reuse_shape(M, K, B) != ReuseShape::kTiles || K < 8192 || M > 4096) return false;
-  return K > 8192 ? (M <= 2048 || B >= 32) : (M > 2048 && B >= 32);
+  return reuse_shape(M, K, B) == ReuseShape::kTiles && K > 8192 && M <= 1024;
 }
 
 size_t v3_lds_bytes(int K) { return (size_t)kWavesPerBlock * (K / DK_GROUP_SIZE) * sizeof(uint16_t); }
-
-int effective_split(int K, int split_k) {
-  const int G = K / DK_GROUP_SIZE;
-  return std::max(1, std::min(split_k, G));
-}
 
 int check_io(const uint32_t* packed, const uint16_t* scales, const uint16_t* x, const uint16_t* y) {
   if (!packed || !scales || !x || !y)
@@ -704,15 +758,7 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
     if (reuse_shape(M, K, B) == ReuseShape::kStream)
       return launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B);
     if (split) return launch_reuse_split(L, p4, scales, x4, y, M, K, B, workspace);
-    if (M > 4096 && M < 8192 && B > 8) return launch_reuse<8, 2, 4>(L, p4, scales, x4, y, M, K, B);
-    if (M > 4096) return launch_reuse<8, 2, 2>(L, p4, scales, x4, y, M, K, B);
-    if (M > 2048) {
-      if (B <= 8) return launch_reuse<8, 1, 2>(L, p4, scales, x4, y, M, K, B);
-      return K <= 4096 ? launch_reuse<8, 1, 4>(L, p4, scales, x4, y, M, K, B)
-                       : launch_reuse<16, 1, 4>(L, p4, scales, x4, y, M, K, B);
-    }
-    if (K < 8192) return launch_reuse<16, 1, 2>(L, p4, scales, x4, y, M, K, B);
-    return launch_reuse<8, 1, 2>(L, p4, scales, x4, y, M, K, B);
+    return launch_reuse_tiles(L, p4, scales, x4, y, M, K, B);
   }
   const dim3 block4(kWavesPerBlock * 64);
   const dim3 rows4((M + kWavesPerBlock - 1) / kWavesPerBlock);

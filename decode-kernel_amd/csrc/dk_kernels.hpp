@@ -824,6 +824,184 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Tiles with both operands staged by the buffer-load-to-LDS path (gfx950
+// loads of 16 bytes per lane that write LDS directly, lane l's bytes at
+// 16 l past the instruction's LDS base). The MFMA B operand takes batch row
+// l % 16 in lane l, so loading it directly makes every load instruction
+// touch 16 batch rows K * 2 bytes apart; at M = K = 4096, B = 16 that layout
+// cost 1.8 us of 6.9 against the same bytes read in row order. Here each
+// wave's block of x (16 batch rows x 512 bytes, two groups) and of weights
+// (16 RT rows x 128 bytes) is read in row order, 1 KiB per instruction,
+// straight into the wave's LDS, and read back in the MFMA layouts; the
+// source chunk of each lane is XOR-swizzled by row so that those reads (16
+// rows, one chunk) fall in 16 distinct groups of four banks with no
+// padding. x loads whose batch rows are all past B are not issued. Measured
+// on MI355X at M = K = 4096 (us, against gemv_reuse with the same waves and
+// blocks): B = 16 5.45 (7.02), B = 12 5.10 (6.25), B = 8 4.82 (5.13), B = 4
+// 4.57 (4.77). Issuing the next block before this block's wait (a second
+// buffer set) gained nothing: the compiler's wait before the LDS reads also
+// covers the other buffer's loads.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// XOR applied to the chunk index of row r of a staged block with kChunks
+// 16-byte chunks per row (16 rows reading one chunk hit distinct banks).
+template <int kChunks>
+__device__ __forceinline__ int stage_swizzle(int r) {
+  if constexpr (kChunks % 16 == 0) {
+    return r & 15;
+  } else {
+    static_assert(kChunks == 8, "rows of 8 or a multiple of 16 chunks");
+    return (r >> 1) & 7;
+  }
+}
+
+template <int KS, int RT>
+struct ReuseDmaLds {
+  uint4 x[KS][16 * 32];      // per wave: 16 batch rows x 32 chunks (two groups)
+  uint4 w[KS][RT * 16 * 8];  // per wave: 16 RT rows x 8 chunks (two groups)
+};
+
+template <int KS, int RT, bool kPairs>
+__global__ __launch_bounds__(KS * 64) void gemv_reuse_lds(const uint4* __restrict__ packed,
+                                                          const uint16_t* __restrict__ scales,
+                                                          const uint4* __restrict__ x4,
+                                                          uint16_t* __restrict__ y, int M, int K,
+                                                          int B) {
+  static_assert(KS >= RT, "wave t sums tile t");
+  write_stamp(DK_STAMP_REUSE);
+  __shared__ ReuseDmaLds<KS, RT> lds;
+  const int G = K >> 7;
+  const int nck = K >> 5;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = blockIdx.x * 16 * RT;
+  const int bt0 = blockIdx.y * kReuseBatch;
+  const int b = bt0 + (lane & 15);  // this lane's batch column
+  const int kq = lane >> 4;
+  const int r_lane = lane & 15;
+  __amdgpu_buffer_rsrc_t rw[RT], rs[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const int rows = __builtin_amdgcn_readfirstlane(max(0, min(16, M - row0 - 16 * t)));
+    const int rbase = rows > 0 ? row0 + 16 * t : 0;
+    rw[t] = buffer_rsrc(packed + (size_t)rbase * nck, (uint32_t)(rows * (K / 2)));
+    rs[t] = buffer_rsrc(scales + (size_t)rbase * G, (uint32_t)(rows * G * 2));
+  }
+  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
+  // x loads (two batch rows each) with a batch row below B (wave-uniform).
+  const int nxl = min(8, (max(0, min(16, B - bt0)) + 1) / 2);
+  uint4* xbuf = lds.x[wave];
+  uint4* wbuf = lds.w[wave];
+  f4_t acc[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+  for (int g0 = 2 * wave; g0 < G; g0 += 2 * KS) {
+    // Weights: load i covers rows 8 (i % 2) .. + 7 of tile i / 2, lane l
+    // chunk l % 8 of row 8 (i % 2) + l / 8 (chunk c = group c / 4 of the
+    // block, bytes 16 (c % 4) of it).
+#pragma unroll
+    for (int i = 0; i < 2 * RT; ++i) {
+      const int r = 8 * (i % 2) + lane / 8;
+      const int c = (lane % 8) ^ stage_swizzle<8>(r);
+      const int off = g0 * 4 + c < G * 4 ? r * nck * 16 + (g0 * 4 + c) * 16 : kOutOfRange;
+      // A local copy of the descriptor: given the array element itself, the
+      // host pass leaves the kernel's launch stub undefined.
+      const __amdgpu_buffer_rsrc_t rwt = rw[i / 2];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rwt, (lds_void_ptr)(wbuf + i * 64), 16, off, 0, 0,
+                                               kLoadNonTemporal);
+    }
+    // x: load i covers batch rows bt0 + 2i and + 1, lane l chunk l % 32 of
+    // row 2i + l / 32 (chunk c = group c / 16, bytes 16 (c % 16)).
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i < nxl) {
+        const int bb = 2 * i + lane / 32;
+        const int p = lane % 32;
+        const int c = (p & 16) | ((p ^ stage_swizzle<32>(bb)) & 15);
+        const bool ok = bt0 + bb < B && g0 * 16 + c < G * 16;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rx, (lds_void_ptr)(xbuf + i * 64), 16,
+            ok ? (bt0 + bb) * K * 2 + (g0 * 16 + c) * 16 : kOutOfRange, 0, 0, 0);
+      }
+    }
+    // Scales of this lane's four D rows: both groups in one 4-byte load where
+    // the scales allow (an even number of groups, so g0 + 1 < G).
+    float sc[RT][2][4];
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if constexpr (kPairs) {
+          const uint32_t two =
+              __builtin_amdgcn_raw_buffer_load_b32(rs[t], ((4 * kq + v) * G + g0) * 2, 0, 0);
+          sc[t][0][v] = h2f((uint16_t)two);
+          sc[t][1][v] = h2f((uint16_t)(two >> 16));
+        } else {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int off = g0 + u < G ? ((4 * kq + v) * G + g0 + u) * 2 : kOutOfRange;
+            sc[t][u][v] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs[t], off, 0, 0));
+          }
+        }
+      }
+    // Every load of the block, LDS writes included, has landed.
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      h8_t xp[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int xc = 16 * u + 4 * kq + j;
+        xp[j] = pair_x8(xbuf[r_lane * 32 + ((xc & 16) | ((xc ^ stage_swizzle<32>(r_lane)) & 15))]);
+      }
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        const int wc = (4 * u + kq) ^ stage_swizzle<8>(r_lane);
+        const uint4 wv = wbuf[(16 * t + r_lane) * 8 + wc];
+        const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+        f4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_word_h8(words[j]), xp[j], c, 0, 0, 0);
+        // A group past G loaded zero weights, so it adds nothing.
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(c[v], sc[t][u][v], acc[t][v]);
+      }
+    }
+    // The reads above have returned before the next block's loads write the
+    // buffers.
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  }
+  // Partials over the wave's own x buffer (no other wave reads it before the
+  // barrier), then tile t's KS partials added in wave order by wave t.
+  float* part = reinterpret_cast<float*>(xbuf);
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part[(t * 64 + lane) * 4 + v] = acc[t][v];
+  __syncthreads();
+  if (wave < RT) {
+    f4_t sum = {0.f, 0.f, 0.f, 0.f};
+    for (int w2 = 0; w2 < KS; ++w2) {
+      const float* pp = reinterpret_cast<const float*>(lds.x[w2]);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sum[v] += pp[(wave * 64 + lane) * 4 + v];
+    }
+    if (b < B) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int orow = row0 + 16 * wave + 4 * kq + v;
+        if (orow < M) y[(size_t)b * M + orow] = f2h(sum[v]);
+      }
+    }
+  }
+}
+
 // Split-K form for rows too few to give every CU a tile with the whole row:
 // grid.z = S workgroups share each set of RT tiles, workgroup z covering
 // groups [z * ceil(G / S), +ceil(G / S)), so each reads only its slice of

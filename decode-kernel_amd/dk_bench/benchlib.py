@@ -19,6 +19,7 @@ _SIGNATURES = {
     "dkb_v4": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, ctypes.c_ulonglong, _I, _I,
                     _P]),
     "dkb_v4s": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P]),
+    "dkb_reuse": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P]),
     "dkb_timestamp": (_I, [_P, _I, _P]),
     "dkb_wall_clock_khz": (_I, []),
 }
@@ -146,3 +147,16 @@ def run_kernel(kernel: tuple, math: int, packed, scales, x, y) -> None:
         v5(math, shape, packed, scales, x, y)
     elif v4s(shape, packed, scales, x, y, math) == 3:
         raise RuntimeError(f"split {shape} math {math} is not in the measurement library")
+
+
+def reuse(kind: int, ks: int, rt: int, sg: int, pairs: bool, packed, scales, x, y) -> int:
+    """The reuse path's tile kernels: kind 0 gemv_reuse<KS, RT, SG, pairs>,
+    kind 1 gemv_reuse_lds<KS, RT, pairs> (SG = 2). Returns 3 (nothing
+    launched) for a shape not instantiated in the measurement library."""
+    m, k = packed.shape[0], packed.shape[1] * 8
+    b = x.shape[0]
+    rc = load().dkb_reuse(kind, ks, rt, sg, int(pairs), packed.data_ptr(), scales.data_ptr(),
+                          x.data_ptr(), y.data_ptr(), m, k, b, stream_handle())
+    if rc not in (0, 3):
+        raise RuntimeError(f"reuse kind {kind} KS{ks} RT{rt} SG{sg}: status {rc}")
+    return rc

@@ -1,6 +1,6 @@
 """Launch-shape and kernel-variant sweeps behind the routing choices.
 
-    python -m dk_bench.levers floor|c0|v4|split|all [--steps 300] [--out PATH]
+    python -m dk_bench.levers floor|c0|v4|split|reuse|all [--steps 300] [--out PATH]
     (from decode-kernel_amd/, after build_ext.py)
 
   floor  read-probe launch shapes at the algorithmic bytes of c0, c1 and c2
@@ -15,7 +15,11 @@
          without the reduction), at short and tall rows, against the
          product's v5 and v4;
   split  the split-K kernel's shapes against the product's v5 (B = 1) over
-         the shapes the streaming kernel's launch rules were set on.
+         the shapes the streaming kernel's launch rules were set on;
+  reuse  the weight-reuse tile kernels (operands loaded directly, or staged
+         in LDS by the buffer-load-to-LDS path) at 3-32 batch rows over the
+         shapes the reuse path's launch rules were set on, against the
+         product's reuse path.
 Every variant that computes y is checked against the product's v5 output
 (bit-exact where the summation order is the same, else within 1e-3 plus one
 fp16 ulp) before it is timed. Timing as in bench.py: HIP graphs of `steps`
@@ -210,9 +214,62 @@ def sweep_split(flush, steps: int) -> dict:
     return out
 
 
+REUSE_PROBLEMS = [(4096, 4096), (4096, 11008), (3072, 8192), (11008, 4096), (6144, 8192),
+                  (5120, 5120), (28672, 8192), (8192, 28672), (2048, 16384), (2048, 8192),
+                  (1024, 4096)]
+REUSE_BATCHES = (3, 4, 5, 8, 12, 16, 32)
+REUSE_SHAPES = [(0, 8, 1, 2, True), (0, 8, 1, 4, False), (0, 16, 1, 4, False), (0, 16, 1, 2, False),
+                (0, 8, 2, 2, True), (0, 8, 2, 4, False),
+                (1, 8, 1, 2, True), (1, 16, 1, 2, True), (1, 8, 2, 2, True), (1, 4, 1, 2, True),
+                (1, 4, 2, 2, True)]
+
+
+def sweep_reuse(flush, steps: int) -> dict:
+    """Tile kernels of the reuse path against the product's reuse path."""
+    from decode_kernel import _cuda
+
+    from . import benchlib
+    from .ablation import gpu_case
+    from .common import weight_copies
+
+    out = {}
+    for m, k in REUSE_PROBLEMS:
+        packed, scales, _ = gpu_case(m, k, seed=4000 + m + k)
+        pk, sc = weight_copies(packed, scales)
+        n = len(pk)
+        gen = torch.Generator(device="cuda").manual_seed(m + k)
+        xall = torch.randn(max(REUSE_BATCHES), k, device="cuda", generator=gen).half()
+        for b in REUSE_BATCHES:
+            x = xall[:b].contiguous()
+            name = f"m{m}_k{k}_b{b}"
+            y_prod = _cuda.w4a16_gemv(pk[0], sc[0], x, reuse_weights=True)
+            y = torch.empty_like(y_prod)
+            rows = {"product_reuse": _time(
+                lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x, reuse_weights=True), steps, flush)}
+            for shape in REUSE_SHAPES:
+                kind, ks, rt, sg, pairs = shape
+                y.fill_(float("nan"))
+                if benchlib.reuse(kind, ks, rt, sg, pairs, pk[0], sc[0], x, y) == 3:
+                    raise RuntimeError(f"reuse {shape} is not instantiated")
+                torch.cuda.synchronize()
+                if not _close(y, y_prod):
+                    raise RuntimeError(f"reuse {shape} differs from the product at {name}")
+                key = "{}_KS{}_RT{}_SG{}{}".format("lds" if kind else "tiles", ks, rt, sg,
+                                                   "_pairs" if pairs else "")
+                rows[key] = _time(lambda i: benchlib.reuse(kind, ks, rt, sg, pairs, pk[i % n],
+                                                           sc[i % n], x, y), steps, flush)
+            best = min((v, kk) for kk, v in rows.items())
+            print(f"reuse {name}: product {rows['product_reuse']:.3f}; best {best[1]} {best[0]:.3f}",
+                  flush=True)
+            out[name] = rows
+        del pk, sc, packed, scales, xall
+        torch.cuda.empty_cache()
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("what", choices=["floor", "c0", "v4", "split", "all"])
+    ap.add_argument("what", choices=["floor", "c0", "v4", "split", "reuse", "all"])
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--out", type=Path, default=None)
     args = ap.parse_args()
@@ -230,6 +287,8 @@ def main() -> None:
         res["v4"] = sweep_v4(flush, args.steps)
     if args.what in ("split", "all"):
         res["split"] = sweep_split(flush, args.steps)
+    if args.what in ("reuse", "all"):
+        res["reuse"] = sweep_reuse(flush, args.steps)
     if args.out:
         args.out.parent.mkdir(parents=True, exist_ok=True)
         args.out.write_text(json.dumps(res, indent=2) + "\n")

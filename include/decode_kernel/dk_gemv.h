@@ -75,8 +75,8 @@ void dk_gemv_config_default(dk_gemv_config* cfg);
 
 /* Bytes of device workspace dk_w4a16_gemv takes for this call: 0 for every
  * variant (v4 included) but the weight-reuse path when its MFMA tiles split
- * K over workgroups (K > 8192 with M <= 2048, or with M <= 4096 and 32 or
- * more batch rows; K = 8192 with M of 2049-4096 and 32 or more batch rows).
+ * K over workgroups (rows longer than 8192 weights at M <= 1024 with 12 or
+ * more batch rows, 33 or more at M <= 512).
  * There it is optional and 8-byte aligned: one 8-byte ticket per set of 32
  * rows and 16 batch rows, padded to 256 bytes, then fp32 partials [4, B, M];
  * without it (NULL or too small) the path runs its single-pass tiles, same

@@ -150,14 +150,16 @@ def test_describe_names_the_dispatched_kernel(lib):
     d = _abi.describe(lib, 4096, 11008, 1, version=4, split_k=4)
     assert d["kernel"].startswith("void dk::gemv_v4_split<")
     assert _abi.describe(lib, 4096, 4096, 16, reuse_weights=1)["kernel"].startswith(
-        "void dk::gemv_reuse<")
+        "void dk::gemv_reuse_lds<16, 1, true>")
+    assert _abi.describe(lib, 28672, 8192, 4, reuse_weights=1)["kernel"].startswith(
+        "void dk::gemv_reuse<8, 2, 2, true>")
     assert _abi.describe(lib, 4096, 4096, 2, reuse_weights=1)["kernel"].startswith(
         "void dk::gemv_v5_lds<") and ", 15, " in _abi.describe(lib, 4096, 4096, 2,
                                                               reuse_weights=1)["kernel"]
     # With the optional workspace the reuse path splits K; without it, not.
-    assert "gemv_reuse_split<" in _abi.describe(lib, 2048, 16384, 16, reuse_weights=1)["kernel"]
-    assert "gemv_reuse<" in _abi.describe(lib, 2048, 16384, 16, workspace_bytes=0,
-                                          reuse_weights=1)["kernel"]
+    assert "gemv_reuse_split<" in _abi.describe(lib, 1024, 16384, 16, reuse_weights=1)["kernel"]
+    assert "gemv_reuse_lds<" in _abi.describe(lib, 1024, 16384, 16, workspace_bytes=0,
+                                              reuse_weights=1)["kernel"]
     assert _abi.describe(lib, 4096, 4096, 1, version=1, warps_per_row=4)["kernel"].startswith(
         "dk::gemv_v1_multiwave(")
     # Invalid calls fail as dk_w4a16_gemv would.
@@ -166,25 +168,23 @@ def test_describe_names_the_dispatched_kernel(lib):
 
 
 def test_reuse_split_workspace_size(lib):
-    # The reuse path's split-K tiles (K > 8192 with M <= 2048 or with M <=
-    # 4096 and 32 or more batch rows; K = 8192 with M of 2049-4096 and 32 or
-    # more batch rows): 8-byte tickets per 32 rows x 16 batch rows, padded
-    # to 256 bytes, then fp32 partials [4, B, M]. Zero where the path
-    # streams or does not split.
+    # The reuse path's split-K tiles (rows longer than 8192 weights at
+    # M <= 1024, where the tiles run: 12 or more batch rows, 33 or more at
+    # M <= 512): 8-byte tickets per 32 rows x 16 batch rows, padded to 256
+    # bytes, then fp32 partials [4, B, M]. Zero where the path streams or
+    # does not split.
     cfg = _abi.default_config(lib, reuse_weights=1)
     ws = lambda m, k, b: lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(cfg))
-    assert ws(4096, 8192, 32) == 2048 + 4 * 32 * 4096 * 4  # 128 x 2 tickets
-    assert ws(2048, 11008, 17) == 1024 + 4 * 17 * 2048 * 4
-    assert ws(3000, 8192, 32) == 1536 + 4 * 32 * 3000 * 4  # 188 tickets -> 1504 -> 1536 bytes
-    assert ws(4096, 8192, 16) == 0     # single-pass tiles
-    assert ws(6144, 8192, 32) == 0     # single-pass tiles
-    assert ws(4096, 4096, 32) == 0     # short rows: single-pass tiles
-    assert ws(4096, 4096, 4) == 0      # short rows: single-pass tiles
-    assert ws(2048, 8192, 4) == 0      # streaming kernel
-    assert ws(2048, 8192, 16) == 0     # rows of 8192 at M <= 2048: single-pass tiles
-    assert ws(2048, 8320, 16) == 512 + 4 * 16 * 2048 * 4  # 64 tickets
-    assert ws(1024, 8192, 16) == 0     # streaming kernel at small M
-    assert ws(8192, 8192, 32) == 0     # two tiles per wave, no split
+    assert ws(1024, 16384, 16) == 256 + 4 * 16 * 1024 * 4   # 32 tickets
+    assert ws(1000, 8320, 12) == 256 + 4 * 12 * 1000 * 4
+    assert ws(600, 65536, 33) == 512 + 4 * 33 * 600 * 4     # 19 x 3 tickets -> 456 -> 512 bytes
+    assert ws(512, 28672, 33) == 512 + 4 * 33 * 512 * 4
+    assert ws(512, 28672, 32) == 0     # streaming kernel
+    assert ws(1024, 16384, 11) == 0    # streaming kernel
+    assert ws(1024, 8192, 16) == 0     # rows of 8192: single-pass tiles
+    assert ws(2048, 16384, 16) == 0    # single-pass tiles from 1025 rows
+    assert ws(4096, 11008, 64) == 0
+    assert ws(4096, 4096, 4) == 0
 
 
 def test_probe_argument_checks(lib):

@@ -134,20 +134,20 @@ def test_batch_sweep_c3(batch):
 
 
 def test_reuse_small_batches_run_the_streaming_kernel():
-    # Up to two batch rows, three below 2^27 weights (but not with rows of
-    # 4097-8191 weights at M >= 3072), four below M = 3072, up
-    # to 8 with M <= 2048, 16 with M <= 1024, 32 with M <= 512 and any with
-    # M <= 128: the reuse path runs the streaming kernel with its batch tiles
-    # (stamp 15), so its output is the v5 output bit for bit. Five rows with
-    # M > 2048 take the MFMA tile kernel, which still meets the oracle's
-    # bound.
-    from decode_kernel import _cuda
+    # Up to two batch rows; three below 2^27 weights with rows shorter than
+    # 8192 weights (but not rows of 4097-8191 weights at M >= 3072); four
+    # below M = 3072; up to 8 at M <= 2048 on rows shorter than 8192
+    # weights; 11 at M <= 1024, 32 at M <= 512 and any at M <= 128: the
+    # reuse path runs the streaming kernel with its batch tiles (stamp 15),
+    # so its output is the v5 output bit for bit. Five rows with M > 2048
+    # take the MFMA tile kernel, which still meets the oracle's bound.
+    from decode_kernel import _abi, _cuda
 
     for (m, k, b) in [(4096, 4096, 1), (4096, 4096, 2), (11008, 4096, 2), (300, 8192, 1),
                       (512, 8192, 2), (8192, 4096, 3), (28672, 8192, 2), (4096, 4096, 3),
-                      (2000, 8192, 4), (512, 8320, 3), (8192, 8192, 3), (1024, 11008, 6),
+                      (2000, 8192, 4), (512, 8320, 3), (1024, 11008, 6), (1024, 4224, 11),
                       (3000, 8192, 4),
-                      (2048, 4224, 8), (40, 197632, 3), (1000, 4224, 16), (500, 4224, 32),
+                      (2048, 4224, 8), (40, 197632, 3), (500, 4224, 32),
                       (100, 8192, 64)]:
         w, x = oracle.make_case(m, k, b, seed=m + k + b)
         _, _, pd, sd, xd = _upload(w, x)
@@ -160,6 +160,12 @@ def test_reuse_small_batches_run_the_streaming_kernel():
     y = _gemv(pd, sd, xd, reuse_weights=True)
     assert int(_cuda.last_kernel_stamp()) == 15
     _check_against_oracle(y, oracle.linear_f64(x, packed, scales), "reuse 3000x8320 B=5")
+    # Where the LDS-staged tiles beat the streaming kernel at small batches:
+    # three rows of 8192 weights or more, 12 rows at M <= 1024, five rows of
+    # 8192 at M <= 2048.
+    lib = _abi.load()
+    for (m, k, b) in [(8192, 8192, 3), (4096, 11008, 3), (1000, 4224, 12), (2048, 8192, 5)]:
+        assert "gemv_reuse_lds<" in _abi.describe(lib, m, k, b, reuse_weights=1)["kernel"], (m, k, b)
 
 
 @pytest.mark.parametrize("m,k,b", [(1100, 65536, 9), (4096, 4096, 8), (4096, 11008, 5),
@@ -167,14 +173,16 @@ def test_reuse_small_batches_run_the_streaming_kernel():
                                    (8216, 4224, 6), (4096, 4096, 16), (3072, 8192, 4),
                                    (8192, 16384, 3), (2048, 8192, 16), (6144, 8192, 16),
                                    (5000, 4224, 5), (5120, 5120, 3), (3000, 8320, 16),
-                                   (4500, 5248, 12)])
+                                   (4500, 5248, 12), (12000, 8320, 5), (9000, 4224, 33),
+                                   (6000, 4224, 40), (3500, 6144, 33), (1000, 4096, 12)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
-    # The single-pass MFMA tile kernel in each of its shapes (one tile per
-    # wave with 16 or 8 waves per tile; two tiles per wave from M = 8192, the
-    # second of them partly past M at M = 8216; the split form is
-    # test_reuse_split_tiles), three and four batch rows on the shapes that
-    # take the tiles there, long rows of 512 groups, K = 4096 and K > 4096,
-    # one and two tiles of batch rows: a
+    # The single-pass MFMA tile kernels in each of their shapes (operands
+    # staged in LDS: one tile per wave with 16 or 8 waves, two tiles per wave
+    # with 8 or 4 waves, the second tile partly past M at M = 8216; operands
+    # loaded directly: M > 8192 with rows longer than 4096 weights up to 8
+    # batch rows; the split form is test_reuse_split_tiles), three and four
+    # batch rows on the shapes that take the tiles there, long rows of 512
+    # groups, K = 4096 and K > 4096, one and two tiles of batch rows: a
     # one-hot batch row selects single scaled weights bit for bit, scaling x
     # by 2 or -1 scales y exactly (2 up to fp16 subnormal rounding), and rows
     # of a batch do not mix.
@@ -207,12 +215,12 @@ def test_reuse_tile_kernel_exact_properties(m, k, b):
 
 
 @pytest.mark.parametrize("m,k,b", [(4096, 4096, 8), (8192, 8192, 4), (6144, 8192, 16),
-                                   (28672, 1024, 5)])
+                                   (28672, 1024, 5), (28672, 8192, 4), (2048, 8192, 16),
+                                   (9000, 4096, 20)])
 def test_reuse_tiles_scale_alignment(m, k, b):
     # With 4-byte aligned scales and an even number of groups per row the
-    # tiles load the scales of two groups at once (up to 8 batch rows, and
-    # between 4096 and 8192 rows); scales that are only 2-byte aligned take
-    # 2-byte loads. Both give the same bits.
+    # tiles load the scales of two groups at once; scales that are only
+    # 2-byte aligned take 2-byte loads. Both give the same bits.
     from decode_kernel import _abi
 
     lib = _abi.load()
@@ -236,13 +244,13 @@ def test_reuse_tiles_scale_alignment(m, k, b):
     _check_against_oracle(y, oracle.linear_f64(x, packed, scales), f"reuse {m}x{k} B={b}")
 
 
-@pytest.mark.parametrize("m,k,b", [(4096, 8192, 32), (3000, 8320, 33), (2000, 12416, 17),
-                                   (2048, 8320, 9), (600, 65536, 17)])
+@pytest.mark.parametrize("m,k,b", [(1024, 16384, 16), (1000, 8320, 12), (777, 12416, 17),
+                                   (512, 28672, 33), (600, 65536, 17)])
 def test_reuse_split_tiles(m, k, b):
-    # The MFMA tiles with K split over four workgroups (reuse path, K > 8192
-    # with M <= 2048 or 32 or more batch rows, K = 8192 with M of 2049-4096
-    # and 32 or more batch rows, a workspace from the caller;
-    # M = 600 and 3000 end in partial sets of 32 rows): against the oracle,
+    # The MFMA tiles with K split over four workgroups (reuse path, rows
+    # longer than 8192 weights at M <= 1024 where the tiles run, a workspace
+    # from the caller; M = 600, 777 and 1000 end in partial sets of 32
+    # rows): against the oracle,
     # bit-identical on repeated calls and
     # with workspaces full of different garbage (each ticket carries the
     # call's generation, so no clearing is needed), and the same bits through
@@ -251,9 +259,10 @@ def test_reuse_split_tiles(m, k, b):
     from decode_kernel import _abi
 
     lib = _abi.load()
-    # |y| grows as sqrt(K): smaller weights at K = 65536 keep one fp16 step
-    # of y inside the absolute gate.
-    w_std = 0.05 if k <= 28672 else 0.005
+    # |y| grows as sqrt(K): smaller weights from K = 28672 keep one fp16 step
+    # of y inside the absolute gate (at W ~ N(0, 0.05) and K = 28672, |y|
+    # reaches ~30 over 33 x 512 outputs, where one fp16 step is 0.03).
+    w_std = 0.05 if k <= 16384 else 0.02 if k <= 28672 else 0.005
     w, x = oracle.make_case(m, k, b, seed=m + b, w_std=w_std)
     packed, scales, pd, sd, xd = _upload(w, x)
     y_ref = oracle.linear_f64(x, packed, scales)
@@ -288,7 +297,7 @@ def test_reuse_split_graph_replays():
     # the last workgroup of each set resets its ticket to that generation
     # with a zero count. Every replay, with eager calls between them, gives
     # the eager result.
-    m, k, b = 2048, 8192, 16
+    m, k, b = 1024, 16384, 16
     w, x = oracle.make_case(m, k, b, seed=5, w_std=0.05)
     _, _, pd, sd, xd = _upload(w, x)
     y_eager = _gemv(pd, sd, xd, reuse_weights=True)

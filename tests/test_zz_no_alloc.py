@@ -60,7 +60,7 @@ def _tight(y, y_ref, label):
 # (config, first call (M, K, B), second, smaller call); the reuse path's
 # split-K tiles take the scratch, the others none.
 PATHS = [
-    (dict(version=5, reuse_weights=1), (2048, 16384, 16), (1024, 12416, 17)),
+    (dict(version=5, reuse_weights=1), (1024, 16384, 16), (800, 9216, 13)),
     (dict(version=5, reuse_weights=1), (4096, 11008, 64), (2048, 9216, 33)),
     (dict(version=4, split_k=4), (4096, 11008, 1), (1000, 1024, 3)),
     (dict(version=5), (4096, 4096, 1), (333, 640, 2)),
@@ -85,11 +85,11 @@ def test_noalloc_matches_the_workspace_entry(cfg, first, second):
 
 
 def test_noalloc_refuses_a_workspace_beyond_the_scratch():
-    # The reuse path's split-K tiles at B = 128 need more than the scratch:
+    # The reuse path's split-K tiles at B = 640 need more than the scratch:
     # refused on the host, before anything is launched (small stand-in
     # buffers), and y is untouched.
     abi, lib = _lib()
-    m, k, b = 4096, 11008, 128
+    m, k, b = 1024, 16384, 640
     c = abi.default_config(lib, reuse_weights=1)
     assert lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(c)) > abi.DK_NOALLOC_SCRATCH_BYTES
     pd = torch.zeros(16, dtype=torch.int32, device="cuda")
@@ -105,7 +105,7 @@ def test_noalloc_refuses_a_workspace_beyond_the_scratch():
 def test_noalloc_graph_replays_with_eager_calls_between():
     abi, lib = _lib()
     c = abi.default_config(lib, reuse_weights=1)
-    m, k, b = 2048, 16384, 16
+    m, k, b = 1024, 16384, 16
     pd, sd, xd, y_ref = _case(m, k, b, seed=4)
     assert lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(c)) > 0  # uses the scratch
     p2, s2, x2, y2_ref = _case(1024, 12416, 17, seed=5)
