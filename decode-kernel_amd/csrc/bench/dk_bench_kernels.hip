@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 
 #include "dk_kernels.hpp"
+#include "dk_mlp.hpp"
 
 #define DKB_API extern "C" __attribute__((visibility("default")))
 
@@ -550,6 +551,33 @@ DKB_API int dkb_reuse(int kind, int KS, int RT, int SG, int pairs, const void* p
   DKB_R1(8, 2, true) DKB_R1(8, 2, false) DKB_R1(4, 1, true) DKB_R1(4, 2, true)
 #undef DKB_R1
 #undef DKB_R0
+  return 3;
+}
+
+// The fused gate/up tile kernels at any instantiated shape (B rows in tiles
+// of 16): kind 0 gate_up_silu_tiles<KS, 2, pairs> (MFMA operands loaded
+// directly), kind 1 gate_up_silu_tiles_lds<KS, pairs> (both operands staged
+// in LDS). Returns 3 (nothing launched) for a shape not instantiated here.
+DKB_API int dkb_gate_up(int kind, int KS, int pairs, const void* gate, const void* gate_scales,
+                        const void* up, const void* up_scales, const void* x, void* h, int I, int H,
+                        int B, hipStream_t stream) {
+  const auto* g = static_cast<const uint4*>(gate);
+  const auto* gs = static_cast<const uint16_t*>(gate_scales);
+  const auto* u = static_cast<const uint4*>(up);
+  const auto* us = static_cast<const uint16_t*>(up_scales);
+  const auto* xx = static_cast<const uint4*>(x);
+  auto* hh = static_cast<uint16_t*>(h);
+  const dim3 grid((I + 15) / 16, (B + 15) / 16);
+#define DKB_GU(kd, ks, pr, kernel)                                                              \
+  if (kind == kd && KS == ks && pairs == (int)pr) {                                            \
+    hipLaunchKernelGGL(kernel, grid, dim3(ks * 64), 0, stream, g, gs, u, us, xx, I, H, B, hh); \
+    return launch_error("gate/up tiles");                                                      \
+  }
+  DKB_GU(0, 8, true, (dk::gate_up_silu_tiles<8, 2, true>))
+  DKB_GU(0, 8, false, (dk::gate_up_silu_tiles<8, 2, false>))
+  DKB_GU(1, 8, true, (dk::gate_up_silu_tiles_lds<8, true>))
+  DKB_GU(1, 4, true, (dk::gate_up_silu_tiles_lds<4, true>))
+#undef DKB_GU
   return 3;
 }
 

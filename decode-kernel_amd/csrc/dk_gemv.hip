@@ -429,10 +429,12 @@ int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x
 //   I = 28672, H = 8192: 50.73 (59.49)   52.05 (70.56)   52.96 (108.97)  59.11 (129.76)  76.80 (256.50)
 //   I = 2752,  H = 4096: 6.62 (7.03)     6.66 (8.34)     6.75 (11.62)    7.20 (15.39)    8.26 (22.66)
 //   I = 1376,  H = 4096: 6.37 (4.66*)    6.42 (5.28*)    6.42 (5.53*)
-// Two batch rows stream everywhere (I = 11008: 13.38 against 12.56).
+// Two batch rows stream everywhere (I = 11008: 13.38 against 12.56); three
+// take the tiles at I = 3584, H = 8192 as well (9.48 against 11.19 for the
+// streaming kernel in a later sweep).
 bool gate_up_tiles(int I, int H, int B) {
-  return !(B <= 2 || (B == 3 && I <= 4096 && H > 4096) || (B <= 8 && I <= 2048) ||
-           (B <= 16 && I <= 1024));
+  (void)H;
+  return !(B <= 2 || (B <= 8 && I <= 2048) || (B <= 16 && I <= 1024));
 }
 
 // Fused gate/up, R rows of each matrix per wave, on the LDS stage loop (U
@@ -482,9 +484,32 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
                    const uint16_t* us, const uint4* x, uint16_t* h, int I, int H, int B) {
   if (gate_up_tiles(I, H, B)) {
     const dim3 grid((I + 15) / 16, (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
+    const bool pairs = (H / DK_GROUP_SIZE) % 2 == 0 && aligned(gs, 4) && aligned(us, 4);
+    // From 8 batch rows, both tiles' operands staged in LDS (as the GEMV's
+    // gemv_reuse_lds), 8 waves up to I = 4096 and 16 batch rows, else 4
+    // (us, against the tiles that load the operands directly):
+    //                        B = 8           B = 16          B = 32
+    //   I = 11008, H = 4096: 13.91 (14.50)   16.05 (19.06)   27.97 (34.47)
+    //   I = 14336, H = 4096: 17.98 (17.72)   20.36 (24.09)   34.24 (43.83)
+    //   I = 3584,  H = 8192: 10.66 (11.70)   11.91 (13.97)   19.53 (24.65)
+    //   I = 2752,  H = 4096: 6.64 (7.01)     7.08 (8.50)     11.40 (13.78)
+    //   I = 28672, H = 8192: 57.23 (59.11)   66.36 (80.54)   127.57 (158.15)
+    // Up to 4 batch rows the direct tiles stay (I = 11008, H = 4096, B = 4:
+    // 12.25 against 12.57; I = 28672, B = 3: 47.68 against 50.50).
+    if (B >= 8) {
+      if (I <= 4096 && B <= 16)
+        return pairs ? L("gate/up launch", dk::gate_up_silu_tiles_lds<8, true>, grid, dim3(8 * 64),
+                         0, g, gs, u, us, x, I, H, B, h)
+                     : L("gate/up launch", dk::gate_up_silu_tiles_lds<8, false>, grid,
+                         dim3(8 * 64), 0, g, gs, u, us, x, I, H, B, h);
+      return pairs ? L("gate/up launch", dk::gate_up_silu_tiles_lds<4, true>, grid, dim3(4 * 64), 0,
+                       g, gs, u, us, x, I, H, B, h)
+                   : L("gate/up launch", dk::gate_up_silu_tiles_lds<4, false>, grid, dim3(4 * 64),
+                       0, g, gs, u, us, x, I, H, B, h);
+    }
     // Paired scale loads up to 8 batch rows, as for the GEMV: I = 11008,
-    // H = 4096, B = 4: 12.28 against 13.67 us; B = 16: 18.95 against 18.56.
-    if (B <= 8 && (H / DK_GROUP_SIZE) % 2 == 0 && aligned(gs, 4) && aligned(us, 4))
+    // H = 4096, B = 4: 12.28 against 13.67 us.
+    if (pairs)
       return L("gate/up launch", dk::gate_up_silu_tiles<8, 2, true>, grid, dim3(8 * 64), 0, g, gs, u,
                us, x, I, H, B, h);
     return L("gate/up launch", dk::gate_up_silu_tiles<8, 2, false>, grid, dim3(8 * 64), 0, g, gs, u,

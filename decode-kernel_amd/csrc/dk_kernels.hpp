@@ -863,38 +863,22 @@ struct ReuseDmaLds {
   uint4 w[KS][RT * 16 * 8];  // per wave: 16 RT rows x 8 chunks (two groups)
 };
 
+// The block loop of the LDS-staged tiles: tile t's weights and scales
+// through descriptors rw[t], rs[t] (rows 0..15 relative to them, G groups
+// per row), x of batch rows bt0 .. bt0 + 15 (those below B) through rx with
+// rows K * 2 bytes apart. acc[t] is this lane's part of tile t's fp32 16x16
+// result over the wave's blocks (groups 2 wave, 2 wave + 1, then every 2 KS).
 template <int KS, int RT, bool kPairs>
-__global__ __launch_bounds__(KS * 64) void gemv_reuse_lds(const uint4* __restrict__ packed,
-                                                          const uint16_t* __restrict__ scales,
-                                                          const uint4* __restrict__ x4,
-                                                          uint16_t* __restrict__ y, int M, int K,
-                                                          int B) {
-  static_assert(KS >= RT, "wave t sums tile t");
-  write_stamp(DK_STAMP_REUSE);
-  __shared__ ReuseDmaLds<KS, RT> lds;
-  const int G = K >> 7;
+__device__ __forceinline__ void reuse_lds_loop(f4_t (&acc)[RT], uint4* xbuf, uint4* wbuf,
+                                               const __amdgpu_buffer_rsrc_t (&rw)[RT],
+                                               const __amdgpu_buffer_rsrc_t (&rs)[RT],
+                                               __amdgpu_buffer_rsrc_t rx, int bt0, int B, int K,
+                                               int G, int lane, int wave) {
   const int nck = K >> 5;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int row0 = blockIdx.x * 16 * RT;
-  const int bt0 = blockIdx.y * kReuseBatch;
-  const int b = bt0 + (lane & 15);  // this lane's batch column
   const int kq = lane >> 4;
   const int r_lane = lane & 15;
-  __amdgpu_buffer_rsrc_t rw[RT], rs[RT];
-#pragma unroll
-  for (int t = 0; t < RT; ++t) {
-    const int rows = __builtin_amdgcn_readfirstlane(max(0, min(16, M - row0 - 16 * t)));
-    const int rbase = rows > 0 ? row0 + 16 * t : 0;
-    rw[t] = buffer_rsrc(packed + (size_t)rbase * nck, (uint32_t)(rows * (K / 2)));
-    rs[t] = buffer_rsrc(scales + (size_t)rbase * G, (uint32_t)(rows * G * 2));
-  }
-  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
   // x loads (two batch rows each) with a batch row below B (wave-uniform).
   const int nxl = min(8, (max(0, min(16, B - bt0)) + 1) / 2);
-  uint4* xbuf = lds.x[wave];
-  uint4* wbuf = lds.w[wave];
-  f4_t acc[RT];
 #pragma unroll
   for (int t = 0; t < RT; ++t) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
   for (int g0 = 2 * wave; g0 < G; g0 += 2 * KS) {
@@ -977,21 +961,65 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_lds(const uint4* __restric
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
   }
-  // Partials over the wave's own x buffer (no other wave reads it before the
-  // barrier), then tile t's KS partials added in wave order by wave t.
-  float* part = reinterpret_cast<float*>(xbuf);
+}
+
+// Partials of the LDS-staged tiles over each wave's own x buffer (no other
+// wave reads it before the barrier that follows), and tile t's KS partials
+// added in wave order (after that barrier).
+template <int KS, int RT>
+__device__ __forceinline__ void reuse_lds_publish(ReuseDmaLds<KS, RT>& lds, const f4_t (&acc)[RT],
+                                                  int wave, int lane) {
+  float* part = reinterpret_cast<float*>(lds.x[wave]);
 #pragma unroll
   for (int t = 0; t < RT; ++t)
 #pragma unroll
     for (int v = 0; v < 4; ++v) part[(t * 64 + lane) * 4 + v] = acc[t][v];
+}
+
+template <int KS, int RT>
+__device__ __forceinline__ f4_t reuse_lds_sum(const ReuseDmaLds<KS, RT>& lds, int t, int lane) {
+  f4_t sum = {0.f, 0.f, 0.f, 0.f};
+  for (int w2 = 0; w2 < KS; ++w2) {
+    const float* part = reinterpret_cast<const float*>(lds.x[w2]);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) sum[v] += part[(t * 64 + lane) * 4 + v];
+  }
+  return sum;
+}
+
+template <int KS, int RT, bool kPairs>
+__global__ __launch_bounds__(KS * 64) void gemv_reuse_lds(const uint4* __restrict__ packed,
+                                                          const uint16_t* __restrict__ scales,
+                                                          const uint4* __restrict__ x4,
+                                                          uint16_t* __restrict__ y, int M, int K,
+                                                          int B) {
+  static_assert(KS >= RT, "wave t sums tile t");
+  write_stamp(DK_STAMP_REUSE);
+  __shared__ ReuseDmaLds<KS, RT> lds;
+  const int G = K >> 7;
+  const int nck = K >> 5;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = blockIdx.x * 16 * RT;
+  const int bt0 = blockIdx.y * kReuseBatch;
+  const int b = bt0 + (lane & 15);  // this lane's batch column
+  const int kq = lane >> 4;
+  __amdgpu_buffer_rsrc_t rw[RT], rs[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const int rows = __builtin_amdgcn_readfirstlane(max(0, min(16, M - row0 - 16 * t)));
+    const int rbase = rows > 0 ? row0 + 16 * t : 0;
+    rw[t] = buffer_rsrc(packed + (size_t)rbase * nck, (uint32_t)(rows * (K / 2)));
+    rs[t] = buffer_rsrc(scales + (size_t)rbase * G, (uint32_t)(rows * G * 2));
+  }
+  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
+  f4_t acc[RT];
+  reuse_lds_loop<KS, RT, kPairs>(acc, lds.x[wave], lds.w[wave], rw, rs, rx, bt0, B, K, G, lane,
+                                 wave);
+  reuse_lds_publish(lds, acc, wave, lane);
   __syncthreads();
   if (wave < RT) {
-    f4_t sum = {0.f, 0.f, 0.f, 0.f};
-    for (int w2 = 0; w2 < KS; ++w2) {
-      const float* pp = reinterpret_cast<const float*>(lds.x[w2]);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) sum[v] += pp[(wave * 64 + lane) * 4 + v];
-    }
+    const f4_t sum = reuse_lds_sum(lds, wave, lane);
     if (b < B) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {

@@ -118,4 +118,48 @@ __global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles(
   }
 }
 
+// The same with both tiles' operands staged in LDS by the buffer-load-to-LDS
+// path (the GEMV's gemv_reuse_lds): tile 0 is 16 rows of Wg, tile 1 the
+// same rows of Wu, one staged block of x serving both.
+template <int KS, bool kPairs>
+__global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles_lds(
+    const uint4* __restrict__ gate, const uint16_t* __restrict__ gate_scales,
+    const uint4* __restrict__ up, const uint16_t* __restrict__ up_scales,
+    const uint4* __restrict__ x4, int I, int H, int B, uint16_t* __restrict__ h) {
+  write_stamp(kStampGateUp);
+  __shared__ ReuseDmaLds<KS, 2> lds;
+  const int G = H >> 7;
+  const int nck = H >> 5;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = blockIdx.x * 16;
+  const int bt0 = blockIdx.y * kReuseBatch;
+  const int b = bt0 + (lane & 15);  // this lane's batch column
+  const int kq = lane >> 4;
+  const int rows = __builtin_amdgcn_readfirstlane(min(16, I - row0));
+  const __amdgpu_buffer_rsrc_t rw[2] = {
+      buffer_rsrc(gate + (size_t)row0 * nck, (uint32_t)(rows * (H / 2))),
+      buffer_rsrc(up + (size_t)row0 * nck, (uint32_t)(rows * (H / 2)))};
+  const __amdgpu_buffer_rsrc_t rs[2] = {
+      buffer_rsrc(gate_scales + (size_t)row0 * G, (uint32_t)(rows * G * 2)),
+      buffer_rsrc(up_scales + (size_t)row0 * G, (uint32_t)(rows * G * 2))};
+  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * H * 2));
+  f4_t acc[2];
+  reuse_lds_loop<KS, 2, kPairs>(acc, lds.x[wave], lds.w[wave], rw, rs, rx, bt0, B, H, G, lane,
+                                wave);
+  reuse_lds_publish(lds, acc, wave, lane);
+  __syncthreads();
+  if (wave == 0) {
+    const f4_t g = reuse_lds_sum(lds, 0, lane);
+    const f4_t u = reuse_lds_sum(lds, 1, lane);
+    if (b < B) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int orow = row0 + 4 * kq + v;
+        if (orow < I) h[(size_t)b * I + orow] = f2h(silu_f32(g[v]) * u[v]);
+      }
+    }
+  }
+}
+
 }  // namespace dk

@@ -20,6 +20,7 @@ _SIGNATURES = {
                     _P]),
     "dkb_v4s": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P]),
     "dkb_reuse": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P]),
+    "dkb_gate_up": (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "dkb_timestamp": (_I, [_P, _I, _P]),
     "dkb_wall_clock_khz": (_I, []),
 }
@@ -159,4 +160,17 @@ def reuse(kind: int, ks: int, rt: int, sg: int, pairs: bool, packed, scales, x, 
                           x.data_ptr(), y.data_ptr(), m, k, b, stream_handle())
     if rc not in (0, 3):
         raise RuntimeError(f"reuse kind {kind} KS{ks} RT{rt} SG{sg}: status {rc}")
+    return rc
+
+
+def gate_up(kind: int, ks: int, pairs: bool, gp, gs, up, us, x, h) -> int:
+    """The fused gate/up tile kernels: kind 0 gate_up_silu_tiles<KS, 2,
+    pairs>, kind 1 gate_up_silu_tiles_lds<KS, pairs>. Returns 3 (nothing
+    launched) for a shape not instantiated in the measurement library."""
+    i, hd = gp.shape[0], gp.shape[1] * 8
+    b = x.shape[0]
+    rc = load().dkb_gate_up(kind, ks, int(pairs), gp.data_ptr(), gs.data_ptr(), up.data_ptr(),
+                            us.data_ptr(), x.data_ptr(), h.data_ptr(), i, hd, b, stream_handle())
+    if rc not in (0, 3):
+        raise RuntimeError(f"gate/up kind {kind} KS{ks}: status {rc}")
     return rc

@@ -1,6 +1,6 @@
 """Launch-shape and kernel-variant sweeps behind the routing choices.
 
-    python -m dk_bench.levers floor|c0|v4|split|reuse|all [--steps 300] [--out PATH]
+    python -m dk_bench.levers floor|c0|v4|split|reuse|mlp|all [--steps 300] [--out PATH]
     (from decode-kernel_amd/, after build_ext.py)
 
   floor  read-probe launch shapes at the algorithmic bytes of c0, c1 and c2
@@ -19,7 +19,9 @@
   reuse  the weight-reuse tile kernels (operands loaded directly, or staged
          in LDS by the buffer-load-to-LDS path) at 3-32 batch rows over the
          shapes the reuse path's launch rules were set on, against the
-         product's reuse path.
+         product's reuse path;
+  mlp    the fused gate/up tile kernels (both forms) at 3-32 batch rows on
+         Llama MLP shapes, against the product's fused gate/up.
 Every variant that computes y is checked against the product's v5 output
 (bit-exact where the summation order is the same, else within 1e-3 plus one
 fp16 ulp) before it is timed. Timing as in bench.py: HIP graphs of `steps`
@@ -267,9 +269,62 @@ def sweep_reuse(flush, steps: int) -> dict:
     return out
 
 
+MLP_PROBLEMS = [(11008, 4096), (3584, 8192), (2752, 4096), (14336, 4096), (28672, 8192)]
+MLP_BATCHES = (3, 4, 8, 16, 32)
+MLP_SHAPES = [(0, 8, True), (1, 8, True), (1, 4, True)]
+
+
+def sweep_mlp(flush, steps: int) -> dict:
+    """Fused gate/up tile kernels against the product's fused gate/up."""
+    from decode_kernel import gate_up_silu
+
+    from . import benchlib
+    from .ablation import gpu_case
+
+    out = {}
+    for i_dim, h_dim in MLP_PROBLEMS:
+        gp, gs, _ = gpu_case(i_dim, h_dim, seed=5000 + i_dim)
+        upk, us, _ = gpu_case(i_dim, h_dim, seed=6000 + i_dim)
+        # Copies of both matrices totalling > 640 MB, so every step reads cold weights.
+        per = (gp.numel() * 4 + gs.numel() * 2) * 2
+        n = max(2, -(-(640 << 20) // per))
+        gps = [gp.clone() for _ in range(n)]
+        gss = [gs.clone() for _ in range(n)]
+        ups = [upk.clone() for _ in range(n)]
+        uss = [us.clone() for _ in range(n)]
+        gen = torch.Generator(device="cuda").manual_seed(i_dim + h_dim)
+        xall = torch.randn(max(MLP_BATCHES), h_dim, device="cuda", generator=gen).half()
+        for b in MLP_BATCHES:
+            x = xall[:b].contiguous()
+            name = f"i{i_dim}_h{h_dim}_b{b}"
+            h_prod = gate_up_silu(x, gps[0], gss[0], ups[0], uss[0])
+            hbuf = torch.empty_like(h_prod)
+            rows = {"product": _time(lambda j: gate_up_silu(x, gps[j % n], gss[j % n], ups[j % n],
+                                                            uss[j % n]), steps, flush)}
+            for shape in MLP_SHAPES:
+                kind, ks, pairs = shape
+                hbuf.fill_(float("nan"))
+                if benchlib.gate_up(kind, ks, pairs, gps[0], gss[0], ups[0], uss[0], x, hbuf) == 3:
+                    raise RuntimeError(f"gate/up {shape} is not instantiated")
+                torch.cuda.synchronize()
+                if not _close(hbuf, h_prod):
+                    raise RuntimeError(f"gate/up {shape} differs from the product at {name}")
+                key = "{}_KS{}".format("lds" if kind else "tiles", ks)
+                rows[key] = _time(lambda j: benchlib.gate_up(kind, ks, pairs, gps[j % n], gss[j % n],
+                                                             ups[j % n], uss[j % n], x, hbuf),
+                                  steps, flush)
+            best = min((v, kk) for kk, v in rows.items())
+            print(f"mlp {name}: product {rows['product']:.3f}; best {best[1]} {best[0]:.3f}",
+                  flush=True)
+            out[name] = rows
+        del gps, gss, ups, uss, gp, gs, upk, us, xall
+        torch.cuda.empty_cache()
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("what", choices=["floor", "c0", "v4", "split", "reuse", "all"])
+    ap.add_argument("what", choices=["floor", "c0", "v4", "split", "reuse", "mlp", "all"])
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--out", type=Path, default=None)
     args = ap.parse_args()
@@ -289,6 +344,8 @@ def main() -> None:
         res["split"] = sweep_split(flush, args.steps)
     if args.what in ("reuse", "all"):
         res["reuse"] = sweep_reuse(flush, args.steps)
+    if args.what in ("mlp", "all"):
+        res["mlp"] = sweep_mlp(flush, args.steps)
     if args.out:
         args.out.parent.mkdir(parents=True, exist_ok=True)
         args.out.write_text(json.dumps(res, indent=2) + "\n")

@@ -57,7 +57,7 @@ def _check_tight(got: np.ndarray, ref: np.ndarray, label: str):
 @pytest.mark.parametrize("i,h,b", [
     (256, 128, 1), (256, 128, 3), (384, 640, 2), (1000, 256, 5), (11008, 4096, 1),
     (11008, 4096, 4), (3584, 8192, 1), (3584, 8192, 2), (11008, 4096, 8), (3584, 8192, 16),
-    (11008, 4096, 16), (11008, 2048, 16),
+    (11008, 4096, 16), (11008, 2048, 16), (3584, 8192, 33), (5000, 4224, 20),
 ])
 def test_mlp_step_matches_oracle(i, h, b):
     from decode_kernel import _cuda, gate_up_silu, mlp_decode
@@ -101,8 +101,9 @@ GATE_UP_SHAPES = [(1000, 4224), (2000, 8320), (3000, 4224), (3000, 8320), (5000,
 @pytest.mark.parametrize("i,h", GATE_UP_SHAPES)
 def test_gate_up_every_dispatch_class(i, h):
     # Batches 1-8 cover every streaming tile size (one row, and tiles of 2, 3
-    # and 4 rows, the last one partly empty at B = 5 and 7); from 5 rows at
-    # I > 2048, and from 9 rows at I > 1024, the MFMA tiles run instead. Each
+    # and 4 rows, the last one partly empty at B = 5 and 7); from 3 rows at
+    # I > 2048, and from 9 rows at I > 1024, the MFMA tiles run instead (with
+    # both operands staged in LDS from 8 rows). Each
     # output row depends on its own activation row only, so the first b rows
     # of one 16-row case give the reference for every b.
     from decode_kernel import _cuda, gate_up_silu
@@ -236,11 +237,11 @@ def test_c_abi_mlp_matches_extension():
     assert torch.equal(hk, ws.view(b, i))
 
 
-@pytest.mark.parametrize("i,h,b", [(11008, 4096, 4), (3584, 8192, 8)])
+@pytest.mark.parametrize("i,h,b", [(11008, 4096, 4), (3584, 8192, 8), (11008, 4096, 16)])
 def test_gate_up_tiles_scale_alignment(i, h, b):
-    # The gate/up tiles load two groups' scales at once up to 8 batch rows
-    # when both scale arrays are 4-byte aligned; 2-byte aligned scales take
-    # 2-byte loads and give the same bits.
+    # The gate/up tiles (both forms) load two groups' scales at once when both
+    # scale arrays are 4-byte aligned; 2-byte aligned scales take 2-byte
+    # loads and give the same bits.
     from decode_kernel import _abi
 
     lib = _abi.load()

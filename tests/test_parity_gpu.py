@@ -174,7 +174,8 @@ def test_reuse_small_batches_run_the_streaming_kernel():
                                    (8192, 16384, 3), (2048, 8192, 16), (6144, 8192, 16),
                                    (5000, 4224, 5), (5120, 5120, 3), (3000, 8320, 16),
                                    (4500, 5248, 12), (12000, 8320, 5), (9000, 4224, 33),
-                                   (6000, 4224, 40), (3500, 6144, 33), (1000, 4096, 12)])
+                                   (6000, 4224, 40), (3500, 6144, 33), (1000, 4096, 12),
+                                   (4096, 4096, 4), (3000, 4096, 5)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
     # The single-pass MFMA tile kernels in each of their shapes (operands
     # staged in LDS: one tile per wave with 16 or 8 waves, two tiles per wave
