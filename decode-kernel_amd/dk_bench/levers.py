@@ -50,11 +50,14 @@ def _close(a, b) -> bool:
     return bool(((a32 - b32).abs() <= 1e-3 + ulp).all())
 
 
-def _time(fn, steps, flush) -> float:
+def _time(fn, steps, flush, runs: int = 1) -> float:
+    """p50 us per step; with runs > 1 the lowest of that many timings (the
+    first timings after a new set of weight copies run up to 8% slow on
+    MI355X, so the product, timed first on each shape, is timed twice)."""
     from .common import time_graph_steps
 
-    st, _ = time_graph_steps(fn, steps=steps, preroll=flush)
-    return st["median_us"]
+    return min(time_graph_steps(fn, steps=steps, preroll=flush)[0]["median_us"]
+               for _ in range(runs))
 
 
 def sweep_floor(flush, steps: int) -> dict:
@@ -84,7 +87,8 @@ def sweep_c0(flush, steps: int) -> dict:
     n = len(pk)
     y_prod = _cuda.w4a16_gemv(pk[0], sc[0], x)
     y = torch.empty_like(y_prod)
-    rows = {"product_v5": _time(lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x), steps, flush)}
+    rows = {"product_v5": _time(lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x), steps, flush,
+                                runs=2)}
     print(f"c0 product v5 {rows['product_v5']:.3f} us", flush=True)
     for shape in V5_C0_SHAPES:
         benchlib.v5(0, shape, pk[0], sc[0], x, y)
@@ -139,7 +143,8 @@ def sweep_v4(flush, steps: int) -> dict:
         n = len(pk)
         y_prod = _cuda.w4a16_gemv(pk[0], sc[0], x)
         y = torch.empty_like(y_prod)
-        rows = {"product_v5": _time(lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x), steps, flush)}
+        rows = {"product_v5": _time(lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x), steps, flush,
+                                    runs=2)}
         for sk in (2, 4, 8, 16):
             rows[f"product_v4_s{sk}"] = _time(
                 lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x, version=4, split_k=sk), steps,
@@ -198,7 +203,8 @@ def sweep_split(flush, steps: int) -> dict:
         n = len(pk)
         y_prod = _cuda.w4a16_gemv(pk[0], sc[0], x)
         y = torch.empty_like(y_prod)
-        rows = {"product_v5": _time(lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x), steps, flush)}
+        rows = {"product_v5": _time(lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x), steps, flush,
+                                    runs=2)}
         for shape in V4S_SHAPES:
             benchlib.v4s(shape, pk[0], sc[0], x, y)
             torch.cuda.synchronize()
@@ -247,7 +253,8 @@ def sweep_reuse(flush, steps: int) -> dict:
             y_prod = _cuda.w4a16_gemv(pk[0], sc[0], x, reuse_weights=True)
             y = torch.empty_like(y_prod)
             rows = {"product_reuse": _time(
-                lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x, reuse_weights=True), steps, flush)}
+                lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x, reuse_weights=True), steps, flush,
+                runs=2)}
             for shape in REUSE_SHAPES:
                 kind, ks, rt, sg, pairs = shape
                 y.fill_(float("nan"))
@@ -300,7 +307,7 @@ def sweep_mlp(flush, steps: int) -> dict:
             h_prod = gate_up_silu(x, gps[0], gss[0], ups[0], uss[0])
             hbuf = torch.empty_like(h_prod)
             rows = {"product": _time(lambda j: gate_up_silu(x, gps[j % n], gss[j % n], ups[j % n],
-                                                            uss[j % n]), steps, flush)}
+                                                            uss[j % n]), steps, flush, runs=2)}
             for shape in MLP_SHAPES:
                 kind, ks, pairs = shape
                 hbuf.fill_(float("nan"))

@@ -5,9 +5,14 @@
 Runs, each after a 1 GiB read-only flush so every launch starts cold:
   * `--copies` launches of the d2d copy over a 64 MiB buffer: known traffic
     (64 MiB read + 64 MiB written) that calibrates FETCH_SIZE / WRITE_SIZE;
-  * `--reps` launches of one GEMV variant at one benchmark configuration, or
-    of another operation on the path (the MLP step, the paired-layout GEMV,
-    the device quantizer: `--config mlp7b|mlp70b|paired_c0|paired_c4b|quant_c4a`).
+  * `--reps` launches of each GEMV variant at each benchmark configuration
+    (comma-separated lists), or of another operation on the path (the MLP
+    step, the paired-layout GEMV, the device quantizer:
+    `--config mlp7b|mlp70b|paired_c0|paired_c4b|quant_c4a`). Variants
+    `no_decode` and `loads_only` run the kernel the product dispatches at one
+    batch row with the ablation maths of dk_bench/libdk_bench.so (the same
+    loads; the decode replaced, or the decode and the activation reads from
+    LDS), so a counter run shows whether they move the product's bytes.
 Replaces the reference's ncu launcher (bench/ncu_launch.py:13-34).
 """
 
@@ -27,6 +32,7 @@ SHAPES = {"c0": (4096, 4096, 1), "c1": (11008, 4096, 1), "c2": (4096, 11008, 1),
           "c4ab8": (28672, 8192, 8), "c4b": (8192, 28672, 1)}
 VARIANTS = {"v5": dict(version=5), "v2": dict(version=2), "v4": dict(version=4, split_k=4),
             "reuse": dict(version=5, reuse_weights=True), "v1": dict(version=1)}
+ABLATIONS = {"no_decode": 1, "loads_only": 2}
 COPY_BYTES = 64 << 20
 
 
@@ -83,15 +89,25 @@ OTHER_OPS = {"mlp7b": _mlp(11008, 4096), "mlp70b": _mlp(28672, 8192),
 
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("--config", default="c0", choices=sorted(SHAPES) + sorted(OTHER_OPS))
-    ap.add_argument("--variant", default="v5", choices=sorted(VARIANTS))
+    ap.add_argument("--config", default="c0",
+                    help="comma-separated: " + ", ".join(sorted(SHAPES) + sorted(OTHER_OPS)))
+    ap.add_argument("--variant", default="v5",
+                    help="comma-separated: " + ", ".join(sorted(VARIANTS) + sorted(ABLATIONS)))
     ap.add_argument("--reps", type=int, default=50)
     ap.add_argument("--copies", type=int, default=5)
     args = ap.parse_args()
+    configs = args.config.split(",")
+    variants = args.variant.split(",")
+    for c in configs:
+        if c not in SHAPES and c not in OTHER_OPS:
+            ap.error(f"unknown config {c}")
+    for v in variants:
+        if v not in VARIANTS and v not in ABLATIONS:
+            ap.error(f"unknown variant {v}")
 
     import torch
 
-    from decode_kernel import _cuda, gemv
+    from decode_kernel import _abi, _cuda, gemv
     from decode_kernel.quantize import quantize_and_pack
     from dk_bench.common import Flush, bytes_moved_w4
     from dk_bench.common import synthetic_case
@@ -102,23 +118,36 @@ def main() -> None:
     for _ in range(args.copies):
         flush()
         _cuda.d2d_copy(src, dst)
-    if args.config in OTHER_OPS:
-        OTHER_OPS[args.config](args.reps, flush)
-        torch.cuda.synchronize()
-        print(json.dumps({"config": args.config, "reps": args.reps, "copy_bytes": COPY_BYTES}),
-              flush=True)
-        return
-    m, k, b = SHAPES[args.config]
-    w, x = synthetic_case(m, k, b, seed=1000)
-    packed, scales = quantize_and_pack(torch.from_numpy(w))
-    pd, sd, xd = packed.cuda(), scales.cuda(), torch.from_numpy(x).cuda()
-    for _ in range(args.reps):
-        flush()
-        gemv(pd, sd, xd, **VARIANTS[args.variant])
-    torch.cuda.synchronize()
-    print(json.dumps({"config": args.config, "variant": args.variant, "M": m, "K": k, "B": b,
-                      "reps": args.reps, "copy_bytes": COPY_BYTES,
-                      "algorithmic_bytes": bytes_moved_w4(m, k, b)}), flush=True)
+    for config in configs:
+        if config in OTHER_OPS:
+            OTHER_OPS[config](args.reps, flush)
+            torch.cuda.synchronize()
+            print(json.dumps({"config": config, "reps": args.reps, "copy_bytes": COPY_BYTES}),
+                  flush=True)
+            continue
+        m, k, b = SHAPES[config]
+        w, x = synthetic_case(m, k, b, seed=1000)
+        packed, scales = quantize_and_pack(torch.from_numpy(w))
+        pd, sd, xd = packed.cuda(), scales.cuda(), torch.from_numpy(x).cuda()
+        for variant in variants:
+            if variant in ABLATIONS:
+                from dk_bench import benchlib
+
+                kern = benchlib.parse_kernel(_abi.describe(_abi.load(), m, k, b)["kernel"])
+                if kern is None:
+                    raise SystemExit(f"{config}: no ablation of the dispatched kernel")
+                y = torch.empty(b, m, dtype=torch.float16, device="cuda")
+                for _ in range(args.reps):
+                    flush()
+                    benchlib.run_kernel(kern, ABLATIONS[variant], pd, sd, xd, y)
+            else:
+                for _ in range(args.reps):
+                    flush()
+                    gemv(pd, sd, xd, **VARIANTS[variant])
+            torch.cuda.synchronize()
+            print(json.dumps({"config": config, "variant": variant, "M": m, "K": k, "B": b,
+                              "reps": args.reps, "copy_bytes": COPY_BYTES,
+                              "algorithmic_bytes": bytes_moved_w4(m, k, b)}), flush=True)
 
 
 if __name__ == "__main__":

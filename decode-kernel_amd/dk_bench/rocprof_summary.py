@@ -37,8 +37,28 @@ def _dbs(root: str) -> list[str]:
     return sorted(glob.glob(os.path.join(root, "**", "*.db"), recursive=True))
 
 
-def _short(name: str, width: int = 64) -> str:
-    return name if len(name) <= width else name[: width - 3] + "..."
+W = 92  # kernel name column
+
+
+def _short(name: str, width: int = W) -> str:
+    """The kernel name without its return type and parameter list (template
+    arguments kept: they tell the launch shapes and the ablation maths
+    apart), shortened in the middle if still too long."""
+    if name.startswith("void "):
+        name = name[5:]
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0 and i > 0:
+            name = name[:i]
+            break
+    if len(name) <= width:
+        return name
+    half = (width - 3) // 2
+    return name[:half] + "..." + name[-(width - 3 - half):]
 
 
 def load_trace(root: str) -> list[dict]:
@@ -88,11 +108,11 @@ def summarize_trace(rows: list[dict], match: str | None) -> str:
         if match and match not in r["name"]:
             continue
         groups[(r["name"], r["grid"])].append(r["dur_ns"] / 1000.0)
-    lines = [f"{'kernel':64s} {'grid':>9s} {'n':>5s} {'mean_us':>9s} {'p50_us':>9s} "
+    lines = [f"{'kernel':{W}s} {'grid':>9s} {'n':>5s} {'mean_us':>9s} {'p50_us':>9s} "
              f"{'min_us':>9s} {'max_us':>9s}"]
     for (name, grid), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
         d.sort()
-        lines.append(f"{_short(name):64s} {grid:9d} {len(d):5d} {statistics.fmean(d):9.2f} "
+        lines.append(f"{_short(name):{W}s} {grid:9d} {len(d):5d} {statistics.fmean(d):9.2f} "
                      f"{d[len(d) // 2]:9.2f} {d[0]:9.2f} {d[-1]:9.2f}")
     return "\n".join(lines)
 
@@ -112,7 +132,7 @@ def summarize_pmc(rows: list[dict], match: str | None) -> tuple[str, dict]:
         lines.append("calibration (64 MiB d2d copy): " + ", ".join(
             f"{k} x{v:.4f}" for k, v in sorted(factors.items())))
     out = {}
-    lines.append(f"{'kernel':64s} {'counter':12s} {'n':>5s} {'mean/dispatch':>14s} {'scaled bytes':>14s}")
+    lines.append(f"{'kernel':{W}s} {'counter':12s} {'n':>5s} {'mean/dispatch':>14s} {'scaled bytes':>14s}")
     for name, cs in sorted(per.items()):
         if match and match not in name and COPY_KERNEL not in name:
             continue
@@ -122,7 +142,7 @@ def summarize_pmc(rows: list[dict], match: str | None) -> tuple[str, dict]:
             out.setdefault(name, {})[cname] = {"mean_per_dispatch": m, "n": len(vals),
                                                "scaled_bytes": scaled}
             sb = f"{scaled:14.0f}" if scaled is not None else f"{'-':>14s}"
-            lines.append(f"{_short(name):64s} {cname:12s} {len(vals):5d} {m:14.1f} {sb}")
+            lines.append(f"{_short(name):{W}s} {cname:12s} {len(vals):5d} {m:14.1f} {sb}")
     return "\n".join(lines), {"factors": factors, "kernels": out}
 
 
