@@ -523,8 +523,8 @@ DKB_API int dkb_wall_clock_khz(void) {
 
 // The reuse path's tile kernels at any instantiated shape (B rows in tiles of
 // 16): kind 0 gemv_reuse<KS, RT, SG, pairs> (MFMA operands loaded directly),
-// kind 1 gemv_reuse_lds<KS, RT, pairs> (both operands staged in LDS by the
-// buffer-load-to-LDS path; SG must be 2). Returns 3 (nothing launched) for a
+// kind 1 gemv_reuse_lds<KS, RT, pairs, SG> (both operands staged in LDS by
+// the buffer-load-to-LDS path, blocks of SG = 2 or 4 groups). Returns 3 (nothing launched) for a
 // shape not instantiated here.
 DKB_API int dkb_reuse(int kind, int KS, int RT, int SG, int pairs, const void* packed,
                       const void* scales, const void* x, void* y, int M, int K, int B,
@@ -539,17 +539,20 @@ DKB_API int dkb_reuse(int kind, int KS, int RT, int SG, int pairs, const void* p
                        (B + 15) / 16), dim3(ks * 64), 0, stream, p, s, xx, yy, M, K, B);        \
     return launch_error("reuse");                                                              \
   }
-#define DKB_R1(ks, rt, pr)                                                                     \
-  if (kind == 1 && KS == ks && RT == rt && SG == 2 && pairs == (int)pr) {                      \
-    hipLaunchKernelGGL((dk::gemv_reuse_lds<ks, rt, pr>), dim3((M + 16 * rt - 1) / (16 * rt),     \
+#define DKB_R1S(ks, rt, pr, sg)                                                                \
+  if (kind == 1 && KS == ks && RT == rt && SG == sg && pairs == (int)pr) {                     \
+    hipLaunchKernelGGL((dk::gemv_reuse_lds<ks, rt, pr, sg>), dim3((M + 16 * rt - 1) / (16 * rt), \
                        (B + 15) / 16), dim3(ks * 64), 0, stream, p, s, xx, yy, M, K, B);        \
     return launch_error("reuse lds");                                                          \
   }
+#define DKB_R1(ks, rt, pr) DKB_R1S(ks, rt, pr, 2)
   DKB_R0(8, 1, 2, true) DKB_R0(8, 1, 2, false) DKB_R0(8, 1, 4, false) DKB_R0(16, 1, 4, false)
   DKB_R0(16, 1, 2, false) DKB_R0(8, 2, 2, true) DKB_R0(8, 2, 2, false) DKB_R0(8, 2, 4, false)
   DKB_R1(8, 1, true) DKB_R1(8, 1, false) DKB_R1(16, 1, true) DKB_R1(16, 1, false)
   DKB_R1(8, 2, true) DKB_R1(8, 2, false) DKB_R1(4, 1, true) DKB_R1(4, 2, true)
+  DKB_R1S(8, 1, true, 4) DKB_R1S(4, 1, true, 4) DKB_R1S(4, 2, true, 4) DKB_R1S(8, 1, false, 4)
 #undef DKB_R1
+#undef DKB_R1S
 #undef DKB_R0
   return 3;
 }

@@ -612,15 +612,15 @@ int launch_reuse(const Launch& L, const uint4* p, const uint16_t* s, const uint4
            K, B);
 }
 
-template <int KS, int RT>
+template <int KS, int RT, int SG = 2>
 int launch_reuse_lds(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x,
                      uint16_t* y, int M, int K, int B) {
   const dim3 grid((M + 16 * RT - 1) / (16 * RT), (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
   if ((K / DK_GROUP_SIZE) % 2 == 0 && aligned(s, 4))
-    return L("reuse launch", dk::gemv_reuse_lds<KS, RT, true>, grid, dim3(KS * 64), 0, p, s, x, y,
-             M, K, B);
-  return L("reuse launch", dk::gemv_reuse_lds<KS, RT, false>, grid, dim3(KS * 64), 0, p, s, x, y, M,
-           K, B);
+    return L("reuse launch", dk::gemv_reuse_lds<KS, RT, true, SG>, grid, dim3(KS * 64), 0, p, s, x,
+             y, M, K, B);
+  return L("reuse launch", dk::gemv_reuse_lds<KS, RT, false, SG>, grid, dim3(KS * 64), 0, p, s, x,
+           y, M, K, B);
 }
 
 // The single-pass tiles. The LDS-staged kernel (gemv_reuse_lds) against the
@@ -659,6 +659,12 @@ int launch_reuse_tiles(const Launch& L, const uint4* p, const uint16_t* s, const
                    : launch_reuse_lds<4, 2>(L, p, s, x, y, M, K, B);
   if (M > 2048 && B > 16) return launch_reuse_lds<8, 2>(L, p, s, x, y, M, K, B);
   if (M > 2048 && B <= 8 && K <= 8192) return launch_reuse_lds<8, 1>(L, p, s, x, y, M, K, B);
+  // Up to 2048 rows of 8192 weights or more, from 8 batch rows: blocks of
+  // four groups, 8 waves (one block per wave at K = 8192; us, against 16
+  // waves with blocks of two): M = 2048, K = 16384, B = 16 12.92 (13.81),
+  // B = 32 12.91 (13.45); M = 2048, K = 8192, B = 8 6.94 (7.17), B = 16 8.04
+  // (8.34). At M = K = 4096 they lose (B = 16: 5.83 against 5.61).
+  if (M <= 2048 && K >= 8192 && B >= 8) return launch_reuse_lds<8, 1, 4>(L, p, s, x, y, M, K, B);
   return launch_reuse_lds<16, 1>(L, p, s, x, y, M, K, B);
 }
 

@@ -857,74 +857,88 @@ __device__ __forceinline__ int stage_swizzle(int r) {
   }
 }
 
-template <int KS, int RT>
+// Per wave, for blocks of SG groups: 16 batch rows x 16 SG chunks of x and
+// 16 RT rows x 4 SG chunks of weights.
+template <int KS, int RT, int SG = 2>
 struct ReuseDmaLds {
-  uint4 x[KS][16 * 32];      // per wave: 16 batch rows x 32 chunks (two groups)
-  uint4 w[KS][RT * 16 * 8];  // per wave: 16 RT rows x 8 chunks (two groups)
+  uint4 x[KS][16 * 16 * SG];
+  uint4 w[KS][RT * 16 * 4 * SG];
 };
 
 // The block loop of the LDS-staged tiles: tile t's weights and scales
 // through descriptors rw[t], rs[t] (rows 0..15 relative to them, G groups
 // per row), x of batch rows bt0 .. bt0 + 15 (those below B) through rx with
 // rows K * 2 bytes apart. acc[t] is this lane's part of tile t's fp32 16x16
-// result over the wave's blocks (groups 2 wave, 2 wave + 1, then every 2 KS).
-template <int KS, int RT, bool kPairs>
+// result over the wave's blocks of SG (2 or 4) groups (groups SG wave ..
+// SG wave + SG - 1, then every SG KS). kPairs: the scales of two groups in
+// one 4-byte load (an even number of groups per row, 4-byte aligned).
+template <int KS, int RT, bool kPairs, int SG = 2>
 __device__ __forceinline__ void reuse_lds_loop(f4_t (&acc)[RT], uint4* xbuf, uint4* wbuf,
                                                const __amdgpu_buffer_rsrc_t (&rw)[RT],
                                                const __amdgpu_buffer_rsrc_t (&rs)[RT],
                                                __amdgpu_buffer_rsrc_t rx, int bt0, int B, int K,
                                                int G, int lane, int wave) {
+  static_assert(SG == 2 || SG == 4, "blocks of two or four groups");
+  constexpr int kWC = 4 * SG;   // weight chunks per row of a block
+  constexpr int kWR = 64 / kWC;  // weight rows per load
+  constexpr int kXC = 16 * SG;  // x chunks per batch row of a block
+  constexpr int kXR = 64 / kXC;  // batch rows per x load
   const int nck = K >> 5;
   const int kq = lane >> 4;
   const int r_lane = lane & 15;
-  // x loads (two batch rows each) with a batch row below B (wave-uniform).
-  const int nxl = min(8, (max(0, min(16, B - bt0)) + 1) / 2);
+  // x loads with a batch row below B (wave-uniform).
+  const int nxl = min(16 / kXR, (max(0, min(16, B - bt0)) + kXR - 1) / kXR);
 #pragma unroll
   for (int t = 0; t < RT; ++t) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
-  for (int g0 = 2 * wave; g0 < G; g0 += 2 * KS) {
-    // Weights: load i covers rows 8 (i % 2) .. + 7 of tile i / 2, lane l
-    // chunk l % 8 of row 8 (i % 2) + l / 8 (chunk c = group c / 4 of the
-    // block, bytes 16 (c % 4) of it).
+  for (int g0 = SG * wave; g0 < G; g0 += SG * KS) {
+    // Weights: load i covers rows kWR (i % (16 / kWR)) .. + kWR - 1 of tile
+    // i / (16 / kWR), lane l chunk l % kWC of row kWR (i % (16 / kWR)) + l /
+    // kWC (chunk c = group c / 4 of the block, bytes 16 (c % 4) of it).
 #pragma unroll
-    for (int i = 0; i < 2 * RT; ++i) {
-      const int r = 8 * (i % 2) + lane / 8;
-      const int c = (lane % 8) ^ stage_swizzle<8>(r);
+    for (int i = 0; i < RT * 16 / kWR; ++i) {
+      const int r = kWR * (i % (16 / kWR)) + lane / kWC;
+      const int c = (lane % kWC) ^ stage_swizzle<kWC>(r);
       const int off = g0 * 4 + c < G * 4 ? r * nck * 16 + (g0 * 4 + c) * 16 : kOutOfRange;
       // A local copy of the descriptor: given the array element itself, the
       // host pass leaves the kernel's launch stub undefined.
-      const __amdgpu_buffer_rsrc_t rwt = rw[i / 2];
+      const __amdgpu_buffer_rsrc_t rwt = rw[i / (16 / kWR)];
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rwt, (lds_void_ptr)(wbuf + i * 64), 16, off, 0, 0,
                                                kLoadNonTemporal);
     }
-    // x: load i covers batch rows bt0 + 2i and + 1, lane l chunk l % 32 of
-    // row 2i + l / 32 (chunk c = group c / 16, bytes 16 (c % 16)).
+    // x: load i covers batch rows bt0 + kXR i .. + kXR - 1, lane l chunk
+    // l % kXC of row kXR i + l / kXC (chunk c = group c / 16, bytes 16 (c % 16)).
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 16 / kXR; ++i) {
       if (i < nxl) {
-        const int bb = 2 * i + lane / 32;
-        const int p = lane % 32;
-        const int c = (p & 16) | ((p ^ stage_swizzle<32>(bb)) & 15);
+        const int bb = kXR * i + lane / kXC;
+        const int p = lane % kXC;
+        const int c = (p & ~15) | ((p ^ stage_swizzle<kXC>(bb)) & 15);
         const bool ok = bt0 + bb < B && g0 * 16 + c < G * 16;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rx, (lds_void_ptr)(xbuf + i * 64), 16,
             ok ? (bt0 + bb) * K * 2 + (g0 * 16 + c) * 16 : kOutOfRange, 0, 0, 0);
       }
     }
-    // Scales of this lane's four D rows: both groups in one 4-byte load where
-    // the scales allow (an even number of groups, so g0 + 1 < G).
-    float sc[RT][2][4];
+    // Scales of this lane's four D rows: two groups in one 4-byte load where
+    // the scales allow (an even number of groups, so g0 + 2v + 1 < G when
+    // g0 + 2v < G).
+    float sc[RT][SG][4];
 #pragma unroll
     for (int t = 0; t < RT; ++t)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         if constexpr (kPairs) {
-          const uint32_t two =
-              __builtin_amdgcn_raw_buffer_load_b32(rs[t], ((4 * kq + v) * G + g0) * 2, 0, 0);
-          sc[t][0][v] = h2f((uint16_t)two);
-          sc[t][1][v] = h2f((uint16_t)(two >> 16));
+#pragma unroll
+          for (int u2 = 0; u2 < SG / 2; ++u2) {
+            const int g = g0 + 2 * u2;
+            const uint32_t two = __builtin_amdgcn_raw_buffer_load_b32(
+                rs[t], g < G ? ((4 * kq + v) * G + g) * 2 : kOutOfRange, 0, 0);
+            sc[t][2 * u2][v] = h2f((uint16_t)two);
+            sc[t][2 * u2 + 1][v] = h2f((uint16_t)(two >> 16));
+          }
         } else {
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
+          for (int u = 0; u < SG; ++u) {
             const int off = g0 + u < G ? ((4 * kq + v) * G + g0 + u) * 2 : kOutOfRange;
             sc[t][u][v] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs[t], off, 0, 0));
           }
@@ -934,17 +948,18 @@ __device__ __forceinline__ void reuse_lds_loop(f4_t (&acc)[RT], uint4* xbuf, uin
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < SG; ++u) {
       h8_t xp[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int xc = 16 * u + 4 * kq + j;
-        xp[j] = pair_x8(xbuf[r_lane * 32 + ((xc & 16) | ((xc ^ stage_swizzle<32>(r_lane)) & 15))]);
+        xp[j] = pair_x8(
+            xbuf[r_lane * kXC + ((xc & ~15) | ((xc ^ stage_swizzle<kXC>(r_lane)) & 15))]);
       }
 #pragma unroll
       for (int t = 0; t < RT; ++t) {
-        const int wc = (4 * u + kq) ^ stage_swizzle<8>(r_lane);
-        const uint4 wv = wbuf[(16 * t + r_lane) * 8 + wc];
+        const int wc = (4 * u + kq) ^ stage_swizzle<kWC>(r_lane);
+        const uint4 wv = wbuf[(16 * t + r_lane) * kWC + wc];
         const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
         f4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -966,9 +981,9 @@ __device__ __forceinline__ void reuse_lds_loop(f4_t (&acc)[RT], uint4* xbuf, uin
 // Partials of the LDS-staged tiles over each wave's own x buffer (no other
 // wave reads it before the barrier that follows), and tile t's KS partials
 // added in wave order (after that barrier).
-template <int KS, int RT>
-__device__ __forceinline__ void reuse_lds_publish(ReuseDmaLds<KS, RT>& lds, const f4_t (&acc)[RT],
-                                                  int wave, int lane) {
+template <int KS, int RT, int SG>
+__device__ __forceinline__ void reuse_lds_publish(ReuseDmaLds<KS, RT, SG>& lds,
+                                                  const f4_t (&acc)[RT], int wave, int lane) {
   float* part = reinterpret_cast<float*>(lds.x[wave]);
 #pragma unroll
   for (int t = 0; t < RT; ++t)
@@ -976,8 +991,9 @@ __device__ __forceinline__ void reuse_lds_publish(ReuseDmaLds<KS, RT>& lds, cons
     for (int v = 0; v < 4; ++v) part[(t * 64 + lane) * 4 + v] = acc[t][v];
 }
 
-template <int KS, int RT>
-__device__ __forceinline__ f4_t reuse_lds_sum(const ReuseDmaLds<KS, RT>& lds, int t, int lane) {
+template <int KS, int RT, int SG>
+__device__ __forceinline__ f4_t reuse_lds_sum(const ReuseDmaLds<KS, RT, SG>& lds, int t,
+                                              int lane) {
   f4_t sum = {0.f, 0.f, 0.f, 0.f};
   for (int w2 = 0; w2 < KS; ++w2) {
     const float* part = reinterpret_cast<const float*>(lds.x[w2]);
@@ -987,7 +1003,7 @@ __device__ __forceinline__ f4_t reuse_lds_sum(const ReuseDmaLds<KS, RT>& lds, in
   return sum;
 }
 
-template <int KS, int RT, bool kPairs>
+template <int KS, int RT, bool kPairs, int SG = 2>
 __global__ __launch_bounds__(KS * 64) void gemv_reuse_lds(const uint4* __restrict__ packed,
                                                           const uint16_t* __restrict__ scales,
                                                           const uint4* __restrict__ x4,
@@ -995,7 +1011,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_lds(const uint4* __restric
                                                           int B) {
   static_assert(KS >= RT, "wave t sums tile t");
   write_stamp(DK_STAMP_REUSE);
-  __shared__ ReuseDmaLds<KS, RT> lds;
+  __shared__ ReuseDmaLds<KS, RT, SG> lds;
   const int G = K >> 7;
   const int nck = K >> 5;
   const int lane = threadIdx.x & 63;
@@ -1014,8 +1030,8 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_lds(const uint4* __restric
   }
   const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
   f4_t acc[RT];
-  reuse_lds_loop<KS, RT, kPairs>(acc, lds.x[wave], lds.w[wave], rw, rs, rx, bt0, B, K, G, lane,
-                                 wave);
+  reuse_lds_loop<KS, RT, kPairs, SG>(acc, lds.x[wave], lds.w[wave], rw, rs, rx, bt0, B, K, G,
+                                     lane, wave);
   reuse_lds_publish(lds, acc, wave, lane);
   __syncthreads();
   if (wave < RT) {

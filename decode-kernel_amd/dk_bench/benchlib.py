@@ -152,8 +152,8 @@ def run_kernel(kernel: tuple, math: int, packed, scales, x, y) -> None:
 
 def reuse(kind: int, ks: int, rt: int, sg: int, pairs: bool, packed, scales, x, y) -> int:
     """The reuse path's tile kernels: kind 0 gemv_reuse<KS, RT, SG, pairs>,
-    kind 1 gemv_reuse_lds<KS, RT, pairs> (SG = 2). Returns 3 (nothing
-    launched) for a shape not instantiated in the measurement library."""
+    kind 1 gemv_reuse_lds<KS, RT, pairs, SG>. Returns 3 (nothing launched)
+    for a shape not instantiated in the measurement library."""
     m, k = packed.shape[0], packed.shape[1] * 8
     b = x.shape[0]
     rc = load().dkb_reuse(kind, ks, rt, sg, int(pairs), packed.data_ptr(), scales.data_ptr(),

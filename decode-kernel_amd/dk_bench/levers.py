@@ -229,7 +229,7 @@ REUSE_BATCHES = (3, 4, 5, 8, 12, 16, 32)
 REUSE_SHAPES = [(0, 8, 1, 2, True), (0, 8, 1, 4, False), (0, 16, 1, 4, False), (0, 16, 1, 2, False),
                 (0, 8, 2, 2, True), (0, 8, 2, 4, False),
                 (1, 8, 1, 2, True), (1, 16, 1, 2, True), (1, 8, 2, 2, True), (1, 4, 1, 2, True),
-                (1, 4, 2, 2, True)]
+                (1, 4, 2, 2, True), (1, 8, 1, 4, True), (1, 4, 1, 4, True), (1, 4, 2, 4, True)]
 
 
 def sweep_reuse(flush, steps: int) -> dict:

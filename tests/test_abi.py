@@ -150,7 +150,7 @@ def test_describe_names_the_dispatched_kernel(lib):
     d = _abi.describe(lib, 4096, 11008, 1, version=4, split_k=4)
     assert d["kernel"].startswith("void dk::gemv_v4_split<")
     assert _abi.describe(lib, 4096, 4096, 16, reuse_weights=1)["kernel"].startswith(
-        "void dk::gemv_reuse_lds<16, 1, true>")
+        "void dk::gemv_reuse_lds<16, 1, true, 2>")
     assert _abi.describe(lib, 28672, 8192, 4, reuse_weights=1)["kernel"].startswith(
         "void dk::gemv_reuse<8, 2, 2, true>")
     assert _abi.describe(lib, 4096, 4096, 2, reuse_weights=1)["kernel"].startswith(

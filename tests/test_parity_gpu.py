@@ -175,7 +175,8 @@ def test_reuse_small_batches_run_the_streaming_kernel():
                                    (5000, 4224, 5), (5120, 5120, 3), (3000, 8320, 16),
                                    (4500, 5248, 12), (12000, 8320, 5), (9000, 4224, 33),
                                    (6000, 4224, 40), (3500, 6144, 33), (1000, 4096, 12),
-                                   (4096, 4096, 4), (3000, 4096, 5)])
+                                   (4096, 4096, 4), (3000, 4096, 5), (2000, 16512, 13),
+                                   (1500, 8320, 9)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
     # The single-pass MFMA tile kernels in each of their shapes (operands
     # staged in LDS: one tile per wave with 16 or 8 waves, two tiles per wave
@@ -217,7 +218,7 @@ def test_reuse_tile_kernel_exact_properties(m, k, b):
 
 @pytest.mark.parametrize("m,k,b", [(4096, 4096, 8), (8192, 8192, 4), (6144, 8192, 16),
                                    (28672, 1024, 5), (28672, 8192, 4), (2048, 8192, 16),
-                                   (9000, 4096, 20)])
+                                   (9000, 4096, 20), (1500, 8192, 12)])
 def test_reuse_tiles_scale_alignment(m, k, b):
     # With 4-byte aligned scales and an even number of groups per row the
     # tiles load the scales of two groups at once; scales that are only
