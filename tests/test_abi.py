@@ -167,6 +167,41 @@ def test_describe_names_the_dispatched_kernel(lib):
         _abi.describe(lib, 64, 200, 1)
 
 
+# The dispatch each routing rule in dk_gemv.hip gives, read back without a
+# GPU (dk_gemv_describe): (M, K, B, config) -> kernel name prefix, grid.
+ROUTES = [
+    ((4096, 4096, 1), {}, "dk::gemv_v5_lds<1, 2, 8, 1, true, dk::LayoutLogical, 5,", [512, 1, 1]),
+    ((4096, 11008, 1), {}, "dk::gemv_v4_split<1, 1, 16, 2, 1, true,", [512, 1, 1]),
+    ((512, 28672, 1), {}, "dk::gemv_v4_split<1, 2, 8, 4, 1, false,", [256, 1, 1]),
+    ((1024, 28672, 1), {}, "dk::gemv_v4_split<2, 2, 8, 4, 1, false,", [256, 1, 1]),
+    ((8192, 28672, 1), {}, "dk::gemv_v5_lds<2, 1, 16, 1, true,", [256, 1, 1]),
+    ((4096, 4096, 2), dict(reuse_weights=1), "dk::gemv_v5_lds<1, 2, 8, 2, true, dk::LayoutLogical, 15,",
+     [512, 1, 1]),
+    ((4096, 4096, 4), dict(reuse_weights=1), "dk::gemv_reuse<8, 1, 2, true>", [256, 1, 1]),
+    ((4096, 4096, 8), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 1, true, 2>", [256, 1, 1]),
+    ((4096, 4096, 16), dict(reuse_weights=1), "dk::gemv_reuse_lds<16, 1, true, 2>", [256, 1, 1]),
+    ((4096, 4096, 32), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 2, true, 2>", [128, 2, 1]),
+    ((28672, 8192, 4), dict(reuse_weights=1), "dk::gemv_reuse<8, 2, 2, true>", [896, 1, 1]),
+    ((28672, 8192, 16), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 2, true, 2>", [896, 1, 1]),
+    ((11008, 4096, 4), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 1, true, 2>", [688, 1, 1]),
+    ((6144, 8192, 32), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 2, true, 2>", [192, 2, 1]),
+    ((2048, 16384, 16), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 1, true, 4>", [128, 1, 1]),
+    ((2048, 16512, 16), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 1, false, 4>", [128, 1, 1]),
+    ((1024, 16384, 16), dict(reuse_weights=1), "dk::gemv_reuse_split<8, 2, 2>", [32, 1, 4]),
+    ((1024, 4096, 8), dict(reuse_weights=1), "dk::gemv_v5_lds<1, 2, 8, 2, true, dk::LayoutLogical, 15,",
+     [128, 4, 1]),
+    ((1024, 4096, 12), dict(reuse_weights=1), "dk::gemv_reuse_lds<16, 1, true, 2>", [64, 1, 1]),
+]
+
+
+@pytest.mark.parametrize("shape,kw,kernel,grid", ROUTES)
+def test_dispatch_routes(lib, shape, kw, kernel, grid):
+    m, k, b = shape
+    d = _abi.describe(lib, m, k, b, **kw)
+    assert d["kernel"].startswith("void " + kernel), d["kernel"]
+    assert d["grid"] == grid and d["launches"] == 1
+
+
 def test_reuse_split_workspace_size(lib):
     # The reuse path's split-K tiles (rows longer than 8192 weights at
     # M <= 1024, where the tiles run: 12 or more batch rows, 33 or more at
