@@ -542,56 +542,23 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
 }
 #undef DK_GATE_UP
 
-// Reuse path: the MFMA tile kernel (KS waves per 16-row tile, RT tiles per
-// wave, blocks of two groups, weights through wave-private LDS) against the
-// streaming kernel with its batch tiles, measured on MI355X back-to-back over
-// cold weights (us per launch, tiles first, * where the streaming kernel is
-// chosen):
+// The reuse path's tiles that load the MFMA operands directly (gemv_reuse:
+// KS waves per 16-row tile, RT tiles per wave, blocks of SG groups, weights
+// through wave-private LDS, x in the MFMA B layout straight from memory).
+// They take the shapes where the LDS-staged tiles (launch_reuse_lds below)
+// measured slower: M > 8192 with rows longer than 4096 weights up to 8 batch
+// rows, and rows of up to 4096 weights at 2049-4096 rows up to 5. Measured
+// when they ran every tile shape (us per launch, against the streaming
+// kernel's batch tiles in brackets, * where those were chosen):
 //                        B = 2          B = 3          B = 4          B = 5    B = 8    B = 16
 //   M = 28672, K = 8192: 29.08 (25.69*) 29.59 (33.42)  30.31 (36.87)  30.29    33.65    44.04
 //   M = 8192, K = 28672: 29.65 (24.58*) 29.40 (30.99)  29.68 (35.14)  30.24    32.76    40.91
-//   M = 4096, K = 11008: 8.68 (7.44*)   8.78 (8.62*)   8.94 (10.14)   9.06     10.64    15.71
-//   M = 3072, K = 8192:  6.84 (5.89*)   6.97 (6.93*)   7.13 (8.09)
 //   M = K = 4096:        4.66 (3.93*)   4.73 (4.44*)   4.82 (4.95)    4.82     5.23     6.82
-//   M = 11008, K = 4096: 9.36 (6.80*)   9.47 (8.50*)   9.56 (9.65)    9.45     10.10    13.09
-//   M = 6144, K = 8192:  11.46 (8.22*)  11.69 (10.03*) 11.88 (11.68)  11.87    13.57    19.73
-// and at small M, with the streaming kernel in brackets:
-//   M = 2048, K = 8192:  B = 4 6.91 (5.55*), B = 5 6.91 (6.45*), B = 8 7.74 (7.39*), B = 16 11.41 (13.09)
-//   M = 2048, K = 16384: B = 5 11.34 (10.35*), B = 8 13.34 (12.13*), B = 16 20.05 (22.60)
-//   M = 1024, K = 11008: B = 16 14.50 (12.15*), B = 32 14.21 (22.40)
-//   M = 1024, K = 4096:  B = 16 6.62 (5.55*), B = 32 6.60 (9.40)
-//   M = 512, K = 8320:   B = 16 11.63 (6.70*), B = 32 11.47 (11.67*)
-// At rows of 4097-8191 weights from M = 3072 the tiles take three rows too
-// (M = K = 5120: 7.59 against 9.75 us; M = 4096, K = 6144: 5.69 against
-// 7.25; M = 13824, K = 5120: 10.42 against 18.57).
 // The tiles cost about the same from one batch row to five (16 MFMA batch
-// columns), so they take three rows on the 70B shapes (M * K >= 2^27) and
-// four from M = 3072 (within 2% of the streaming kernel at M = 6144,
-// K = 8192); M / 16 tiles leave most CUs idle at small M, where the
-// streaming kernel splits the batch over more workgroups instead. Two tiles
-// per wave share each activation load once there are enough tiles for the
-// chip (M > 4096); up to M = 4096 one tile per wave with 16 waves per tile,
-// except rows of 8192 weights or more at M <= 2048, with 8 (M = 2048,
-// K = 16384, B = 16: 20.05 against 21.51 us; M = K = 4096, B = 16: 7.24
-// against 7.39 in an earlier form of the kernel); between 4096 and 8192
-// rows, two tiles per wave as well: up to 8 batch rows with blocks of two
-// groups, 11-21% faster than 4 waves with one tile (us, B = 4 and 8):
-// M = K = 5120 6.57 (7.72), 7.78 (9.18); M = 4608, K = 8192 8.85 (10.88),
-// 10.98 (12.74); M = 7168, K = 8192 9.57 (11.37), 11.37 (13.01);
-// M = 6144, K = 14336 13.70 (17.35), 17.24 (20.74); from 9 batch rows
-// with blocks of four groups, 16-31% faster (us, B = 16, against 4
-// waves with one tile and blocks of two): M = K = 5120 10.13 (13.55);
-// M = 6144, K = 4096 8.21 (11.13); M = 4608, K = 8192 14.29 (18.96);
-// M = 7168, K = 8192 15.23 (19.30); M = 6144, K = 14336 22.90 (31.75);
-// M = 5120, K = 13824 21.39 (31.15); M = 6144, K = 8192 14.76 (19.07). From 2049
-// to 4096 rows, with the paired scale loads and uniform descriptors, 8 waves
-// now beat 16 up to 8 batch rows, and blocks of four groups beat two above
-// (us, 16 waves with blocks of two in brackets): M = K = 4096: B = 8 5.02
-// (5.19), B = 16 6.77 with 8 waves (6.87); M = 4096, K = 11008: B = 5 8.40
-// (8.60), B = 16 15.25 with 16 waves (15.77); M = 3072, K = 8192: B = 8 7.74
-// (7.98), B = 16 11.39 (12.17).
-// The weights come through LDS in 128-256 contiguous bytes per row (8-20%
-// faster than loading the MFMA layout directly at M = 11008 or K = 28672).
+// columns); two tiles per wave share each activation load once there are
+// enough tiles for the chip (M > 4096). The weights come through LDS in
+// 128-256 contiguous bytes per row (8-20% faster than loading the MFMA
+// layout directly at M = 11008 or K = 28672).
 template <int KS, int RT, int SG>
 int launch_reuse(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                  int M, int K, int B) {
