@@ -21,6 +21,8 @@
 // kernel here computes the GEMV (checked against the product by the tools).
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include "dk_kernels.hpp"
 #include "dk_mlp.hpp"
 
@@ -546,6 +548,14 @@ DKB_API int dkb_reuse(int kind, int KS, int RT, int SG, int pairs, const void* p
     return launch_error("reuse lds");                                                          \
   }
 #define DKB_R1(ks, rt, pr) DKB_R1S(ks, rt, pr, 2)
+#define DKB_R2(ks, rt)                                                                         \
+  if (kind == 2 && KS == ks && RT == rt && SG == 2 && pairs) {                                 \
+    hipLaunchKernelGGL((dk::gemv_reuse_pf<ks, rt>), dim3((M + 16 * rt - 1) / (16 * rt),        \
+                       (B + 15) / 16), dim3(ks * 64), 0, stream, p, s, xx, yy, M, K, B);        \
+    return launch_error("reuse pf");                                                           \
+  }
+  DKB_R2(4, 1) DKB_R2(6, 1) DKB_R2(7, 1) DKB_R2(4, 2) DKB_R2(6, 2)
+#undef DKB_R2
   DKB_R0(8, 1, 2, true) DKB_R0(8, 1, 2, false) DKB_R0(8, 1, 4, false) DKB_R0(16, 1, 4, false)
   DKB_R0(16, 1, 2, false) DKB_R0(8, 2, 2, true) DKB_R0(8, 2, 2, false) DKB_R0(8, 2, 4, false)
   DKB_R1(8, 1, true) DKB_R1(8, 1, false) DKB_R1(16, 1, true) DKB_R1(16, 1, false)
@@ -554,6 +564,47 @@ DKB_API int dkb_reuse(int kind, int KS, int RT, int SG, int pairs, const void* p
 #undef DKB_R1
 #undef DKB_R1S
 #undef DKB_R0
+  return 3;
+}
+
+// The split-K tile kernels (B rows in tiles of 16, S slices of each row):
+// kind 0 gemv_reuse_split<KS, RT, 2> (MFMA operands loaded directly), kind 1
+// gemv_reuse_split_pf<KS, RT> (double-buffered LDS staging; an even number
+// of groups per row and 4-byte aligned scales). workspace: one 8-byte
+// ticket per set of RT tiles and batch tile, padded to 256 bytes, then
+// S * B * M fp32 partials. Returns 3 (nothing launched) for a shape not
+// instantiated here.
+DKB_API size_t dkb_reuse_split_workspace(int RT, int S, int M, int B) {
+  const size_t tickets = (size_t)((M + 16 * RT - 1) / (16 * RT)) * (size_t)((B + 15) / 16);
+  return (tickets * 8 + 255) / 256 * 256 + (size_t)S * B * M * sizeof(float);
+}
+
+DKB_API int dkb_reuse_split(int kind, int KS, int RT, int S, const void* packed, const void* scales,
+                            const void* x, void* y, void* workspace, int M, int K, int B,
+                            hipStream_t stream) {
+  static std::atomic<unsigned long long> gens{0x5bd1e9955bd1e995ull};
+  const auto* p = static_cast<const uint4*>(packed);
+  const auto* s = static_cast<const uint16_t*>(scales);
+  const auto* xx = static_cast<const uint4*>(x);
+  auto* yy = static_cast<uint16_t*>(y);
+  const size_t tickets = (size_t)((M + 16 * RT - 1) / (16 * RT)) * (size_t)((B + 15) / 16);
+  auto* tk = static_cast<unsigned long long*>(workspace);
+  auto* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + (tickets * 8 + 255) / 256 * 256);
+  const unsigned long long gen =
+      (gens.fetch_add(1ull, std::memory_order_relaxed) & ((1ull << 58) - 1ull)) << 6;
+  const dim3 grid((M + 16 * RT - 1) / (16 * RT), (B + 15) / 16, S);
+  if (S < 1 || S > 63) return 2;
+#define DKB_S(kd, ks, rt, kernel)                                                              \
+  if (kind == kd && KS == ks && RT == rt) {                                                    \
+    hipLaunchKernelGGL((kernel), grid, dim3(ks * 64), 0, stream, p, s, xx, yy, part, tk, gen, M, \
+                       K, B);                                                                  \
+    return launch_error("reuse split");                                                        \
+  }
+  DKB_S(0, 8, 2, (dk::gemv_reuse_split<8, 2, 2>))
+  DKB_S(1, 4, 1, (dk::gemv_reuse_split_pf<4, 1>))
+  DKB_S(1, 6, 1, (dk::gemv_reuse_split_pf<6, 1>))
+  DKB_S(1, 4, 2, (dk::gemv_reuse_split_pf<4, 2>))
+#undef DKB_S
   return 3;
 }
 

@@ -590,9 +590,47 @@ int launch_reuse_lds(const Launch& L, const uint4* p, const uint16_t* s, const u
            y, M, K, B);
 }
 
-// The single-pass tiles. The LDS-staged kernel (gemv_reuse_lds) against the
-// tiles that load the MFMA operands directly (gemv_reuse, the earlier rule's
-// shape) in brackets, us per launch, from the same sweep:
+template <int KS, int RT>
+int launch_reuse_pf(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
+                    int M, int K, int B) {
+  const dim3 grid((M + 16 * RT - 1) / (16 * RT), (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
+  return L("reuse launch", dk::gemv_reuse_pf<KS, RT>, grid, dim3(KS * 64), 0, p, s, x, y, M, K, B);
+}
+
+// Where the double-buffered tiles (gemv_reuse_pf, 4 waves; paired scales
+// only) take the single pass: 0 nowhere, else RT, the tiles per wave. From
+// the sweep of every tile kernel (dk_bench.levers reuse), us, the
+// double-buffered tiles against the best single-buffered ones in brackets:
+//                        B = 8          B = 12         B = 16         B = 32
+//   M = K = 4096:        4.69 (4.87)    4.88 (5.17)    4.97 (5.45)    6.50 (6.37)
+//   M = 4096, K = 11008: 8.99 (8.71)    9.44 (9.59)    10.00 (10.76)  12.94 (13.39)
+//   M = 3072, K = 8192:  7.12 (7.05)    7.36 (7.81)    7.76 (8.52)    10.02 (10.58)
+//   M = 2048, K = 16384: 11.26 (10.73)  11.53 (12.01)  12.33 (13.62)  12.24 (13.44)
+//   M = 2048, K = 4096:  4.54 (4.66)    4.73 (4.87)    4.79 (5.09)    4.79 (5.13)
+//   M = 6144, K = 8192:  10.24 (9.91)   10.44 (10.73)  10.82 (11.46)  19.33 (18.67)
+//   M = 8192, K = 28672: 27.13 (27.76)  29.74 (31.51)  33.20 (34.60)  66.16 (63.84)
+//   M = 5120, K = 5120:  8.02 (6.98)    8.07 (7.48)    8.16 (7.92)    14.11 (11.76)
+//   M = 28672, K = 8192: 34.97 (33.56)  36.79 (37.13)  39.34 (38.62)  70.05 (66.75)
+// One tile per wave up to 4096 rows from 9 batch rows (and 8 on rows of up
+// to 4096 weights); two from 4097 rows on rows of 8192+ weights at 9-16
+// batch rows, and at 2049-4096 rows above 16. At M <= 1024 above 32 batch
+// rows (three batch tiles) the single-buffered tiles keep rows shorter than
+// 16384 weights (M = 512, K = 8192, B = 33: 6.40 against 6.71).
+int reuse_pf_rt(int M, int K, int B) {
+  if (M > 8192) return 0;
+  if (M > 4096) return B >= 9 && B <= 16 && K >= 8192 ? 2 : 0;
+  if (M > 2048) {
+    if (B > 16) return K >= 8192 ? 2 : 0;
+    return B >= 9 || (B == 8 && K <= 4096) ? 1 : 0;
+  }
+  if (B < 9) return 0;
+  return M <= 1024 && B > 32 && K < 16384 ? 0 : 1;
+}
+
+// The single-pass tiles. Where the double-buffered tiles do not run
+// (reuse_pf_rt, or scales that do not pair), the single-buffered LDS-staged
+// kernel (gemv_reuse_lds) against the tiles that load the MFMA operands
+// directly (gemv_reuse) in brackets, us per launch, from an earlier sweep:
 //                        B = 4          B = 8          B = 16         B = 32
 //   M = K = 4096:        4.65 (4.62)    4.94 (5.01)    5.58 (6.78)    6.37 (7.82)
 //   M = 4096, K = 11008: 7.84 (8.40)    8.85 (10.65)   10.97 (15.20)  13.24 (16.92)
@@ -603,9 +641,10 @@ int launch_reuse_lds(const Launch& L, const uint4* p, const uint16_t* s, const u
 //   M = 8192, K = 28672: 25.70 (26.18)  29.02 (32.87)  34.79 (41.08)  64.65 (77.98)
 //   M = 11008, K = 4096: 8.42 (8.84)    9.42 (10.12)   11.21 (13.05)  15.25 (18.63)
 //   M = 28672, K = 8192: 30.64 (28.43)  34.18 (34.22)  39.05 (44.75)  66.82 (77.26)
-// Up to 4096 rows (256 tiles) one tile per wave, 16 waves (8 up to 8 batch
-// rows of up to 8192 weights: M = K = 4096, B = 8 4.94 against 5.09), two
-// per wave above 16 batch rows (the grid then has two batch tiles); to 8192
+// Up to 4096 rows (256 tiles) one tile per wave: 16 waves, or 8 at 6-8
+// batch rows of up to 8192 weights (M = 3072, K = 8192, B = 8: 7.05
+// against 7.31) while 16 keep up to 5 (B = 3: 6.25 against 6.86); two per
+// wave above 16 batch rows (the grid then has two batch tiles); to 8192
 // rows two tiles per wave, 8 waves (4 above 16 batch rows: M = 6144,
 // K = 8192, B = 32 18.98 against 20.24); above, 4 waves (two tiles per wave
 // from 9 batch rows). The direct tiles stay at M = 28672, K = 8192 up to 8
@@ -614,6 +653,11 @@ int launch_reuse_lds(const Launch& L, const uint4* p, const uint16_t* s, const u
 // 4.60, B = 5 4.61 against 4.77).
 int launch_reuse_tiles(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x,
                        uint16_t* y, int M, int K, int B) {
+  if ((K / DK_GROUP_SIZE) % 2 == 0 && aligned(s, 4)) {
+    const int rt = reuse_pf_rt(M, K, B);
+    if (rt == 1) return launch_reuse_pf<4, 1>(L, p, s, x, y, M, K, B);
+    if (rt == 2) return launch_reuse_pf<4, 2>(L, p, s, x, y, M, K, B);
+  }
   if (M > 2048 && M <= 4096 && K <= 4096 && B <= 5)
     return launch_reuse<8, 1, 2>(L, p, s, x, y, M, K, B);
   if (M > 8192) {
@@ -625,13 +669,19 @@ int launch_reuse_tiles(const Launch& L, const uint4* p, const uint16_t* s, const
     return B <= 16 ? launch_reuse_lds<8, 2>(L, p, s, x, y, M, K, B)
                    : launch_reuse_lds<4, 2>(L, p, s, x, y, M, K, B);
   if (M > 2048 && B > 16) return launch_reuse_lds<8, 2>(L, p, s, x, y, M, K, B);
-  if (M > 2048 && B <= 8 && K <= 8192) return launch_reuse_lds<8, 1>(L, p, s, x, y, M, K, B);
-  // Up to 2048 rows of 8192 weights or more, from 8 batch rows: blocks of
+  if (M > 2048 && B >= 6 && B <= 8 && K <= 8192) return launch_reuse_lds<8, 1>(L, p, s, x, y, M, K, B);
+  // Up to 2048 rows of 8192 weights or more, from 9 batch rows: blocks of
   // four groups, 8 waves (one block per wave at K = 8192; us, against 16
   // waves with blocks of two): M = 2048, K = 16384, B = 16 12.92 (13.81),
-  // B = 32 12.91 (13.45); M = 2048, K = 8192, B = 8 6.94 (7.17), B = 16 8.04
-  // (8.34). At M = K = 4096 they lose (B = 16: 5.83 against 5.61).
-  if (M <= 2048 && K >= 8192 && B >= 8) return launch_reuse_lds<8, 1, 4>(L, p, s, x, y, M, K, B);
+  // B = 32 12.91 (13.45); M = 2048, K = 8192, B = 16 8.04 (8.34). At 8
+  // batch rows, and above 32 at M <= 1024, blocks of two with 8 waves
+  // (against blocks of four): M = 2048, K = 8192, B = 8 6.76 (7.06);
+  // M = 1024, K = 8192, B = 33 6.63 (7.39). At M = K = 4096 blocks of four
+  // lose (B = 16: 5.83 against 5.61).
+  if (M <= 2048 && K >= 8192 && B >= 8) {
+    if (B == 8 || (M <= 1024 && B > 32)) return launch_reuse_lds<8, 1>(L, p, s, x, y, M, K, B);
+    return launch_reuse_lds<8, 1, 4>(L, p, s, x, y, M, K, B);
+  }
   return launch_reuse_lds<16, 1>(L, p, s, x, y, M, K, B);
 }
 
@@ -639,20 +689,18 @@ int launch_reuse_tiles(const Launch& L, const uint4* p, const uint16_t* s, const
 // that the down projection's split-K workspace after it stays aligned.
 size_t mlp_h_bytes(int I, int B) { return ((size_t)B * (size_t)I * sizeof(uint16_t) + 255) / 256 * 256; }
 
-// Split-K tiles: S workgroups per set of RT tiles, the tickets (8 bytes per
-// set) first in the workspace, then the fp32 partials [S][B][M].
-constexpr int kSplitRT = 2;
-constexpr int kSplitS = 4;
-
+// Split-K tiles: S workgroups per tile, the tickets (8 bytes per tile and
+// batch tile) first in the workspace, then the fp32 partials [S][B][M].
 size_t split_tickets(int M, int B) {
-  return (size_t)((M + 16 * kSplitRT - 1) / (16 * kSplitRT)) *
-         (size_t)((B + dk::kReuseBatch - 1) / dk::kReuseBatch);
+  return (size_t)((M + 15) / 16) * (size_t)((B + dk::kReuseBatch - 1) / dk::kReuseBatch);
 }
 
 size_t split_ticket_bytes(int M, int B) { return (split_tickets(M, B) * 8 + 255) / 256 * 256; }
 
-size_t split_workspace_bytes(int M, int B) {
-  return split_ticket_bytes(M, B) + (size_t)kSplitS * B * M * sizeof(float);
+int reuse_split_slices(int M, int K, int B);
+
+size_t split_workspace_bytes(int M, int K, int B) {
+  return split_ticket_bytes(M, B) + (size_t)reuse_split_slices(M, K, B) * B * M * sizeof(float);
 }
 
 // Generation of a split call (take_ticket): distinct for every launch in a
@@ -663,15 +711,22 @@ unsigned long long next_gen() {
   return (g_ticket_gen.fetch_add(1ull, std::memory_order_relaxed) & ((1ull << 58) - 1ull)) << 6;
 }
 
+// The double-buffered split tiles (4 waves, one tile each) where the scales
+// come in pairs; else the tiles that load the MFMA operands directly, two
+// per wave of 8 (their tickets, one per pair of tiles, fit the same
+// workspace).
 int launch_reuse_split(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x,
                        uint16_t* y, int M, int K, int B, void* workspace) {
+  const int S = reuse_split_slices(M, K, B);
   auto* tickets = static_cast<unsigned long long*>(workspace);
   auto* partials =
       reinterpret_cast<float*>(static_cast<char*>(workspace) + split_ticket_bytes(M, B));
-  const dim3 grid((M + 16 * kSplitRT - 1) / (16 * kSplitRT),
-                  (B + dk::kReuseBatch - 1) / dk::kReuseBatch, kSplitS);
-  return L("reuse split launch", dk::gemv_reuse_split<8, kSplitRT, 2>, grid, dim3(8 * 64), 0, p, s,
-           x, y, partials, tickets, next_gen(), M, K, B);
+  const int bt = (B + dk::kReuseBatch - 1) / dk::kReuseBatch;
+  if ((K / DK_GROUP_SIZE) % 2 == 0 && aligned(s, 4))
+    return L("reuse split launch", dk::gemv_reuse_split_pf<4, 1>, dim3((M + 15) / 16, bt, S),
+             dim3(4 * 64), 0, p, s, x, y, partials, tickets, next_gen(), M, K, B);
+  return L("reuse split launch", dk::gemv_reuse_split<8, 2, 2>, dim3((M + 31) / 32, bt, S),
+           dim3(8 * 64), 0, p, s, x, y, partials, tickets, next_gen(), M, K, B);
 }
 
 enum class ReuseShape { kStream, kTiles };
@@ -686,35 +741,49 @@ enum class ReuseShape { kStream, kTiles };
 //   M = 3072, K = 8192,  B = 3: tiles 6.40 (stream 7.11)
 //   M = K = 4096,        B = 3: stream 4.55 (tiles 4.60)
 //   M = 6144, K = 8192,  B = 3: tiles 9.14 (stream 10.45)
+//   M = 11008, K = 4096, B = 3: tiles 7.82 (stream 8.51)
+//   M = 2560, K = 8192,  B = 4: tiles 6.27 (stream 9.61)
 // Up to 512 rows the streaming kernel keeps every batch up to 32 rows (M =
 // 512, K = 8320, B = 32: 11.67 against 11.47 for the earlier tiles); it also
-// keeps four batch rows below 3072 rows and up to eight at M <= 2048 on rows
-// shorter than 8192 weights, where the earlier tiles lost and no sweep point
-// says otherwise.
+// keeps up to eight batch rows at M <= 2048 on rows shorter than 8192
+// weights, where the earlier tiles lost and no sweep point says otherwise.
 ReuseShape reuse_shape(int M, int K, int B) {
   if (B <= 2 || M <= 128) return ReuseShape::kStream;
   if (M <= 512) return B <= 32 ? ReuseShape::kStream : ReuseShape::kTiles;
   if (M <= 1024) return B < 12 ? ReuseShape::kStream : ReuseShape::kTiles;
   if (M <= 2048 && (B <= 4 || (B <= 8 && K < 8192))) return ReuseShape::kStream;
-  if (B == 4 && M < 3072) return ReuseShape::kStream;
   if (B == 3) {
-    const bool tiles = K >= 8192 || (size_t)M * (size_t)K >= ((size_t)1 << 27) ||
+    const bool tiles = K >= 8192 || M > 8192 || (size_t)M * (size_t)K >= ((size_t)1 << 27) ||
                        (M >= 3072 && K > 4096 && K < 8192);
     return tiles ? ReuseShape::kTiles : ReuseShape::kStream;
   }
   return ReuseShape::kTiles;
 }
 
-// The tiles split K over workgroups, given a workspace, only for rows longer
-// than 8192 weights at M <= 1024 (M / 16 tiles cover too few CUs); the
-// reduction across workgroups costs several microseconds on this 8-XCD part
-// (the partials and tickets pass the non-coherent L2s), and the LDS-staged
-// tiles beat it wherever else it ran (us, split-K in brackets): M = 2048,
-// K = 16384: B = 16 13.65 (16.30), B = 32 13.31 (19.75); M = 4096,
-// K = 11008, B = 32 13.24 (24.79); M = 3072, K = 8192, B = 32 10.58 (21.07).
-bool reuse_split(int M, int K, int B) {
-  return reuse_shape(M, K, B) == ReuseShape::kTiles && K > 8192 && M <= 1024;
+// The tiles split K over S workgroups per tile, given a workspace, where a
+// tile per workgroup leaves most CUs idle and the rows are long: up to 64
+// tiles (M <= 1024 at 16 batch rows) on rows of 16384+ weights, up to 128
+// on rows of 28672+. The reduction across workgroups costs several
+// microseconds on this 8-XCD part (the partials and tickets pass the
+// non-coherent L2s), so the rows must be long enough to repay it. From the
+// sweep of the double-buffered tiles (us; single-pass tiles, then the
+// earlier split of 8 waves with two tiles each, in brackets):
+//   M = 1024, K = 16384, B = 16: S = 2 11.61 (12.11, 15.75)
+//   M = 1024, K = 28672, B = 16: S = 4 14.63 (20.97, 20.36)
+//   M = 512,  K = 28672, B = 33: S = 2 14.74 (17.87, 20.60)
+//   M = 600,  K = 65536, B = 16: S = 4 19.44 (40.85, 32.77)
+// and single-pass where it lost: M = 1024, K = 28672, B = 33: 18.27 (S = 2
+// 24.18); M = 1024, K = 14336, B = 16: 11.44 (S = 2 11.32, S = 4 12.13).
+int reuse_split_slices(int M, int K, int B) {
+  if (reuse_shape(M, K, B) != ReuseShape::kTiles || M > 1024) return 0;
+  const long long tiles = (long long)((M + 15) / 16) * ((B + dk::kReuseBatch - 1) / dk::kReuseBatch);
+  if (tiles <= 64 && K >= 28672) return 4;
+  if (tiles <= 64 && K >= 16384) return 2;
+  if (tiles <= 128 && K >= 28672) return 2;
+  return 0;
 }
+
+bool reuse_split(int M, int K, int B) { return reuse_split_slices(M, K, B) > 0; }
 
 size_t v3_lds_bytes(int K) { return (size_t)kWavesPerBlock * (K / DK_GROUP_SIZE) * sizeof(uint16_t); }
 
@@ -891,7 +960,7 @@ int dk_gemv_validate(int M, int K, int B, const dk_gemv_config* cfg) {
 size_t dk_gemv_workspace_bytes(int M, int K, int B, const dk_gemv_config* cfg) {
   if (dk_gemv_validate(M, K, B, cfg) != DK_OK) return 0;
   if (M <= 0 || K <= 0 || B <= 0) return 0;
-  if (cfg->reuse_weights) return reuse_split(M, K, B) ? split_workspace_bytes(M, B) : 0;
+  if (cfg->reuse_weights) return reuse_split(M, K, B) ? split_workspace_bytes(M, K, B) : 0;
   return 0;
 }
 

@@ -865,20 +865,22 @@ struct ReuseDmaLds {
   uint4 w[KS][RT * 16 * 4 * SG];
 };
 
-// The block loop of the LDS-staged tiles: tile t's weights and scales
-// through descriptors rw[t], rs[t] (rows 0..15 relative to them, G groups
-// per row), x of batch rows bt0 .. bt0 + 15 (those below B) through rx with
-// rows K * 2 bytes apart. acc[t] is this lane's part of tile t's fp32 16x16
-// result over the wave's blocks of SG (2 or 4) groups (groups SG wave ..
-// SG wave + SG - 1, then every SG KS). kPairs: the scales of two groups in
-// one 4-byte load (an even number of groups per row, 4-byte aligned).
-template <int KS, int RT, bool kPairs, int SG = 2>
-__device__ __forceinline__ void reuse_lds_loop(f4_t (&acc)[RT], uint4* xbuf, uint4* wbuf,
-                                               const __amdgpu_buffer_rsrc_t (&rw)[RT],
-                                               const __amdgpu_buffer_rsrc_t (&rs)[RT],
-                                               __amdgpu_buffer_rsrc_t rx, int bt0, int B, int K,
-                                               int G, int lane, int wave) {
-  static_assert(SG == 2 || SG == 4, "blocks of two or four groups");
+// One block of SG (2 or 4) groups of the LDS-staged tiles, groups g0 ..
+// g0 + SG - 1: tile t's weights and scales through descriptors rw[t], rs[t]
+// (rows 0..15 relative to them, G groups per row), x of batch rows bt0 ..
+// bt0 + 15 (those below B; nxl loads cover them) through rx with rows K * 2
+// bytes apart, added into acc[t], this lane's part of tile t's fp32 16x16
+// result. kTail: the block may run past group G - 1, so each load checks
+// its group (a block that ends inside the row needs no check, and its loads
+// issue with no address arithmetic beyond the loop's increments). kPairs:
+// the scales of two groups in one 4-byte load (an even number of groups per
+// row, 4-byte aligned).
+template <int RT, bool kPairs, int SG, bool kTail>
+__device__ __forceinline__ void reuse_lds_block(f4_t (&acc)[RT], uint4* xbuf, uint4* wbuf,
+                                                const __amdgpu_buffer_rsrc_t (&rw)[RT],
+                                                const __amdgpu_buffer_rsrc_t (&rs)[RT],
+                                                __amdgpu_buffer_rsrc_t rx, int bt0, int B, int K,
+                                                int G, int lane, int g0, int nxl) {
   constexpr int kWC = 4 * SG;   // weight chunks per row of a block
   constexpr int kWR = 64 / kWC;  // weight rows per load
   constexpr int kXC = 16 * SG;  // x chunks per batch row of a block
@@ -886,96 +888,115 @@ __device__ __forceinline__ void reuse_lds_loop(f4_t (&acc)[RT], uint4* xbuf, uin
   const int nck = K >> 5;
   const int kq = lane >> 4;
   const int r_lane = lane & 15;
+  // Weights: load i covers rows kWR (i % (16 / kWR)) .. + kWR - 1 of tile
+  // i / (16 / kWR), lane l chunk l % kWC of row kWR (i % (16 / kWR)) + l /
+  // kWC (chunk c = group c / 4 of the block, bytes 16 (c % 4) of it).
+#pragma unroll
+  for (int i = 0; i < RT * 16 / kWR; ++i) {
+    const int r = kWR * (i % (16 / kWR)) + lane / kWC;
+    const int c = (lane % kWC) ^ stage_swizzle<kWC>(r);
+    const int off = !kTail || g0 * 4 + c < G * 4 ? r * nck * 16 + (g0 * 4 + c) * 16 : kOutOfRange;
+    // A local copy of the descriptor: given the array element itself, the
+    // host pass leaves the kernel's launch stub undefined.
+    const __amdgpu_buffer_rsrc_t rwt = rw[i / (16 / kWR)];
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rwt, (lds_void_ptr)(wbuf + i * 64), 16, off, 0, 0,
+                                             kLoadNonTemporal);
+  }
+  // x: load i covers batch rows bt0 + kXR i .. + kXR - 1, lane l chunk
+  // l % kXC of row kXR i + l / kXC (chunk c = group c / 16, bytes 16 (c % 16)).
+#pragma unroll
+  for (int i = 0; i < 16 / kXR; ++i) {
+    if (i < nxl) {
+      const int bb = kXR * i + lane / kXC;
+      const int p = lane % kXC;
+      const int c = (p & ~15) | ((p ^ stage_swizzle<kXC>(bb)) & 15);
+      const bool ok = bt0 + bb < B && (!kTail || g0 * 16 + c < G * 16);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rx, (lds_void_ptr)(xbuf + i * 64), 16,
+          ok ? (bt0 + bb) * K * 2 + (g0 * 16 + c) * 16 : kOutOfRange, 0, 0, 0);
+    }
+  }
+  // Scales of this lane's four D rows: two groups in one 4-byte load where
+  // the scales allow (an even number of groups, so g0 + 2v + 1 < G when
+  // g0 + 2v < G).
+  float sc[RT][SG][4];
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if constexpr (kPairs) {
+#pragma unroll
+        for (int u2 = 0; u2 < SG / 2; ++u2) {
+          const int g = g0 + 2 * u2;
+          const uint32_t two = __builtin_amdgcn_raw_buffer_load_b32(
+              rs[t], !kTail || g < G ? ((4 * kq + v) * G + g) * 2 : kOutOfRange, 0, 0);
+          sc[t][2 * u2][v] = h2f((uint16_t)two);
+          sc[t][2 * u2 + 1][v] = h2f((uint16_t)(two >> 16));
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < SG; ++u) {
+          const int off = !kTail || g0 + u < G ? ((4 * kq + v) * G + g0 + u) * 2 : kOutOfRange;
+          sc[t][u][v] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs[t], off, 0, 0));
+        }
+      }
+    }
+  // Every load of the block, LDS writes included, has landed.
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int u = 0; u < SG; ++u) {
+    h8_t xp[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int xc = 16 * u + 4 * kq + j;
+      xp[j] = pair_x8(
+          xbuf[r_lane * kXC + ((xc & ~15) | ((xc ^ stage_swizzle<kXC>(r_lane)) & 15))]);
+    }
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      const int wc = (4 * u + kq) ^ stage_swizzle<kWC>(r_lane);
+      const uint4 wv = wbuf[(16 * t + r_lane) * kWC + wc];
+      const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+      f4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_word_h8(words[j]), xp[j], c, 0, 0, 0);
+      // A group past G loaded zero weights, so it adds nothing.
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(c[v], sc[t][u][v], acc[t][v]);
+    }
+  }
+  // The reads above have returned before the next block's loads write the
+  // buffers.
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// The block loop of the LDS-staged tiles: acc[t] over the wave's blocks of
+// SG groups (groups SG wave .. SG wave + SG - 1, then every SG KS), the
+// blocks that end inside the row first, then the one that runs past its
+// end if the row's group count is not a multiple of SG.
+template <int KS, int RT, bool kPairs, int SG = 2>
+__device__ __forceinline__ void reuse_lds_loop(f4_t (&acc)[RT], uint4* xbuf, uint4* wbuf,
+                                               const __amdgpu_buffer_rsrc_t (&rw)[RT],
+                                               const __amdgpu_buffer_rsrc_t (&rs)[RT],
+                                               __amdgpu_buffer_rsrc_t rx, int bt0, int B, int K,
+                                               int G, int lane, int wave) {
+  static_assert(SG == 2 || SG == 4, "blocks of two or four groups");
+  constexpr int kXR = 64 / (16 * SG);  // batch rows per x load
   // x loads with a batch row below B (wave-uniform).
   const int nxl = min(16 / kXR, (max(0, min(16, B - bt0)) + kXR - 1) / kXR);
 #pragma unroll
   for (int t = 0; t < RT; ++t) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
-  for (int g0 = SG * wave; g0 < G; g0 += SG * KS) {
-    // Weights: load i covers rows kWR (i % (16 / kWR)) .. + kWR - 1 of tile
-    // i / (16 / kWR), lane l chunk l % kWC of row kWR (i % (16 / kWR)) + l /
-    // kWC (chunk c = group c / 4 of the block, bytes 16 (c % 4) of it).
-#pragma unroll
-    for (int i = 0; i < RT * 16 / kWR; ++i) {
-      const int r = kWR * (i % (16 / kWR)) + lane / kWC;
-      const int c = (lane % kWC) ^ stage_swizzle<kWC>(r);
-      const int off = g0 * 4 + c < G * 4 ? r * nck * 16 + (g0 * 4 + c) * 16 : kOutOfRange;
-      // A local copy of the descriptor: given the array element itself, the
-      // host pass leaves the kernel's launch stub undefined.
-      const __amdgpu_buffer_rsrc_t rwt = rw[i / (16 / kWR)];
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rwt, (lds_void_ptr)(wbuf + i * 64), 16, off, 0, 0,
-                                               kLoadNonTemporal);
-    }
-    // x: load i covers batch rows bt0 + kXR i .. + kXR - 1, lane l chunk
-    // l % kXC of row kXR i + l / kXC (chunk c = group c / 16, bytes 16 (c % 16)).
-#pragma unroll
-    for (int i = 0; i < 16 / kXR; ++i) {
-      if (i < nxl) {
-        const int bb = kXR * i + lane / kXC;
-        const int p = lane % kXC;
-        const int c = (p & ~15) | ((p ^ stage_swizzle<kXC>(bb)) & 15);
-        const bool ok = bt0 + bb < B && g0 * 16 + c < G * 16;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rx, (lds_void_ptr)(xbuf + i * 64), 16,
-            ok ? (bt0 + bb) * K * 2 + (g0 * 16 + c) * 16 : kOutOfRange, 0, 0, 0);
-      }
-    }
-    // Scales of this lane's four D rows: two groups in one 4-byte load where
-    // the scales allow (an even number of groups, so g0 + 2v + 1 < G when
-    // g0 + 2v < G).
-    float sc[RT][SG][4];
-#pragma unroll
-    for (int t = 0; t < RT; ++t)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        if constexpr (kPairs) {
-#pragma unroll
-          for (int u2 = 0; u2 < SG / 2; ++u2) {
-            const int g = g0 + 2 * u2;
-            const uint32_t two = __builtin_amdgcn_raw_buffer_load_b32(
-                rs[t], g < G ? ((4 * kq + v) * G + g) * 2 : kOutOfRange, 0, 0);
-            sc[t][2 * u2][v] = h2f((uint16_t)two);
-            sc[t][2 * u2 + 1][v] = h2f((uint16_t)(two >> 16));
-          }
-        } else {
-#pragma unroll
-          for (int u = 0; u < SG; ++u) {
-            const int off = g0 + u < G ? ((4 * kq + v) * G + g0 + u) * 2 : kOutOfRange;
-            sc[t][u][v] = h2f(__builtin_amdgcn_raw_buffer_load_b16(rs[t], off, 0, 0));
-          }
-        }
-      }
-    // Every load of the block, LDS writes included, has landed.
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int u = 0; u < SG; ++u) {
-      h8_t xp[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int xc = 16 * u + 4 * kq + j;
-        xp[j] = pair_x8(
-            xbuf[r_lane * kXC + ((xc & ~15) | ((xc ^ stage_swizzle<kXC>(r_lane)) & 15))]);
-      }
-#pragma unroll
-      for (int t = 0; t < RT; ++t) {
-        const int wc = (4 * u + kq) ^ stage_swizzle<kWC>(r_lane);
-        const uint4 wv = wbuf[(16 * t + r_lane) * kWC + wc];
-        const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
-        f4_t c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          c = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_word_h8(words[j]), xp[j], c, 0, 0, 0);
-        // A group past G loaded zero weights, so it adds nothing.
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(c[v], sc[t][u][v], acc[t][v]);
-      }
-    }
-    // The reads above have returned before the next block's loads write the
-    // buffers.
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-  }
+  int g0 = SG * wave;
+  for (; g0 + SG <= G; g0 += SG * KS)
+    reuse_lds_block<RT, kPairs, SG, false>(acc, xbuf, wbuf, rw, rs, rx, bt0, B, K, G, lane, g0,
+                                           nxl);
+  if (g0 < G)
+    reuse_lds_block<RT, kPairs, SG, true>(acc, xbuf, wbuf, rw, rs, rx, bt0, B, K, G, lane, g0,
+                                          nxl);
 }
 
 // Partials of the LDS-staged tiles over each wave's own x buffer (no other
@@ -1046,6 +1067,308 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_lds(const uint4* __restric
   }
 }
 
+// ---------------------------------------------------------------------------
+// Double-buffered LDS-staged tiles: blocks of two groups with paired scales,
+// block n + 1's loads issued into one buffer before block n is computed
+// from the other. Per wave two buffers, each one block: 16 batch rows x 32
+// chunks of x, 16 RT rows x 8 chunks of weights, and the scale pairs of
+// tile t's row r in dword 64 t + r (the scale loads of lanes 16-63 land
+// zeros in the rest). The scales come through LDS like the rest, so a
+// block's loads write no register: the buffers reach each step as
+// __restrict__ pointers, which lets the compiler wait for the block being
+// computed without waiting for the one being loaded.
+// ---------------------------------------------------------------------------
+template <int KS, int RT>
+struct ReusePfLds {
+  uint4 x[2][KS][16 * 32];
+  uint4 w[2][KS][RT * 16 * 8];
+  uint4 s[2][KS][RT * 16];
+  int last;  // the split-K form's ticket result
+  static_assert(sizeof(x[0][0]) >= 256 * RT * sizeof(float), "partials fit an x buffer");
+};
+
+// Loads per block and wave: two per tile of weights, eight of x, one per
+// tile of scales.
+template <int RT>
+constexpr int kReusePfLoads = 3 * RT + 8;
+
+// s_waitcnt vmcnt(N) alone (the gfx9 encoding, expcnt and lgkmcnt at their
+// maximum).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// A window of each row: groups [gbeg, gbeg + G) of a K-long row, tile t's
+// weights and scales through descriptors rw[t], rs[t] (starting at group
+// gbeg of the tile's first row; rows K / 2 bytes and Gs scales apart), x of
+// batch rows bt0 .. bt0 + 15 (those below B) through rx (rows K * 2 bytes
+// apart).
+// (The descriptors travel as arrays beside it: a struct holding them is
+// rejected by the host pass of a template instantiated from a kernel.)
+struct ReuseWindow {
+  int bt0, B, K, G, Gs, gbeg;
+};
+
+// Issues the loads of the block at window group g0 into xb, wb, sb: every
+// x load, those of batch rows >= B out of range, so that each block issues
+// the same number of loads.
+template <int RT>
+__device__ __forceinline__ void reuse_pf_issue(uint4* __restrict__ xb, uint4* __restrict__ wb,
+                                               uint4* __restrict__ sb,
+                                               const __amdgpu_buffer_rsrc_t (&rw)[RT],
+                                               const __amdgpu_buffer_rsrc_t (&rs)[RT],
+                                               __amdgpu_buffer_rsrc_t rx, const ReuseWindow& win,
+                                               int lane, int g0) {
+  // Weights: load i covers rows 8 (i % 2) .. + 7 of tile i / 2, lane l
+  // chunk l % 8 of row 8 (i % 2) + l / 8 (chunk c = group c / 4 of the
+  // block, bytes 16 (c % 4) of it).
+#pragma unroll
+  for (int i = 0; i < 2 * RT; ++i) {
+    const int r = 8 * (i % 2) + lane / 8;
+    const int c = (lane % 8) ^ stage_swizzle<8>(r);
+    const __amdgpu_buffer_rsrc_t rwt = rw[i / 2];
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rwt, (lds_void_ptr)(wb + i * 64), 16,
+                                             r * (win.K / 2) + (g0 * 4 + c) * 16, 0, 0,
+                                             kLoadNonTemporal);
+  }
+  // x: load i covers batch rows bt0 + 2 i, bt0 + 2 i + 1, lane l chunk
+  // l % 32 of row 2 i + l / 32 (chunk c = group c / 16, bytes 16 (c % 16)).
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int bb = 2 * i + lane / 32;
+    const int p = lane % 32;
+    const int c = (p & 16) | ((p ^ stage_swizzle<32>(bb)) & 15);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rx, (lds_void_ptr)(xb + i * 64), 16,
+        win.bt0 + bb < win.B ? (win.bt0 + bb) * win.K * 2 + (win.gbeg + g0) * 256 + c * 16
+                             : kOutOfRange,
+        0, 0, 0);
+  }
+  // Scale pairs: lane r < 16 row r of tile t.
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const __amdgpu_buffer_rsrc_t rst = rs[t];
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rst, (lds_void_ptr)(sb + 16 * t), 4,
+                                             lane < 16 ? (lane * win.Gs + g0) * 2 : kOutOfRange,
+                                             0, 0, 0);
+  }
+}
+
+// One step: with kNext, issues the block at gn into nx, nw, ns and waits
+// for all but those loads; else waits for every load. Then adds the block
+// in cx, cw, cs into acc.
+template <int RT, bool kNext>
+__device__ __forceinline__ void reuse_pf_step(f4_t (&acc)[RT], const uint4* __restrict__ cx,
+                                              const uint4* __restrict__ cw,
+                                              const uint4* __restrict__ cs, uint4* __restrict__ nx,
+                                              uint4* __restrict__ nw, uint4* __restrict__ ns,
+                                              const __amdgpu_buffer_rsrc_t (&rw)[RT],
+                                              const __amdgpu_buffer_rsrc_t (&rs)[RT],
+                                              __amdgpu_buffer_rsrc_t rx, const ReuseWindow& win,
+                                              int lane, int gn) {
+  const int kq = lane >> 4;
+  const int r_lane = lane & 15;
+  if constexpr (kNext) {
+    // The previous step's reads of the buffers about to be refilled have
+    // returned (its MFMAs consumed them; this orders the loads after them).
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_sched_barrier(0);
+    reuse_pf_issue<RT>(nx, nw, ns, rw, rs, rx, win, lane, gn);
+    wait_vmcnt<kReusePfLoads<RT>>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  uint32_t sc[RT][4];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const uint4 s4 = cs[16 * t + kq];  // rows 4 kq .. 4 kq + 3 of tile t
+    sc[t][0] = s4.x;
+    sc[t][1] = s4.y;
+    sc[t][2] = s4.z;
+    sc[t][3] = s4.w;
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    h8_t xp[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int xc = 16 * u + 4 * kq + j;
+      xp[j] = pair_x8(cx[r_lane * 32 + ((xc & 16) | ((xc ^ stage_swizzle<32>(r_lane)) & 15))]);
+    }
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      const int wc = (4 * u + kq) ^ stage_swizzle<8>(r_lane);
+      const uint4 wv = cw[(16 * t + r_lane) * 8 + wc];
+      const uint32_t words[4] = {wv.x, wv.y, wv.z, wv.w};
+      f4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(unpack_word_h8(words[j]), xp[j], c, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        acc[t][v] = __builtin_fmaf(c[v], h2f((uint16_t)(sc[t][v] >> (16 * u))), acc[t][v]);
+    }
+  }
+}
+
+// acc[t] over the wave's blocks of the window (window groups 2 wave, 2 wave
+// + 1, then every 2 KS; G even), two buffers in turn.
+template <int KS, int RT>
+__device__ __forceinline__ void reuse_pf_loop(f4_t (&acc)[RT], ReusePfLds<KS, RT>& lds,
+                                              const __amdgpu_buffer_rsrc_t (&rw)[RT],
+                                              const __amdgpu_buffer_rsrc_t (&rs)[RT],
+                                              __amdgpu_buffer_rsrc_t rx, const ReuseWindow& win,
+                                              int lane, int wave) {
+#pragma unroll
+  for (int t = 0; t < RT; ++t) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+  const int nb = max(0, (win.G / 2 - wave + KS - 1) / KS);  // blocks of this wave
+  if (nb == 0) return;
+  uint4* xa = lds.x[0][wave];
+  uint4* xb = lds.x[1][wave];
+  uint4* wa = lds.w[0][wave];
+  uint4* wb = lds.w[1][wave];
+  uint4* sa = lds.s[0][wave];
+  uint4* sb = lds.s[1][wave];
+  int g = 2 * wave;
+  reuse_pf_issue<RT>(xa, wa, sa, rw, rs, rx, win, lane, g);
+  for (int n = 0;;) {
+    if (n + 1 < nb) {
+      reuse_pf_step<RT, true>(acc, xa, wa, sa, xb, wb, sb, rw, rs, rx, win, lane, g + 2 * KS);
+    } else {
+      reuse_pf_step<RT, false>(acc, xa, wa, sa, xb, wb, sb, rw, rs, rx, win, lane, 0);
+      break;
+    }
+    ++n;
+    g += 2 * KS;
+    if (n + 1 < nb) {
+      reuse_pf_step<RT, true>(acc, xb, wb, sb, xa, wa, sa, rw, rs, rx, win, lane, g + 2 * KS);
+    } else {
+      reuse_pf_step<RT, false>(acc, xb, wb, sb, xa, wa, sa, rw, rs, rx, win, lane, 0);
+      break;
+    }
+    ++n;
+    g += 2 * KS;
+  }
+}
+
+// Tile t's KS wave partials, published in each wave's first x buffer (no
+// other wave touches it) and added in wave order after a barrier.
+template <int KS, int RT>
+__device__ __forceinline__ f4_t reuse_pf_partials(ReusePfLds<KS, RT>& lds, const f4_t (&acc)[RT],
+                                                  int wave, int lane) {
+  float* part = reinterpret_cast<float*>(lds.x[0][wave]);
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) part[(t * 64 + lane) * 4 + v] = acc[t][v];
+  __syncthreads();
+  f4_t sum = {0.f, 0.f, 0.f, 0.f};
+  if (wave < RT) {
+    for (int w2 = 0; w2 < KS; ++w2) {
+      const float* pw = reinterpret_cast<const float*>(lds.x[0][w2]);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sum[v] += pw[(wave * 64 + lane) * 4 + v];
+    }
+  }
+  return sum;
+}
+
+// The single-pass double-buffered tiles: RT tiles of 16 rows x 16 batch
+// rows per workgroup, KS waves splitting each row's blocks. Needs an even
+// number of groups per row and 4-byte aligned scales.
+template <int KS, int RT>
+__global__ __launch_bounds__(KS * 64) void gemv_reuse_pf(const uint4* __restrict__ packed,
+                                                         const uint16_t* __restrict__ scales,
+                                                         const uint4* __restrict__ x4,
+                                                         uint16_t* __restrict__ y, int M, int K,
+                                                         int B) {
+  static_assert(KS >= RT, "wave t sums tile t");
+  write_stamp(DK_STAMP_REUSE);
+  __shared__ ReusePfLds<KS, RT> lds;
+  const int G = K >> 7;
+  const int nck = K >> 5;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = blockIdx.x * 16 * RT;
+  __amdgpu_buffer_rsrc_t rw[RT], rs[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const int rows = __builtin_amdgcn_readfirstlane(max(0, min(16, M - row0 - 16 * t)));
+    const int rbase = rows > 0 ? row0 + 16 * t : 0;
+    rw[t] = buffer_rsrc(packed + (size_t)rbase * nck, (uint32_t)(rows * (K / 2)));
+    rs[t] = buffer_rsrc(scales + (size_t)rbase * G, (uint32_t)(rows * G * 2));
+  }
+  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
+  ReuseWindow win;
+  win.bt0 = blockIdx.y * kReuseBatch;
+  win.B = B;
+  win.K = K;
+  win.G = G;
+  win.Gs = G;
+  win.gbeg = 0;
+  f4_t acc[RT];
+  reuse_pf_loop<KS, RT>(acc, lds, rw, rs, rx, win, lane, wave);
+  const f4_t sum = reuse_pf_partials<KS, RT>(lds, acc, wave, lane);
+  const int b = win.bt0 + (lane & 15);
+  if (wave < RT && b < B) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int orow = row0 + 16 * wave + 4 * (lane >> 4) + v;
+      if (orow < M) y[(size_t)b * M + orow] = f2h(sum[v]);
+    }
+  }
+}
+
+// The end of a split-K tile workgroup (blockIdx.z = slice z of gridDim.z):
+// wave t < RT holds tile t's sums over the slice for its lane's four rows
+// and batch column b in sum. Writes them to partials[z][b][row]
+// (agent-scope stores, past the non-coherent L2s) and takes a ticket; the
+// last of the slices to arrive adds them in order z = 0, 1, ...
+// (bit-reproducible) and writes y.
+template <int RT>
+__device__ __forceinline__ void reuse_split_finish(const f4_t& sum, int& last,
+                                                   uint16_t* __restrict__ y,
+                                                   float* __restrict__ partials,
+                                                   unsigned long long* __restrict__ tickets,
+                                                   unsigned long long gen, int row0, int b, int M,
+                                                   int B, int wave, int lane) {
+  const int S = gridDim.z;
+  const int split = blockIdx.z;
+  const int kq = lane >> 4;
+  if (wave < RT && b < B) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int orow = row0 + 16 * wave + 4 * kq + v;
+      if (orow < M)
+        __hip_atomic_store(&partials[((size_t)split * B + b) * M + orow], sum[v], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // Every wave's partial stores are complete before the ticket is taken.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  unsigned long long* ticket = &tickets[blockIdx.y * gridDim.x + blockIdx.x];
+  if (threadIdx.x == 0) last = take_ticket(ticket, gen, S);
+  __syncthreads();
+  if (!last) return;
+  if (wave < RT && b < B) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int orow = row0 + 16 * wave + 4 * kq + v;
+      if (orow >= M) continue;
+      float total = 0.f;
+      for (int z = 0; z < S; ++z)
+        total += __hip_atomic_load(&partials[((size_t)z * B + b) * M + orow], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+      y[(size_t)b * M + orow] = f2h(total);
+    }
+  }
+  if (threadIdx.x == 0) release_ticket(ticket, gen);
+}
+
 // Split-K form for rows too few to give every CU a tile with the whole row:
 // grid.z = S workgroups share each set of RT tiles, workgroup z covering
 // groups [z * ceil(G / S), +ceil(G / S)), so each reads only its slice of
@@ -1094,38 +1417,58 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_split(
                               b < B);
   reuse_tile_publish(lds, acc, wave, lane);
   __syncthreads();
-  if (wave < RT) {
-    const f4_t sum = reuse_tile_sum(lds, wave, lane);
-    if (b < B) {
+  f4_t sum = {0.f, 0.f, 0.f, 0.f};
+  if (wave < RT) sum = reuse_tile_sum(lds, wave, lane);
+  reuse_split_finish<RT>(sum, last, y, partials, tickets, gen, row0, b, M, B, wave, lane);
+}
+
+// The double-buffered tiles in split-K form: grid.z = S workgroups share
+// each set of RT tiles, workgroup z covering groups [z gps, (z + 1) gps) of
+// every row, gps = 2 ceil(G / 2S) (whole blocks of two groups), then
+// reuse_split_finish. Needs an even number of groups per row and 4-byte
+// aligned scales.
+template <int KS, int RT>
+__global__ __launch_bounds__(KS * 64) void gemv_reuse_split_pf(
+    const uint4* __restrict__ packed, const uint16_t* __restrict__ scales,
+    const uint4* __restrict__ x4, uint16_t* __restrict__ y, float* __restrict__ partials,
+    unsigned long long* __restrict__ tickets, unsigned long long gen, int M, int K, int B) {
+  static_assert(KS >= RT, "wave t sums tile t");
+  write_stamp(DK_STAMP_REUSE);
+  __shared__ ReusePfLds<KS, RT> lds;
+  const int S = gridDim.z;
+  const int Gall = K >> 7;
+  const int gps = 2 * ((Gall + 2 * S - 1) / (2 * S));
+  const int gbeg = min((int)blockIdx.z * gps, Gall);
+  const int G = min(gbeg + gps, Gall) - gbeg;  // groups of this slice (even; 0 if none)
+  const int nck = K >> 5;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = blockIdx.x * 16 * RT;
+  __amdgpu_buffer_rsrc_t rw[RT], rs[RT];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int orow = row0 + 16 * wave + 4 * kq + v;
-        if (orow < M)
-          __hip_atomic_store(&partials[((size_t)split * B + b) * M + orow], sum[v],
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
+  for (int t = 0; t < RT; ++t) {
+    // Descriptors start at the slice's first group of the tile's first row
+    // and end after its last group of the tile's last row.
+    const int rows = __builtin_amdgcn_readfirstlane(max(0, min(16, M - row0 - 16 * t)));
+    const int rbase = rows > 0 ? row0 + 16 * t : 0;
+    const uint32_t wbytes = rows > 0 ? (uint32_t)((rows - 1) * (K / 2) + G * 64) : 0u;
+    const uint32_t sbytes = rows > 0 ? (uint32_t)(((rows - 1) * Gall + G) * 2) : 0u;
+    rw[t] = buffer_rsrc(packed + (size_t)rbase * nck + (size_t)gbeg * 4, wbytes);
+    rs[t] = buffer_rsrc(scales + (size_t)rbase * Gall + gbeg, sbytes);
   }
-  // Every wave's partial stores are complete before the ticket is taken.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  unsigned long long* ticket = &tickets[blockIdx.y * gridDim.x + blockIdx.x];
-  if (threadIdx.x == 0) last = take_ticket(ticket, gen, S);
-  __syncthreads();
-  if (!last) return;
-  if (wave < RT && b < B) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int orow = row0 + 16 * wave + 4 * kq + v;
-      if (orow >= M) continue;
-      float sum = 0.f;
-      for (int z = 0; z < S; ++z)
-        sum += __hip_atomic_load(&partials[((size_t)z * B + b) * M + orow], __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-      y[(size_t)b * M + orow] = f2h(sum);
-    }
-  }
-  if (threadIdx.x == 0) release_ticket(ticket, gen);
+  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
+  ReuseWindow win;
+  win.bt0 = blockIdx.y * kReuseBatch;
+  win.B = B;
+  win.K = K;
+  win.G = G;
+  win.Gs = Gall;
+  win.gbeg = gbeg;
+  f4_t acc[RT];
+  reuse_pf_loop<KS, RT>(acc, lds, rw, rs, rx, win, lane, wave);
+  const f4_t sum = reuse_pf_partials<KS, RT>(lds, acc, wave, lane);
+  reuse_split_finish<RT>(sum, lds.last, y, partials, tickets, gen, row0, win.bt0 + (lane & 15), M,
+                         B, wave, lane);
 }
 
 }  // namespace dk

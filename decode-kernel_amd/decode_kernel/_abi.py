@@ -17,7 +17,7 @@ DK_OK = 0
 DK_ERR_INVALID_ARGUMENT = 1
 DK_ERR_HIP = 2
 DK_ERR_UNSUPPORTED = 3
-DK_NOALLOC_SCRATCH_BYTES = 8 << 20  # include/decode_kernel/dk_gemv.h
+DK_NOALLOC_SCRATCH_BYTES = 512 << 10  # include/decode_kernel/dk_gemv.h
 
 
 class GemvConfig(ctypes.Structure):

@@ -20,6 +20,8 @@ _SIGNATURES = {
                     _P]),
     "dkb_v4s": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _P]),
     "dkb_reuse": (_I, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P]),
+    "dkb_reuse_split_workspace": (ctypes.c_size_t, [_I, _I, _I, _I]),
+    "dkb_reuse_split": (_I, [_I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "dkb_gate_up": (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "dkb_timestamp": (_I, [_P, _I, _P]),
     "dkb_wall_clock_khz": (_I, []),
@@ -152,14 +154,36 @@ def run_kernel(kernel: tuple, math: int, packed, scales, x, y) -> None:
 
 def reuse(kind: int, ks: int, rt: int, sg: int, pairs: bool, packed, scales, x, y) -> int:
     """The reuse path's tile kernels: kind 0 gemv_reuse<KS, RT, SG, pairs>,
-    kind 1 gemv_reuse_lds<KS, RT, pairs, SG>. Returns 3 (nothing launched)
-    for a shape not instantiated in the measurement library."""
+    kind 1 gemv_reuse_lds<KS, RT, pairs, SG>, kind 2 gemv_reuse_pf<KS, RT>
+    (SG 2, pairs). Returns 3 (nothing launched) for a shape not instantiated
+    in the measurement library."""
     m, k = packed.shape[0], packed.shape[1] * 8
     b = x.shape[0]
     rc = load().dkb_reuse(kind, ks, rt, sg, int(pairs), packed.data_ptr(), scales.data_ptr(),
                           x.data_ptr(), y.data_ptr(), m, k, b, stream_handle())
     if rc not in (0, 3):
         raise RuntimeError(f"reuse kind {kind} KS{ks} RT{rt} SG{sg}: status {rc}")
+    return rc
+
+
+def reuse_split_workspace(rt: int, s: int, m: int, b: int) -> int:
+    """Bytes of the workspace reuse_split needs: tickets, then fp32 partials."""
+    return int(load().dkb_reuse_split_workspace(rt, s, m, b))
+
+
+def reuse_split(kind: int, ks: int, rt: int, s: int, packed, scales, x, y, workspace) -> int:
+    """The split-K tile kernels, S slices per row: kind 0
+    gemv_reuse_split<KS, RT, 2>, kind 1 gemv_reuse_split_pf<KS, RT>.
+    workspace: a uint8 tensor of at least reuse_split_workspace() bytes.
+    Returns 3 (nothing launched) for a shape not instantiated."""
+    m, k = packed.shape[0], packed.shape[1] * 8
+    b = x.shape[0]
+    if workspace.numel() < reuse_split_workspace(rt, s, m, b):
+        raise ValueError("workspace too small")
+    rc = load().dkb_reuse_split(kind, ks, rt, s, packed.data_ptr(), scales.data_ptr(), x.data_ptr(),
+                                y.data_ptr(), workspace.data_ptr(), m, k, b, stream_handle())
+    if rc not in (0, 3):
+        raise RuntimeError(f"reuse split kind {kind} KS{ks} RT{rt} S{s}: status {rc}")
     return rc
 
 

@@ -75,11 +75,13 @@ void dk_gemv_config_default(dk_gemv_config* cfg);
 
 /* Bytes of device workspace dk_w4a16_gemv takes for this call: 0 for every
  * variant (v4 included) but the weight-reuse path when its MFMA tiles split
- * K over workgroups (rows longer than 8192 weights at M <= 1024 with 12 or
- * more batch rows, 33 or more at M <= 512).
- * There it is optional and 8-byte aligned: one 8-byte ticket per set of 32
- * rows and 16 batch rows, padded to 256 bytes, then fp32 partials [4, B, M];
- * without it (NULL or too small) the path runs its single-pass tiles, same
+ * K over S workgroups per tile (at M <= 1024 where the tiles run, 12 or
+ * more batch rows, 33 or more at M <= 512: S = 4 on rows of 28672+ weights
+ * with at most 64 tiles of 16 rows x 16 batch rows, S = 2 on rows of
+ * 16384+ with at most 64 tiles or 28672+ with at most 128).
+ * There it is optional and 8-byte aligned: one 8-byte ticket per tile,
+ * padded to 256 bytes, then fp32 partials [S, B, M]; at most 263168 bytes.
+ * Without it (NULL or too small) the path runs its single-pass tiles, same
  * results within rounding. It needs no clearing: each ticket carries the
  * call's generation. Calls that overlap in time need separate workspaces.
  * No counterpart in the reference, whose v4 took an fp32 [B, M] buffer
@@ -110,15 +112,16 @@ int dk_w4a16_gemv(const uint32_t* packed, const uint16_t* scales,
                   size_t workspace_bytes, hipStream_t stream);
 
 /* Size of the per-GPU device array behind dk_w4a16_gemv_noalloc. */
-#define DK_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+#define DK_NOALLOC_SCRATCH_BYTES ((size_t)512 << 10)
 
 /* dk_w4a16_gemv for callers that cannot allocate: code under HIP graph
  * capture, tight serving loops, hosts that forbid hipMalloc. No counterpart
  * in the reference. The reuse path's split-K tiles take their workspace from
- * a library-owned device array of DK_NOALLOC_SCRATCH_BYTES (8 MiB) on each
+ * a library-owned device array of DK_NOALLOC_SCRATCH_BYTES (512 KiB) on each
  * GPU, held until the process ends; nothing is allocated, cleared or freed
- * by a call. A call whose dk_gemv_workspace_bytes() exceeds the array
- * returns DK_ERR_UNSUPPORTED before any launch. Every call on one GPU shares
+ * by a call. Every call's dk_gemv_workspace_bytes() fits it (at most 263168
+ * bytes); one that did not would return DK_ERR_UNSUPPORTED before any
+ * launch. Every call on one GPU shares
  * that GPU's array: calls that overlap in time on one GPU (different
  * streams, or host threads) race and must not be issued. Arguments, checks
  * and results otherwise as dk_w4a16_gemv. */
@@ -214,7 +217,7 @@ const char* dk_last_error(void);
 
 /* ABI version of this header, (major << 16) | minor. */
 int dk_abi_version(void);
-#define DK_ABI_VERSION ((1 << 16) | 3)
+#define DK_ABI_VERSION ((1 << 16) | 4)
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.dk_abi_version() == (1 << 16) | 3
+    assert lib.dk_abi_version() == (1 << 16) | 4
 
 
 def test_default_config_matches_reference(lib):
@@ -150,16 +150,16 @@ def test_describe_names_the_dispatched_kernel(lib):
     d = _abi.describe(lib, 4096, 11008, 1, version=4, split_k=4)
     assert d["kernel"].startswith("void dk::gemv_v4_split<")
     assert _abi.describe(lib, 4096, 4096, 16, reuse_weights=1)["kernel"].startswith(
-        "void dk::gemv_reuse_lds<16, 1, true, 2>")
+        "void dk::gemv_reuse_pf<4, 1>")
     assert _abi.describe(lib, 28672, 8192, 4, reuse_weights=1)["kernel"].startswith(
         "void dk::gemv_reuse<8, 2, 2, true>")
     assert _abi.describe(lib, 4096, 4096, 2, reuse_weights=1)["kernel"].startswith(
         "void dk::gemv_v5_lds<") and ", 15, " in _abi.describe(lib, 4096, 4096, 2,
                                                               reuse_weights=1)["kernel"]
     # With the optional workspace the reuse path splits K; without it, not.
-    assert "gemv_reuse_split<" in _abi.describe(lib, 1024, 16384, 16, reuse_weights=1)["kernel"]
-    assert "gemv_reuse_lds<" in _abi.describe(lib, 1024, 16384, 16, workspace_bytes=0,
-                                              reuse_weights=1)["kernel"]
+    assert "gemv_reuse_split_pf<" in _abi.describe(lib, 1024, 16384, 16, reuse_weights=1)["kernel"]
+    assert "gemv_reuse_pf<" in _abi.describe(lib, 1024, 16384, 16, workspace_bytes=0,
+                                             reuse_weights=1)["kernel"]
     assert _abi.describe(lib, 4096, 4096, 1, version=1, warps_per_row=4)["kernel"].startswith(
         "dk::gemv_v1_multiwave(")
     # Invalid calls fail as dk_w4a16_gemv would.
@@ -178,19 +178,33 @@ ROUTES = [
     ((4096, 4096, 2), dict(reuse_weights=1), "dk::gemv_v5_lds<1, 2, 8, 2, true, dk::LayoutLogical, 15,",
      [512, 1, 1]),
     ((4096, 4096, 4), dict(reuse_weights=1), "dk::gemv_reuse<8, 1, 2, true>", [256, 1, 1]),
-    ((4096, 4096, 8), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 1, true, 2>", [256, 1, 1]),
-    ((4096, 4096, 16), dict(reuse_weights=1), "dk::gemv_reuse_lds<16, 1, true, 2>", [256, 1, 1]),
+    ((4096, 4096, 8), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1>", [256, 1, 1]),
+    ((4096, 4096, 16), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1>", [256, 1, 1]),
     ((4096, 4096, 32), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 2, true, 2>", [128, 2, 1]),
+    ((4096, 11008, 32), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 2>", [128, 2, 1]),
+    ((3072, 8192, 8), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 1, true, 2>", [192, 1, 1]),
+    ((3072, 8192, 3), dict(reuse_weights=1), "dk::gemv_reuse_lds<16, 1, true, 2>", [192, 1, 1]),
+    ((2560, 8192, 4), dict(reuse_weights=1), "dk::gemv_reuse_lds<16, 1, true, 2>", [160, 1, 1]),
     ((28672, 8192, 4), dict(reuse_weights=1), "dk::gemv_reuse<8, 2, 2, true>", [896, 1, 1]),
     ((28672, 8192, 16), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 2, true, 2>", [896, 1, 1]),
     ((11008, 4096, 4), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 1, true, 2>", [688, 1, 1]),
+    ((11008, 4096, 3), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 1, true, 2>", [688, 1, 1]),
+    ((6144, 8192, 12), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 2>", [192, 1, 1]),
     ((6144, 8192, 32), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 2, true, 2>", [192, 2, 1]),
-    ((2048, 16384, 16), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 1, true, 4>", [128, 1, 1]),
+    ((5120, 5120, 12), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 2, true, 2>", [160, 1, 1]),
+    ((2048, 16384, 16), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1>", [128, 1, 1]),
+    ((2048, 16384, 8), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 1, true, 2>", [128, 1, 1]),
     ((2048, 16512, 16), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 1, false, 4>", [128, 1, 1]),
-    ((1024, 16384, 16), dict(reuse_weights=1), "dk::gemv_reuse_split<8, 2, 2>", [32, 1, 4]),
+    ((1024, 16384, 16), dict(reuse_weights=1), "dk::gemv_reuse_split_pf<4, 1>", [64, 1, 2]),
+    ((1024, 28672, 16), dict(reuse_weights=1), "dk::gemv_reuse_split_pf<4, 1>", [64, 1, 4]),
+    ((512, 28672, 33), dict(reuse_weights=1), "dk::gemv_reuse_split_pf<4, 1>", [32, 3, 2]),
+    ((1024, 28672, 33), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1>", [64, 3, 1]),
+    ((777, 28800, 17), dict(reuse_weights=1), "dk::gemv_reuse_split<8, 2, 2>", [25, 2, 2]),
+    ((1024, 14336, 16), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1>", [64, 1, 1]),
+    ((512, 8192, 33), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 1, true, 2>", [32, 3, 1]),
     ((1024, 4096, 8), dict(reuse_weights=1), "dk::gemv_v5_lds<1, 2, 8, 2, true, dk::LayoutLogical, 15,",
      [128, 4, 1]),
-    ((1024, 4096, 12), dict(reuse_weights=1), "dk::gemv_reuse_lds<16, 1, true, 2>", [64, 1, 1]),
+    ((1024, 4096, 12), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1>", [64, 1, 1]),
 ]
 
 
@@ -203,23 +217,43 @@ def test_dispatch_routes(lib, shape, kw, kernel, grid):
 
 
 def test_reuse_split_workspace_size(lib):
-    # The reuse path's split-K tiles (rows longer than 8192 weights at
-    # M <= 1024, where the tiles run: 12 or more batch rows, 33 or more at
-    # M <= 512): 8-byte tickets per 32 rows x 16 batch rows, padded to 256
-    # bytes, then fp32 partials [4, B, M]. Zero where the path streams or
-    # does not split.
+    # The reuse path's split-K tiles (M <= 1024 where the tiles run: 12 or
+    # more batch rows, 33 or more at M <= 512; S = 4 slices on rows of
+    # 28672+ weights at up to 64 tiles of 16 rows x 16 batch rows, S = 2 on
+    # 16384+ at up to 64 tiles or 28672+ at up to 128): an 8-byte ticket per
+    # tile, padded to 256 bytes, then fp32 partials [S, B, M]. Zero where the
+    # path streams or does not split.
     cfg = _abi.default_config(lib, reuse_weights=1)
     ws = lambda m, k, b: lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(cfg))
-    assert ws(1024, 16384, 16) == 256 + 4 * 16 * 1024 * 4   # 32 tickets
-    assert ws(1000, 8320, 12) == 256 + 4 * 12 * 1000 * 4
-    assert ws(600, 65536, 33) == 512 + 4 * 33 * 600 * 4     # 19 x 3 tickets -> 456 -> 512 bytes
-    assert ws(512, 28672, 33) == 512 + 4 * 33 * 512 * 4
+    assert ws(1024, 16384, 16) == 512 + 2 * 16 * 1024 * 4   # 64 tickets
+    assert ws(1024, 28672, 16) == 512 + 4 * 16 * 1024 * 4
+    assert ws(1000, 16384, 12) == 512 + 2 * 12 * 1000 * 4  # 63 tickets -> 504 -> 512 bytes
+    assert ws(600, 65536, 12) == 512 + 4 * 12 * 600 * 4    # 38 tickets -> 304 -> 512 bytes
+    assert ws(600, 65536, 33) == 1024 + 2 * 33 * 600 * 4   # 38 x 3 tickets -> 912 -> 1024 bytes
+    assert ws(512, 28672, 33) == 768 + 2 * 33 * 512 * 4
+    assert ws(777, 28800, 17) == 1024 + 2 * 17 * 777 * 4   # 49 x 2 tickets -> 784 -> 1024 bytes
+    assert ws(1024, 28672, 33) == 0    # 192 tiles: single pass
+    assert ws(1024, 14336, 16) == 0    # rows shorter than 16384 weights
     assert ws(512, 28672, 32) == 0     # streaming kernel
     assert ws(1024, 16384, 11) == 0    # streaming kernel
     assert ws(1024, 8192, 16) == 0     # rows of 8192: single-pass tiles
     assert ws(2048, 16384, 16) == 0    # single-pass tiles from 1025 rows
     assert ws(4096, 11008, 64) == 0
     assert ws(4096, 4096, 4) == 0
+
+
+def test_reuse_split_workspace_fits_the_noalloc_scratch(lib):
+    # The split runs on at most 128 tiles with S = 2 or 64 with S = 4, so
+    # S * B * M <= 65536 partials and 128 tickets: the workspace never
+    # exceeds 263168 bytes, and dk_w4a16_gemv_noalloc's scratch holds every
+    # call's.
+    cfg = _abi.default_config(lib, reuse_weights=1)
+    worst = 0
+    for m in list(range(16, 1025, 16)) + [1, 17, 600, 777, 1000, 1023]:
+        for b in (1, 12, 13, 16, 17, 24, 32, 33, 48, 64, 65, 100, 128, 640):
+            for k in (16384, 16512, 28672, 28800, 65536, 1 << 20):
+                worst = max(worst, lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(cfg)))
+    assert 0 < worst <= 263168 <= _abi.DK_NOALLOC_SCRATCH_BYTES
 
 
 def test_probe_argument_checks(lib):
@@ -298,7 +332,7 @@ def test_torch_extension_surface():
     for pat in (r"version: [\w.]*Int = 5", r"split_k: [\w.]*Int = 4",
                 r"reuse_weights: bool = False", r"warps_per_row: [\w.]*Int = 1"):
         assert re.search(pat, doc), (pat, doc)
-    assert _cuda.ABI_VERSION == (1 << 16) | 3
+    assert _cuda.ABI_VERSION == (1 << 16) | 4
 
 
 def test_extension_rejects_cpu_tensors():

@@ -135,9 +135,9 @@ def test_batch_sweep_c3(batch):
 
 def test_reuse_small_batches_run_the_streaming_kernel():
     # Up to two batch rows; three below 2^27 weights with rows shorter than
-    # 8192 weights (but not rows of 4097-8191 weights at M >= 3072); four
-    # below M = 3072; up to 8 at M <= 2048 on rows shorter than 8192
-    # weights; 11 at M <= 1024, 32 at M <= 512 and any at M <= 128: the
+    # 8192 weights up to 8192 rows (but not rows of 4097-8191 weights at
+    # M >= 3072); four at M <= 2048; up to 8 at M <= 2048 on rows shorter
+    # than 8192 weights; 11 at M <= 1024, 32 at M <= 512 and any at M <= 128: the
     # reuse path runs the streaming kernel with its batch tiles (stamp 15),
     # so its output is the v5 output bit for bit. Five rows with M > 2048
     # take the MFMA tile kernel, which still meets the oracle's bound.
@@ -146,7 +146,6 @@ def test_reuse_small_batches_run_the_streaming_kernel():
     for (m, k, b) in [(4096, 4096, 1), (4096, 4096, 2), (11008, 4096, 2), (300, 8192, 1),
                       (512, 8192, 2), (8192, 4096, 3), (28672, 8192, 2), (4096, 4096, 3),
                       (2000, 8192, 4), (512, 8320, 3), (1024, 11008, 6), (1024, 4224, 11),
-                      (3000, 8192, 4),
                       (2048, 4224, 8), (40, 197632, 3), (500, 4224, 32),
                       (100, 8192, 64)]:
         w, x = oracle.make_case(m, k, b, seed=m + k + b)
@@ -161,10 +160,11 @@ def test_reuse_small_batches_run_the_streaming_kernel():
     assert int(_cuda.last_kernel_stamp()) == 15
     _check_against_oracle(y, oracle.linear_f64(x, packed, scales), "reuse 3000x8320 B=5")
     # Where the LDS-staged tiles beat the streaming kernel at small batches:
-    # three rows of 8192 weights or more, 12 rows at M <= 1024, five rows of
-    # 8192 at M <= 2048.
+    # three rows of 8192 weights or more (or above 8192 rows), four above
+    # 2048 rows, 12 rows at M <= 1024, five rows of 8192 at M <= 2048.
     lib = _abi.load()
-    for (m, k, b) in [(8192, 8192, 3), (4096, 11008, 3), (1000, 4224, 12), (2048, 8192, 5)]:
+    for (m, k, b) in [(8192, 8192, 3), (4096, 11008, 3), (1000, 4224, 12), (2048, 8192, 5),
+                      (3000, 8192, 4), (11008, 4096, 3)]:
         assert "gemv_reuse_lds<" in _abi.describe(lib, m, k, b, reuse_weights=1)["kernel"], (m, k, b)
 
 
@@ -176,11 +176,15 @@ def test_reuse_small_batches_run_the_streaming_kernel():
                                    (4500, 5248, 12), (12000, 8320, 5), (9000, 4224, 33),
                                    (6000, 4224, 40), (3500, 6144, 33), (1000, 4096, 12),
                                    (4096, 4096, 4), (3000, 4096, 5), (2000, 16512, 13),
-                                   (1500, 8320, 9)])
+                                   (1500, 8320, 9), (4100, 8192, 12), (4096, 11008, 32),
+                                   (1000, 16384, 33), (2040, 8192, 20)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
     # The single-pass MFMA tile kernels in each of their shapes (operands
     # staged in LDS: one tile per wave with 16 or 8 waves, two tiles per wave
-    # with 8 or 4 waves, the second tile partly past M at M = 8216; operands
+    # with 8 or 4 waves, the second tile partly past M at M = 8216; double
+    # buffered with 4 waves, one tile per wave up to 4096 rows and two from
+    # 4097, M = 4100 ending in a partial pair of tiles, three batch tiles at
+    # M = 1000 and two, the second partial, at M = 2040; operands
     # loaded directly: M > 8192 with rows longer than 4096 weights up to 8
     # batch rows; the split form is test_reuse_split_tiles), three and four
     # batch rows on the shapes that take the tiles there, long rows of 512
@@ -222,7 +226,11 @@ def test_reuse_tile_kernel_exact_properties(m, k, b):
 def test_reuse_tiles_scale_alignment(m, k, b):
     # With 4-byte aligned scales and an even number of groups per row the
     # tiles load the scales of two groups at once; scales that are only
-    # 2-byte aligned take 2-byte loads. Both give the same bits.
+    # 2-byte aligned take 2-byte loads. Both give the same bits in the
+    # single-buffered tiles. The double-buffered tiles stage pairs only, so
+    # where the dispatch names them (aligned scales) 2-byte aligned scales
+    # run the single-buffered tiles, which add the groups in another order:
+    # both meet the oracle there, and each is repeatable.
     from decode_kernel import _abi
 
     lib = _abi.load()
@@ -242,17 +250,27 @@ def test_reuse_tiles_scale_alignment(m, k, b):
         return y
 
     y = call(sd.data_ptr())
-    assert torch.equal(call(shifted.data_ptr()), y)
-    _check_against_oracle(y, oracle.linear_f64(x, packed, scales), f"reuse {m}x{k} B={b}")
+    y_shifted = call(shifted.data_ptr())
+    y_ref = oracle.linear_f64(x, packed, scales)
+    _check_against_oracle(y, y_ref, f"reuse {m}x{k} B={b}")
+    if "gemv_reuse_pf<" in _abi.describe(lib, m, k, b, reuse_weights=1)["kernel"]:
+        _check_against_oracle(y_shifted, y_ref, f"reuse {m}x{k} B={b}, 2-byte aligned scales")
+        assert torch.equal(call(shifted.data_ptr()), y_shifted)
+        assert torch.equal(call(sd.data_ptr()), y)
+    else:
+        assert torch.equal(y_shifted, y)
 
 
-@pytest.mark.parametrize("m,k,b", [(1024, 16384, 16), (1000, 8320, 12), (777, 12416, 17),
-                                   (512, 28672, 33), (600, 65536, 17)])
+@pytest.mark.parametrize("m,k,b", [(1024, 16384, 16), (1000, 16384, 12), (777, 28800, 17),
+                                   (512, 28672, 33), (600, 65536, 17), (1024, 28672, 16),
+                                   (600, 65536, 12)])
 def test_reuse_split_tiles(m, k, b):
-    # The MFMA tiles with K split over four workgroups (reuse path, rows
-    # longer than 8192 weights at M <= 1024 where the tiles run, a workspace
-    # from the caller; M = 600, 777 and 1000 end in partial sets of 32
-    # rows): against the oracle,
+    # The MFMA tiles with K split over S workgroups per tile (reuse path,
+    # M <= 1024 where the tiles run, a workspace from the caller): the
+    # double-buffered split with S = 2 (rows of 16384 and 28672+ weights)
+    # and S = 4 (28672+ at up to 64 tiles), and at K = 28800 (an odd number
+    # of groups) the split whose tiles load the MFMA operands directly;
+    # M = 600, 777 and 1000 end in partial tiles: against the oracle,
     # bit-identical on repeated calls and
     # with workspaces full of different garbage (each ticket carries the
     # call's generation, so no clearing is needed), and the same bits through

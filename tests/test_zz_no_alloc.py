@@ -1,10 +1,12 @@
 """dk_w4a16_gemv_noalloc, the entry point that allocates nothing, through the
 C ABI against dk_w4a16_gemv with a caller workspace (same kernels, so the
 same bits), on two calls in a row per path, the second with a smaller input:
-the reuse path's split-K tiles (the scratch's user) and paths without
-scratch. Also: a call whose workspace would exceed the scratch is refused
-before any launch, and a captured call replays with eager calls of another
-shape between the replays.
+the reuse path's split-K tiles (the scratch's user: the double-buffered
+split, then the split for rows of an odd number of groups) and paths
+without scratch. Also: a captured call replays with eager calls of another
+shape between the replays. (Every call's workspace fits the scratch, which
+a CPU test of test_abi.py checks over a grid of shapes, so the refusal of
+a larger one has no call to test.)
 """
 
 from __future__ import annotations
@@ -60,7 +62,7 @@ def _tight(y, y_ref, label):
 # (config, first call (M, K, B), second, smaller call); the reuse path's
 # split-K tiles take the scratch, the others none.
 PATHS = [
-    (dict(version=5, reuse_weights=1), (1024, 16384, 16), (800, 9216, 13)),
+    (dict(version=5, reuse_weights=1), (1024, 16384, 16), (1000, 16512, 13)),
     (dict(version=5, reuse_weights=1), (4096, 11008, 64), (2048, 9216, 33)),
     (dict(version=4, split_k=4), (4096, 11008, 1), (1000, 1024, 3)),
     (dict(version=5), (4096, 4096, 1), (333, 640, 2)),
@@ -82,24 +84,6 @@ def test_noalloc_matches_the_workspace_entry(cfg, first, second):
         torch.cuda.synchronize()
         assert torch.equal(y, y_ws), f"{cfg} M={m} K={k} B={b}: differs from dk_w4a16_gemv"
         _tight(y, y_ref, f"noalloc {cfg} M={m} K={k} B={b}")
-
-
-def test_noalloc_refuses_a_workspace_beyond_the_scratch():
-    # The reuse path's split-K tiles at B = 640 need more than the scratch:
-    # refused on the host, before anything is launched (small stand-in
-    # buffers), and y is untouched.
-    abi, lib = _lib()
-    m, k, b = 1024, 16384, 640
-    c = abi.default_config(lib, reuse_weights=1)
-    assert lib.dk_gemv_workspace_bytes(m, k, b, ctypes.byref(c)) > abi.DK_NOALLOC_SCRATCH_BYTES
-    pd = torch.zeros(16, dtype=torch.int32, device="cuda")
-    y = torch.full((4,), 7.0, dtype=torch.float16, device="cuda")
-    rc = lib.dk_w4a16_gemv_noalloc(pd.data_ptr(), pd.data_ptr(), pd.data_ptr(), y.data_ptr(), m,
-                                   k, b, ctypes.byref(c), torch.cuda.current_stream().cuda_stream)
-    assert rc == abi.DK_ERR_UNSUPPORTED
-    assert "dk_w4a16_gemv_noalloc holds" in lib.dk_last_error().decode()
-    torch.cuda.synchronize()
-    assert bool((y == 7.0).all())
 
 
 def test_noalloc_graph_replays_with_eager_calls_between():
