@@ -495,7 +495,16 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
     //   I = 2752,  H = 4096: 6.64 (7.01)     7.08 (8.50)     11.40 (13.78)
     //   I = 28672, H = 8192: 57.23 (59.11)   66.36 (80.54)   127.57 (158.15)
     // Up to 4 batch rows the direct tiles stay (I = 11008, H = 4096, B = 4:
-    // 12.25 against 12.57; I = 28672, B = 3: 47.68 against 50.50).
+    // 12.25 against 12.57; I = 28672, B = 3: 47.68 against 50.50). Up to
+    // I = 4096 at 9-16 batch rows, double buffered with 4 waves (the GEMV's
+    // gemv_reuse_pf; us, against the best single-buffered kernel): I = 3584,
+    // H = 8192, B = 16 11.28 (11.98); I = 2752, H = 4096, B = 16 6.85
+    // (7.20). With more tiles than CUs they lose to the single-buffered 4
+    // waves, which fit three workgroups per CU (I = 11008, H = 4096, B = 16:
+    // 17.76 against 15.67).
+    if (pairs && I <= 4096 && B >= 9 && B <= 16)
+      return L("gate/up launch", dk::gate_up_silu_tiles_pf<4>, grid, dim3(4 * 64), 0, g, gs, u, us,
+               x, I, H, B, h);
     if (B >= 8) {
       if (I <= 4096 && B <= 16)
         return pairs ? L("gate/up launch", dk::gate_up_silu_tiles_lds<8, true>, grid, dim3(8 * 64),

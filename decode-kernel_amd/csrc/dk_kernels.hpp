@@ -1255,25 +1255,36 @@ __device__ __forceinline__ void reuse_pf_loop(f4_t (&acc)[RT], ReusePfLds<KS, RT
 }
 
 // Tile t's KS wave partials, published in each wave's first x buffer (no
-// other wave touches it) and added in wave order after a barrier.
+// other wave touches it; every load of the wave has landed) and, after a
+// barrier, added in wave order.
 template <int KS, int RT>
-__device__ __forceinline__ f4_t reuse_pf_partials(ReusePfLds<KS, RT>& lds, const f4_t (&acc)[RT],
-                                                  int wave, int lane) {
+__device__ __forceinline__ void reuse_pf_publish(ReusePfLds<KS, RT>& lds, const f4_t (&acc)[RT],
+                                                 int wave, int lane) {
   float* part = reinterpret_cast<float*>(lds.x[0][wave]);
 #pragma unroll
   for (int t = 0; t < RT; ++t)
 #pragma unroll
     for (int v = 0; v < 4; ++v) part[(t * 64 + lane) * 4 + v] = acc[t][v];
-  __syncthreads();
+}
+
+template <int KS, int RT>
+__device__ __forceinline__ f4_t reuse_pf_sum(const ReusePfLds<KS, RT>& lds, int t, int lane) {
   f4_t sum = {0.f, 0.f, 0.f, 0.f};
-  if (wave < RT) {
-    for (int w2 = 0; w2 < KS; ++w2) {
-      const float* pw = reinterpret_cast<const float*>(lds.x[0][w2]);
+  for (int w2 = 0; w2 < KS; ++w2) {
+    const float* pw = reinterpret_cast<const float*>(lds.x[0][w2]);
 #pragma unroll
-      for (int v = 0; v < 4; ++v) sum[v] += pw[(wave * 64 + lane) * 4 + v];
-    }
+    for (int v = 0; v < 4; ++v) sum[v] += pw[(t * 64 + lane) * 4 + v];
   }
   return sum;
+}
+
+// Wave t < RT: tile t's sums (zeros in the other waves).
+template <int KS, int RT>
+__device__ __forceinline__ f4_t reuse_pf_partials(ReusePfLds<KS, RT>& lds, const f4_t (&acc)[RT],
+                                                  int wave, int lane) {
+  reuse_pf_publish(lds, acc, wave, lane);
+  __syncthreads();
+  return wave < RT ? reuse_pf_sum(lds, wave, lane) : f4_t{0.f, 0.f, 0.f, 0.f};
 }
 
 // The single-pass double-buffered tiles: RT tiles of 16 rows x 16 batch

@@ -162,4 +162,53 @@ __global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles_lds(
   }
 }
 
+// The same double buffered (the GEMV's gemv_reuse_pf): tiles 0 and 1 are
+// 16 rows of Wg and Wu, each block's loads issued a block ahead. Needs an
+// even number of groups per row and 4-byte aligned scales.
+template <int KS>
+__global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles_pf(
+    const uint4* __restrict__ gate, const uint16_t* __restrict__ gate_scales,
+    const uint4* __restrict__ up, const uint16_t* __restrict__ up_scales,
+    const uint4* __restrict__ x4, int I, int H, int B, uint16_t* __restrict__ h) {
+  write_stamp(kStampGateUp);
+  __shared__ ReusePfLds<KS, 2> lds;
+  const int G = H >> 7;
+  const int nck = H >> 5;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = blockIdx.x * 16;
+  const int kq = lane >> 4;
+  const int rows = __builtin_amdgcn_readfirstlane(min(16, I - row0));
+  const __amdgpu_buffer_rsrc_t rw[2] = {
+      buffer_rsrc(gate + (size_t)row0 * nck, (uint32_t)(rows * (H / 2))),
+      buffer_rsrc(up + (size_t)row0 * nck, (uint32_t)(rows * (H / 2)))};
+  const __amdgpu_buffer_rsrc_t rs[2] = {
+      buffer_rsrc(gate_scales + (size_t)row0 * G, (uint32_t)(rows * G * 2)),
+      buffer_rsrc(up_scales + (size_t)row0 * G, (uint32_t)(rows * G * 2))};
+  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * H * 2));
+  ReuseWindow win;
+  win.bt0 = blockIdx.y * kReuseBatch;
+  win.B = B;
+  win.K = H;
+  win.G = G;
+  win.Gs = G;
+  win.gbeg = 0;
+  f4_t acc[2];
+  reuse_pf_loop<KS, 2>(acc, lds, rw, rs, rx, win, lane, wave);
+  reuse_pf_publish(lds, acc, wave, lane);
+  __syncthreads();
+  const int b = win.bt0 + (lane & 15);
+  if (wave == 0) {
+    const f4_t g = reuse_pf_sum(lds, 0, lane);
+    const f4_t u = reuse_pf_sum(lds, 1, lane);
+    if (b < B) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int orow = row0 + 4 * kq + v;
+        if (orow < I) h[(size_t)b * I + orow] = f2h(silu_f32(g[v]) * u[v]);
+      }
+    }
+  }
+}
+
 }  // namespace dk

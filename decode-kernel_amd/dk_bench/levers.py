@@ -1,6 +1,6 @@
 """Launch-shape and kernel-variant sweeps behind the routing choices.
 
-    python -m dk_bench.levers floor|c0|v4|split|reuse|mlp|all [--steps 300] [--out PATH]
+    python -m dk_bench.levers floor|c0|v4|split|reuse|rsplit|mlp|all [--steps 300] [--out PATH]
     (from decode-kernel_amd/, after build_ext.py)
 
   floor  read-probe launch shapes at the algorithmic bytes of c0, c1 and c2
@@ -17,10 +17,13 @@
   split  the split-K kernel's shapes against the product's v5 (B = 1) over
          the shapes the streaming kernel's launch rules were set on;
   reuse  the weight-reuse tile kernels (operands loaded directly, or staged
-         in LDS by the buffer-load-to-LDS path) at 3-32 batch rows over the
-         shapes the reuse path's launch rules were set on, against the
-         product's reuse path;
-  mlp    the fused gate/up tile kernels (both forms) at 3-32 batch rows on
+         in LDS by the buffer-load-to-LDS path, single or double buffered)
+         at 3-32 batch rows over the shapes the reuse path's launch rules
+         were set on, against the product's reuse path;
+  rsplit the reuse path's split-K tiles (2-8 slices, both forms) and the
+         single-pass tiles at M <= 2048 on long rows, 5-33 batch rows,
+         against the product's reuse path;
+  mlp    the fused gate/up tile kernels (all three forms) at 3-32 batch rows on
          Llama MLP shapes, against the product's fused gate/up.
 Every variant that computes y is checked against the product's v5 output
 (bit-exact where the summation order is the same, else within 1e-3 plus one
@@ -224,12 +227,16 @@ def sweep_split(flush, steps: int) -> dict:
 
 REUSE_PROBLEMS = [(4096, 4096), (4096, 11008), (3072, 8192), (11008, 4096), (6144, 8192),
                   (5120, 5120), (28672, 8192), (8192, 28672), (2048, 16384), (2048, 8192),
-                  (1024, 4096)]
+                  (2048, 4096), (1536, 8192), (2560, 8192), (1024, 4096)]
 REUSE_BATCHES = (3, 4, 5, 8, 12, 16, 32)
+# (kind, waves, tiles per wave, groups per block, paired scales): kind 0
+# operands loaded directly, 1 staged in LDS, 2 staged and double buffered.
 REUSE_SHAPES = [(0, 8, 1, 2, True), (0, 8, 1, 4, False), (0, 16, 1, 4, False), (0, 16, 1, 2, False),
                 (0, 8, 2, 2, True), (0, 8, 2, 4, False),
                 (1, 8, 1, 2, True), (1, 16, 1, 2, True), (1, 8, 2, 2, True), (1, 4, 1, 2, True),
-                (1, 4, 2, 2, True), (1, 8, 1, 4, True), (1, 4, 1, 4, True), (1, 4, 2, 4, True)]
+                (1, 4, 2, 2, True), (1, 8, 1, 4, True), (1, 4, 1, 4, True), (1, 4, 2, 4, True),
+                (2, 4, 1, 2, True), (2, 6, 1, 2, True), (2, 4, 2, 2, True), (2, 6, 2, 2, True)]
+_REUSE_KINDS = ("tiles", "lds", "pf")
 
 
 def sweep_reuse(flush, steps: int) -> dict:
@@ -263,7 +270,7 @@ def sweep_reuse(flush, steps: int) -> dict:
                 torch.cuda.synchronize()
                 if not _close(y, y_prod):
                     raise RuntimeError(f"reuse {shape} differs from the product at {name}")
-                key = "{}_KS{}_RT{}_SG{}{}".format("lds" if kind else "tiles", ks, rt, sg,
+                key = "{}_KS{}_RT{}_SG{}{}".format(_REUSE_KINDS[kind], ks, rt, sg,
                                                    "_pairs" if pairs else "")
                 rows[key] = _time(lambda i: benchlib.reuse(kind, ks, rt, sg, pairs, pk[i % n],
                                                            sc[i % n], x, y), steps, flush)
@@ -276,9 +283,74 @@ def sweep_reuse(flush, steps: int) -> dict:
     return out
 
 
+RSPLIT_PROBLEMS = [(1024, 8192), (1024, 14336), (1024, 16384), (512, 28672), (1024, 28672),
+                   (600, 65536), (768, 12288), (512, 16384), (512, 8192), (2048, 16384)]
+RSPLIT_BATCHES = (5, 8, 12, 16, 33)
+RSPLIT_SINGLE = [(1, 8, 1, 2), (1, 8, 1, 4), (2, 4, 1, 2), (2, 6, 1, 2)]
+# (kind, waves, tiles per wave, slices): kind 0 operands loaded directly,
+# 1 double-buffered LDS staging.
+RSPLIT_SHAPES = [(0, 8, 2, 4), (1, 4, 1, 2), (1, 4, 1, 4), (1, 4, 1, 8), (1, 6, 1, 4),
+                 (1, 4, 2, 4), (1, 4, 2, 2)]
+
+
+def sweep_rsplit(flush, steps: int) -> dict:
+    """Split-K and single-pass tiles of the reuse path against the product's
+    reuse path, at M <= 2048 on long rows."""
+    from decode_kernel import _cuda
+
+    from . import benchlib
+    from .ablation import gpu_case
+    from .common import weight_copies
+
+    out = {}
+    for m, k in RSPLIT_PROBLEMS:
+        packed, scales, _ = gpu_case(m, k, seed=4000 + m + k)
+        pk, sc = weight_copies(packed, scales)
+        n = len(pk)
+        gen = torch.Generator(device="cuda").manual_seed(m + k)
+        xall = torch.randn(max(RSPLIT_BATCHES), k, device="cuda", generator=gen).half()
+        ws = torch.empty(max(benchlib.reuse_split_workspace(rt, s_, m, max(RSPLIT_BATCHES))
+                             for _, _, rt, s_ in RSPLIT_SHAPES), dtype=torch.uint8, device="cuda")
+        for b in RSPLIT_BATCHES:
+            x = xall[:b].contiguous()
+            name = f"m{m}_k{k}_b{b}"
+            y_prod = _cuda.w4a16_gemv(pk[0], sc[0], x, reuse_weights=True)
+            y = torch.empty_like(y_prod)
+            rows = {"product_reuse": _time(
+                lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x, reuse_weights=True), steps, flush,
+                runs=2)}
+            for kind, ks, rt, sg in RSPLIT_SINGLE:
+                y.fill_(float("nan"))
+                if benchlib.reuse(kind, ks, rt, sg, True, pk[0], sc[0], x, y) == 3:
+                    raise RuntimeError(f"reuse {(kind, ks, rt, sg)} is not instantiated")
+                torch.cuda.synchronize()
+                if not _close(y, y_prod):
+                    raise RuntimeError(f"reuse {(kind, ks, rt, sg)} differs from the product at {name}")
+                rows[f"{_REUSE_KINDS[kind]}_KS{ks}_RT{rt}_SG{sg}"] = _time(
+                    lambda i: benchlib.reuse(kind, ks, rt, sg, True, pk[i % n], sc[i % n], x, y),
+                    steps, flush)
+            for kind, ks, rt, s_ in RSPLIT_SHAPES:
+                y.fill_(float("nan"))
+                if benchlib.reuse_split(kind, ks, rt, s_, pk[0], sc[0], x, y, ws) == 3:
+                    raise RuntimeError(f"split {(kind, ks, rt, s_)} is not instantiated")
+                torch.cuda.synchronize()
+                if not _close(y, y_prod):
+                    raise RuntimeError(f"split {(kind, ks, rt, s_)} differs from the product at {name}")
+                rows["{}_KS{}_RT{}_S{}".format("split" if kind == 0 else "splitpf", ks, rt, s_)] = \
+                    _time(lambda i: benchlib.reuse_split(kind, ks, rt, s_, pk[i % n], sc[i % n], x, y,
+                                                         ws), steps, flush)
+            best = min((v, kk) for kk, v in rows.items())
+            print(f"rsplit {name}: product {rows['product_reuse']:.3f}; best {best[1]} {best[0]:.3f}",
+                  flush=True)
+            out[name] = rows
+        del pk, sc, packed, scales, xall, ws
+        torch.cuda.empty_cache()
+    return out
+
+
 MLP_PROBLEMS = [(11008, 4096), (3584, 8192), (2752, 4096), (14336, 4096), (28672, 8192)]
 MLP_BATCHES = (3, 4, 8, 16, 32)
-MLP_SHAPES = [(0, 8, True), (1, 8, True), (1, 4, True)]
+MLP_SHAPES = [(0, 8, True), (1, 8, True), (1, 4, True), (2, 4, True), (2, 6, True)]
 
 
 def sweep_mlp(flush, steps: int) -> dict:
@@ -316,7 +388,7 @@ def sweep_mlp(flush, steps: int) -> dict:
                 torch.cuda.synchronize()
                 if not _close(hbuf, h_prod):
                     raise RuntimeError(f"gate/up {shape} differs from the product at {name}")
-                key = "{}_KS{}".format("lds" if kind else "tiles", ks)
+                key = "{}_KS{}".format(_REUSE_KINDS[kind], ks)
                 rows[key] = _time(lambda j: benchlib.gate_up(kind, ks, pairs, gps[j % n], gss[j % n],
                                                              ups[j % n], uss[j % n], x, hbuf),
                                   steps, flush)
@@ -331,7 +403,7 @@ def sweep_mlp(flush, steps: int) -> dict:
 
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("what", choices=["floor", "c0", "v4", "split", "reuse", "mlp", "all"])
+    ap.add_argument("what", choices=["floor", "c0", "v4", "split", "reuse", "rsplit", "mlp", "all"])
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--out", type=Path, default=None)
     args = ap.parse_args()
@@ -351,6 +423,8 @@ def main() -> None:
         res["split"] = sweep_split(flush, args.steps)
     if args.what in ("reuse", "all"):
         res["reuse"] = sweep_reuse(flush, args.steps)
+    if args.what in ("rsplit", "all"):
+        res["rsplit"] = sweep_rsplit(flush, args.steps)
     if args.what in ("mlp", "all"):
         res["mlp"] = sweep_mlp(flush, args.steps)
     if args.out:

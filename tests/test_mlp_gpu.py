@@ -95,7 +95,7 @@ def test_mlp_step_matches_oracle(i, h, b):
 # Ragged shapes in every I range (<= 2048, 4096, above) and H range (<= 4096,
 # 8192, above) the gate/up dispatch tells apart.
 GATE_UP_SHAPES = [(1000, 4224), (2000, 8320), (3000, 4224), (3000, 8320), (5000, 4224),
-                  (4500, 8320), (1800, 6144), (700, 3968), (5000, 5120)]
+                  (4500, 8320), (1800, 6144), (700, 3968), (5000, 5120), (2752, 4096)]
 
 
 @pytest.mark.parametrize("i,h", GATE_UP_SHAPES)
@@ -103,7 +103,8 @@ def test_gate_up_every_dispatch_class(i, h):
     # Batches 1-8 cover every streaming tile size (one row, and tiles of 2, 3
     # and 4 rows, the last one partly empty at B = 5 and 7); from 3 rows at
     # I > 2048, and from 9 rows at I > 1024, the MFMA tiles run instead (with
-    # both operands staged in LDS from 8 rows). Each
+    # both operands staged in LDS from 8 rows, double buffered at 9-16 rows
+    # up to I = 4096 where the scales pair: I = 1800 and 2752). Each
     # output row depends on its own activation row only, so the first b rows
     # of one 16-row case give the reference for every b.
     from decode_kernel import _cuda, gate_up_silu
