@@ -28,8 +28,11 @@ sys.path.insert(0, str(HERE.parents[1]))
 sys.path.insert(0, str(HERE.parents[2]))
 
 SHAPES = {"c0": (4096, 4096, 1), "c1": (11008, 4096, 1), "c2": (4096, 11008, 1),
-          "c3b8": (4096, 4096, 8), "c3b16": (4096, 4096, 16), "c4a": (28672, 8192, 1),
-          "c4ab8": (28672, 8192, 8), "c4b": (8192, 28672, 1)}
+          "c3b8": (4096, 4096, 8), "c3b12": (4096, 4096, 12), "c3b16": (4096, 4096, 16),
+          "c4a": (28672, 8192, 1), "c4ab8": (28672, 8192, 8), "c4b": (8192, 28672, 1),
+          # shapes of the reuse path's two-tile and split-K routes
+          "m6144k8192b16": (6144, 8192, 16), "m1024k16384b16": (1024, 16384, 16),
+          "m1024k28672b16": (1024, 28672, 16)}
 VARIANTS = {"v5": dict(version=5), "v2": dict(version=2), "v4": dict(version=4, split_k=4),
             "reuse": dict(version=5, reuse_weights=True), "v1": dict(version=1)}
 ABLATIONS = {"no_decode": 1, "loads_only": 2}
