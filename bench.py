@@ -474,15 +474,25 @@ def main():
                 same = measure_read_same_size(copies[0], preroll=preroll)
                 entry["same_size_read"] = same
                 log(f"   same-size STREAM read {same['median_us']:7.2f} us  {same['gbps']:8.1f} GB/s")
+            first = True
             for v in variants:
                 if v == "v0" and name != "c0":
                     continue
                 headline_row = name == "c0" and v == "v5"
                 steps = args.steps if headline_row else other_steps
-                r = bench_variant(_cuda, copies, xd, v, steps, preroll,
-                                  warmup=args.warmup if headline_row else 1,
-                                  y_ref=y_ref if v == "v5" else None,
-                                  call_level_flush=flush if headline_row else None)
+                # The first variant timed on a new set of weight copies is
+                # timed twice and the lower median kept: the first timings
+                # after new copies run up to 8% slow on MI355X, whichever
+                # kernel comes first.
+                for run in range(2 if first else 1):
+                    r_run = bench_variant(_cuda, copies, xd, v, steps, preroll,
+                                          warmup=args.warmup if headline_row else 1,
+                                          y_ref=y_ref if v == "v5" else None,
+                                          call_level_flush=flush if headline_row else None)
+                    if first:
+                        r_run["runs"] = 2
+                    r = r_run if run == 0 or r_run["median_us"] < r["median_us"] else r
+                first = False
                 r["kernel"] = (None if v == "v5_paired" else
                                kernel_of(m, k, b, **VARIANTS[v])["kernel"])
                 r["pct_of_read_roof"] = 100.0 * r["gbps"] / roof["gbps"]

@@ -556,6 +556,14 @@ DKB_API int dkb_reuse(int kind, int KS, int RT, int SG, int pairs, const void* p
   }
   DKB_R2(4, 1) DKB_R2(6, 1) DKB_R2(7, 1) DKB_R2(4, 2) DKB_R2(6, 2)
 #undef DKB_R2
+#define DKB_RX(kd, ks, rt, xl)                                                                 \
+  if (kind == kd && KS == ks && RT == rt && SG == 2 && pairs && B <= 2 * xl) {                 \
+    hipLaunchKernelGGL((dk::gemv_reuse_pf<ks, rt, xl>), dim3((M + 16 * rt - 1) / (16 * rt), 1), \
+                       dim3(ks * 64), 0, stream, p, s, xx, yy, M, K, B);                       \
+    return launch_error("reuse pf");                                                           \
+  }
+  DKB_RX(3, 4, 1, 4) DKB_RX(3, 6, 1, 4) DKB_RX(4, 4, 1, 2) DKB_RX(4, 6, 1, 2)
+#undef DKB_RX
   DKB_R0(8, 1, 2, true) DKB_R0(8, 1, 2, false) DKB_R0(8, 1, 4, false) DKB_R0(16, 1, 4, false)
   DKB_R0(16, 1, 2, false) DKB_R0(8, 2, 2, true) DKB_R0(8, 2, 2, false) DKB_R0(8, 2, 4, false)
   DKB_R1(8, 1, true) DKB_R1(8, 1, false) DKB_R1(16, 1, true) DKB_R1(16, 1, false)

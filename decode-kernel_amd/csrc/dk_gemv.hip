@@ -599,45 +599,61 @@ int launch_reuse_lds(const Launch& L, const uint4* p, const uint16_t* s, const u
            y, M, K, B);
 }
 
-template <int KS, int RT>
+template <int KS, int RT, int XL>
 int launch_reuse_pf(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                     int M, int K, int B) {
   const dim3 grid((M + 16 * RT - 1) / (16 * RT), (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
-  return L("reuse launch", dk::gemv_reuse_pf<KS, RT>, grid, dim3(KS * 64), 0, p, s, x, y, M, K, B);
+  return L("reuse launch", dk::gemv_reuse_pf<KS, RT, XL>, grid, dim3(KS * 64), 0, p, s, x, y, M, K,
+           B);
 }
 
-// Where the double-buffered tiles (gemv_reuse_pf, 4 waves; paired scales
-// only) take the single pass: 0 nowhere, else RT, the tiles per wave. From
-// the sweep of every tile kernel (dk_bench.levers reuse), us, the
-// double-buffered tiles against the best single-buffered ones in brackets:
+// A shape of the double-buffered tiles (gemv_reuse_pf): KS waves, RT tiles
+// per wave, XL x loads per block; KS = 0: not these tiles.
+struct PfShape {
+  int ks = 0, rt = 0, xl = 0;
+};
+
+// Where the double-buffered tiles take the single pass (paired scales
+// only). From the sweep of every tile kernel (dk_bench.levers reuse), us,
+// the double-buffered tiles against the best single-buffered ones in
+// brackets; from 9 batch rows 4 waves with 8 x loads per block:
 //                        B = 8          B = 12         B = 16         B = 32
-//   M = K = 4096:        4.69 (4.87)    4.88 (5.17)    4.97 (5.45)    6.50 (6.37)
-//   M = 4096, K = 11008: 8.99 (8.71)    9.44 (9.59)    10.00 (10.76)  12.94 (13.39)
-//   M = 3072, K = 8192:  7.12 (7.05)    7.36 (7.81)    7.76 (8.52)    10.02 (10.58)
-//   M = 2048, K = 16384: 11.26 (10.73)  11.53 (12.01)  12.33 (13.62)  12.24 (13.44)
-//   M = 2048, K = 4096:  4.54 (4.66)    4.73 (4.87)    4.79 (5.09)    4.79 (5.13)
-//   M = 6144, K = 8192:  10.24 (9.91)   10.44 (10.73)  10.82 (11.46)  19.33 (18.67)
-//   M = 8192, K = 28672: 27.13 (27.76)  29.74 (31.51)  33.20 (34.60)  66.16 (63.84)
-//   M = 5120, K = 5120:  8.02 (6.98)    8.07 (7.48)    8.16 (7.92)    14.11 (11.76)
-//   M = 28672, K = 8192: 34.97 (33.56)  36.79 (37.13)  39.34 (38.62)  70.05 (66.75)
-// One tile per wave up to 4096 rows from 9 batch rows (and 8 on rows of up
-// to 4096 weights); two from 4097 rows on rows of 8192+ weights at 9-16
-// batch rows, and at 2049-4096 rows above 16. At M <= 1024 above 32 batch
-// rows (three batch tiles) the single-buffered tiles keep rows shorter than
-// 16384 weights (M = 512, K = 8192, B = 33: 6.40 against 6.71).
-int reuse_pf_rt(int M, int K, int B) {
-  if (M > 8192) return 0;
-  if (M > 4096) return B >= 9 && B <= 16 && K >= 8192 ? 2 : 0;
+//   M = K = 4096:        4.56 (4.87)    4.88 (5.17)    4.97 (5.45)    6.50 (6.37)
+//   M = 4096, K = 11008: 8.55 (8.71)    9.44 (9.59)    10.00 (10.76)  12.94 (13.39)
+//   M = 3072, K = 8192:  6.72 (7.01)    7.36 (7.81)    7.76 (8.52)    10.02 (10.58)
+//   M = 2048, K = 16384: 9.97 (10.73)   11.53 (12.01)  12.33 (13.62)  12.24 (13.44)
+//   M = 2048, K = 4096:  4.30 (4.65)    4.73 (4.87)    4.79 (5.09)    4.79 (5.13)
+//   M = 6144, K = 8192:  10.21 (9.88)   10.44 (10.73)  10.82 (11.46)  19.33 (18.67)
+//   M = 8192, K = 28672: 26.88 (27.47)  29.74 (31.51)  33.20 (34.60)  66.16 (63.84)
+//   M = 5120, K = 5120:  7.64 (6.98)    8.07 (7.48)    8.16 (7.92)    14.11 (11.76)
+//   M = 28672, K = 8192: 34.93 (33.47)  36.79 (37.13)  39.34 (38.62)  70.05 (66.75)
+// Up to 8 batch rows (one batch tile), 6 waves with 4 x loads per block,
+// rows 8-15 of the x buffers held at zero (M = K = 4096: B = 3 4.33, B = 4
+// 4.35, B = 5 4.33 against 4.54, 4.59, 4.60 for the single-buffered tiles
+// or the streaming kernel; M = 2048, K = 16384, B = 5 9.35 against 9.73);
+// rows of 8192+ weights keep the single-buffered 16 waves at 3 batch rows
+// and rows of 8192+ at up to 5 (M = 4096, K = 11008, B = 4: 7.32 against
+// 7.74). One tile per wave up to 4096 rows; two from 4097 rows on rows of
+// 8192+ weights at 9-16 batch rows, and at 2049-4096 rows above 16. Above
+// 4096 rows up to 8 batch rows and at M <= 1024 above 32 batch rows (three
+// batch tiles) on rows shorter than 16384 weights the single-buffered
+// tiles stay (M = 6144, K = 8192, B = 8: 9.88 against 10.21; M = 512,
+// K = 8192, B = 33: 6.40 against 6.71).
+PfShape reuse_pf_shape(int M, int K, int B) {
+  if (M > 8192) return {};
+  if (M > 4096) return B >= 9 && B <= 16 && K >= 8192 ? PfShape{4, 2, 8} : PfShape{};
   if (M > 2048) {
-    if (B > 16) return K >= 8192 ? 2 : 0;
-    return B >= 9 || (B == 8 && K <= 4096) ? 1 : 0;
+    if (B > 16) return K >= 8192 ? PfShape{4, 2, 8} : PfShape{};
+    if (B >= 9) return {4, 1, 8};
+    if (B >= 6 || (B >= 4 && K <= 8192) || K <= 4096) return {6, 1, 4};
+    return {};
   }
-  if (B < 9) return 0;
-  return M <= 1024 && B > 32 && K < 16384 ? 0 : 1;
+  if (B >= 9) return M <= 1024 && B > 32 && K < 16384 ? PfShape{} : PfShape{4, 1, 8};
+  return B >= 5 ? PfShape{6, 1, 4} : PfShape{};
 }
 
 // The single-pass tiles. Where the double-buffered tiles do not run
-// (reuse_pf_rt, or scales that do not pair), the single-buffered LDS-staged
+// (reuse_pf_shape, or scales that do not pair), the single-buffered LDS-staged
 // kernel (gemv_reuse_lds) against the tiles that load the MFMA operands
 // directly (gemv_reuse) in brackets, us per launch, from an earlier sweep:
 //                        B = 4          B = 8          B = 16         B = 32
@@ -663,9 +679,10 @@ int reuse_pf_rt(int M, int K, int B) {
 int launch_reuse_tiles(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x,
                        uint16_t* y, int M, int K, int B) {
   if ((K / DK_GROUP_SIZE) % 2 == 0 && aligned(s, 4)) {
-    const int rt = reuse_pf_rt(M, K, B);
-    if (rt == 1) return launch_reuse_pf<4, 1>(L, p, s, x, y, M, K, B);
-    if (rt == 2) return launch_reuse_pf<4, 2>(L, p, s, x, y, M, K, B);
+    const PfShape pf = reuse_pf_shape(M, K, B);
+    if (pf.ks == 6) return launch_reuse_pf<6, 1, 4>(L, p, s, x, y, M, K, B);
+    if (pf.ks == 4 && pf.rt == 1) return launch_reuse_pf<4, 1, 8>(L, p, s, x, y, M, K, B);
+    if (pf.ks == 4 && pf.rt == 2) return launch_reuse_pf<4, 2, 8>(L, p, s, x, y, M, K, B);
   }
   if (M > 2048 && M <= 4096 && K <= 4096 && B <= 5)
     return launch_reuse<8, 1, 2>(L, p, s, x, y, M, K, B);
@@ -748,22 +765,27 @@ enum class ReuseShape { kStream, kTiles };
 //   M = 1024, K = 4096:  B = 8 stream 3.73 (4.64), B = 12 tiles 4.87 (4.99)
 //   M = 4096, K = 11008, B = 3: tiles 7.50 (stream 9.63)
 //   M = 3072, K = 8192,  B = 3: tiles 6.40 (stream 7.11)
-//   M = K = 4096,        B = 3: stream 4.55 (tiles 4.60)
 //   M = 6144, K = 8192,  B = 3: tiles 9.14 (stream 10.45)
 //   M = 11008, K = 4096, B = 3: tiles 7.82 (stream 8.51)
 //   M = 2560, K = 8192,  B = 4: tiles 6.27 (stream 9.61)
+//   M = K = 4096,        B = 3: tiles 4.33 (stream 4.54; double buffered)
+//   M = 2048, K = 4096,  B = 8: tiles 4.30 (stream 4.71; double buffered)
 // Up to 512 rows the streaming kernel keeps every batch up to 32 rows (M =
 // 512, K = 8320, B = 32: 11.67 against 11.47 for the earlier tiles); it also
-// keeps up to eight batch rows at M <= 2048 on rows shorter than 8192
-// weights, where the earlier tiles lost and no sweep point says otherwise.
+// keeps up to four batch rows at M <= 2048, and up to eight there on rows
+// shorter than 8192 weights with an odd number of groups (the
+// double-buffered tiles need pairs of groups; the single-buffered ones
+// were level with the streaming kernel: M = 2048, K = 4096, B = 8 4.65
+// against 4.68).
 ReuseShape reuse_shape(int M, int K, int B) {
   if (B <= 2 || M <= 128) return ReuseShape::kStream;
   if (M <= 512) return B <= 32 ? ReuseShape::kStream : ReuseShape::kTiles;
   if (M <= 1024) return B < 12 ? ReuseShape::kStream : ReuseShape::kTiles;
-  if (M <= 2048 && (B <= 4 || (B <= 8 && K < 8192))) return ReuseShape::kStream;
+  if (M <= 2048 && (B <= 4 || (B <= 8 && K < 8192 && (K / DK_GROUP_SIZE) % 2 == 1)))
+    return ReuseShape::kStream;
   if (B == 3) {
     const bool tiles = K >= 8192 || M > 8192 || (size_t)M * (size_t)K >= ((size_t)1 << 27) ||
-                       (M >= 3072 && K > 4096 && K < 8192);
+                       (M >= 3072 && K > 4096 && K < 8192) || (M > 2048 && M <= 4096 && K <= 4096);
     return tiles ? ReuseShape::kTiles : ReuseShape::kStream;
   }
   return ReuseShape::kTiles;

@@ -1087,10 +1087,10 @@ struct ReusePfLds {
   static_assert(sizeof(x[0][0]) >= 256 * RT * sizeof(float), "partials fit an x buffer");
 };
 
-// Loads per block and wave: two per tile of weights, eight of x, one per
-// tile of scales.
-template <int RT>
-constexpr int kReusePfLoads = 3 * RT + 8;
+// Loads per block and wave: two per tile of weights, kXL of x (two batch
+// rows each), one per tile of scales.
+template <int RT, int kXL>
+constexpr int kReusePfLoads = 3 * RT + kXL;
 
 // s_waitcnt vmcnt(N) alone (the gfx9 encoding, expcnt and lgkmcnt at their
 // maximum).
@@ -1111,10 +1111,11 @@ struct ReuseWindow {
   int bt0, B, K, G, Gs, gbeg;
 };
 
-// Issues the loads of the block at window group g0 into xb, wb, sb: every
-// x load, those of batch rows >= B out of range, so that each block issues
-// the same number of loads.
-template <int RT>
+// Issues the loads of the block at window group g0 into xb, wb, sb: the
+// kXL x loads of batch rows bt0 .. bt0 + 2 kXL - 1, those of rows >= B out
+// of range, so that each block issues the same number of loads (rows from
+// 2 kXL on are never loaded: the caller keeps them zero).
+template <int RT, int kXL>
 __device__ __forceinline__ void reuse_pf_issue(uint4* __restrict__ xb, uint4* __restrict__ wb,
                                                uint4* __restrict__ sb,
                                                const __amdgpu_buffer_rsrc_t (&rw)[RT],
@@ -1136,7 +1137,7 @@ __device__ __forceinline__ void reuse_pf_issue(uint4* __restrict__ xb, uint4* __
   // x: load i covers batch rows bt0 + 2 i, bt0 + 2 i + 1, lane l chunk
   // l % 32 of row 2 i + l / 32 (chunk c = group c / 16, bytes 16 (c % 16)).
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kXL; ++i) {
     const int bb = 2 * i + lane / 32;
     const int p = lane % 32;
     const int c = (p & 16) | ((p ^ stage_swizzle<32>(bb)) & 15);
@@ -1159,7 +1160,7 @@ __device__ __forceinline__ void reuse_pf_issue(uint4* __restrict__ xb, uint4* __
 // One step: with kNext, issues the block at gn into nx, nw, ns and waits
 // for all but those loads; else waits for every load. Then adds the block
 // in cx, cw, cs into acc.
-template <int RT, bool kNext>
+template <int RT, bool kNext, int kXL>
 __device__ __forceinline__ void reuse_pf_step(f4_t (&acc)[RT], const uint4* __restrict__ cx,
                                               const uint4* __restrict__ cw,
                                               const uint4* __restrict__ cs, uint4* __restrict__ nx,
@@ -1175,8 +1176,8 @@ __device__ __forceinline__ void reuse_pf_step(f4_t (&acc)[RT], const uint4* __re
     // returned (its MFMAs consumed them; this orders the loads after them).
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_sched_barrier(0);
-    reuse_pf_issue<RT>(nx, nw, ns, rw, rs, rx, win, lane, gn);
-    wait_vmcnt<kReusePfLoads<RT>>();
+    reuse_pf_issue<RT, kXL>(nx, nw, ns, rw, rs, rx, win, lane, gn);
+    wait_vmcnt<kReusePfLoads<RT, kXL>>();
   } else {
     wait_vmcnt<0>();
   }
@@ -1215,8 +1216,9 @@ __device__ __forceinline__ void reuse_pf_step(f4_t (&acc)[RT], const uint4* __re
 }
 
 // acc[t] over the wave's blocks of the window (window groups 2 wave, 2 wave
-// + 1, then every 2 KS; G even), two buffers in turn.
-template <int KS, int RT>
+// + 1, then every 2 KS; G even), two buffers in turn. With kXL < 8 (batch
+// tiles of at most 2 kXL rows) the x rows from 2 kXL on are zeroed once.
+template <int KS, int RT, int kXL = 8>
 __device__ __forceinline__ void reuse_pf_loop(f4_t (&acc)[RT], ReusePfLds<KS, RT>& lds,
                                               const __amdgpu_buffer_rsrc_t (&rw)[RT],
                                               const __amdgpu_buffer_rsrc_t (&rs)[RT],
@@ -1232,21 +1234,30 @@ __device__ __forceinline__ void reuse_pf_loop(f4_t (&acc)[RT], ReusePfLds<KS, RT
   uint4* wb = lds.w[1][wave];
   uint4* sa = lds.s[0][wave];
   uint4* sb = lds.s[1][wave];
+  static_assert(kXL == 2 || kXL == 4 || kXL == 8, "x loads per block");
+  if constexpr (kXL < 8) {
+    // Rows 2 kXL .. 15 of both x buffers (64 lanes x 16 bytes per store).
+#pragma unroll
+    for (int i = kXL; i < 8; ++i) {
+      xa[i * 64 + lane] = uint4{0u, 0u, 0u, 0u};
+      xb[i * 64 + lane] = uint4{0u, 0u, 0u, 0u};
+    }
+  }
   int g = 2 * wave;
-  reuse_pf_issue<RT>(xa, wa, sa, rw, rs, rx, win, lane, g);
+  reuse_pf_issue<RT, kXL>(xa, wa, sa, rw, rs, rx, win, lane, g);
   for (int n = 0;;) {
     if (n + 1 < nb) {
-      reuse_pf_step<RT, true>(acc, xa, wa, sa, xb, wb, sb, rw, rs, rx, win, lane, g + 2 * KS);
+      reuse_pf_step<RT, true, kXL>(acc, xa, wa, sa, xb, wb, sb, rw, rs, rx, win, lane, g + 2 * KS);
     } else {
-      reuse_pf_step<RT, false>(acc, xa, wa, sa, xb, wb, sb, rw, rs, rx, win, lane, 0);
+      reuse_pf_step<RT, false, kXL>(acc, xa, wa, sa, xb, wb, sb, rw, rs, rx, win, lane, 0);
       break;
     }
     ++n;
     g += 2 * KS;
     if (n + 1 < nb) {
-      reuse_pf_step<RT, true>(acc, xb, wb, sb, xa, wa, sa, rw, rs, rx, win, lane, g + 2 * KS);
+      reuse_pf_step<RT, true, kXL>(acc, xb, wb, sb, xa, wa, sa, rw, rs, rx, win, lane, g + 2 * KS);
     } else {
-      reuse_pf_step<RT, false>(acc, xb, wb, sb, xa, wa, sa, rw, rs, rx, win, lane, 0);
+      reuse_pf_step<RT, false, kXL>(acc, xb, wb, sb, xa, wa, sa, rw, rs, rx, win, lane, 0);
       break;
     }
     ++n;
@@ -1288,9 +1299,10 @@ __device__ __forceinline__ f4_t reuse_pf_partials(ReusePfLds<KS, RT>& lds, const
 }
 
 // The single-pass double-buffered tiles: RT tiles of 16 rows x 16 batch
-// rows per workgroup, KS waves splitting each row's blocks. Needs an even
-// number of groups per row and 4-byte aligned scales.
-template <int KS, int RT>
+// rows per workgroup, KS waves splitting each row's blocks; kXL x loads per
+// block (batch tiles of up to 2 kXL rows: B <= 2 kXL or kXL = 8). Needs an
+// even number of groups per row and 4-byte aligned scales.
+template <int KS, int RT, int kXL = 8>
 __global__ __launch_bounds__(KS * 64) void gemv_reuse_pf(const uint4* __restrict__ packed,
                                                          const uint16_t* __restrict__ scales,
                                                          const uint4* __restrict__ x4,
@@ -1321,7 +1333,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_pf(const uint4* __restrict
   win.Gs = G;
   win.gbeg = 0;
   f4_t acc[RT];
-  reuse_pf_loop<KS, RT>(acc, lds, rw, rs, rx, win, lane, wave);
+  reuse_pf_loop<KS, RT, kXL>(acc, lds, rw, rs, rx, win, lane, wave);
   const f4_t sum = reuse_pf_partials<KS, RT>(lds, acc, wave, lane);
   const int b = win.bt0 + (lane & 15);
   if (wave < RT && b < B) {

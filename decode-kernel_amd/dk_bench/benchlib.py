@@ -155,8 +155,9 @@ def run_kernel(kernel: tuple, math: int, packed, scales, x, y) -> None:
 def reuse(kind: int, ks: int, rt: int, sg: int, pairs: bool, packed, scales, x, y) -> int:
     """The reuse path's tile kernels: kind 0 gemv_reuse<KS, RT, SG, pairs>,
     kind 1 gemv_reuse_lds<KS, RT, pairs, SG>, kind 2 gemv_reuse_pf<KS, RT>
-    (SG 2, pairs). Returns 3 (nothing launched) for a shape not instantiated
-    in the measurement library."""
+    (SG 2, pairs), kinds 3 and 4 gemv_reuse_pf<KS, RT, kXL> with 4 and 2 x
+    loads per block (up to 8 and 4 batch rows). Returns 3 (nothing launched)
+    for a shape not instantiated in the measurement library."""
     m, k = packed.shape[0], packed.shape[1] * 8
     b = x.shape[0]
     rc = load().dkb_reuse(kind, ks, rt, sg, int(pairs), packed.data_ptr(), scales.data_ptr(),

@@ -235,8 +235,12 @@ REUSE_SHAPES = [(0, 8, 1, 2, True), (0, 8, 1, 4, False), (0, 16, 1, 4, False), (
                 (0, 8, 2, 2, True), (0, 8, 2, 4, False),
                 (1, 8, 1, 2, True), (1, 16, 1, 2, True), (1, 8, 2, 2, True), (1, 4, 1, 2, True),
                 (1, 4, 2, 2, True), (1, 8, 1, 4, True), (1, 4, 1, 4, True), (1, 4, 2, 4, True),
-                (2, 4, 1, 2, True), (2, 6, 1, 2, True), (2, 4, 2, 2, True), (2, 6, 2, 2, True)]
-_REUSE_KINDS = ("tiles", "lds", "pf")
+                (2, 4, 1, 2, True), (2, 6, 1, 2, True), (2, 4, 2, 2, True), (2, 6, 2, 2, True),
+                (3, 4, 1, 2, True), (3, 6, 1, 2, True), (4, 4, 1, 2, True), (4, 6, 1, 2, True)]
+# kinds 3 and 4: double buffered with 4 and 2 x loads per block (batches of
+# up to 8 and 4 rows; skipped above).
+_REUSE_KINDS = ("tiles", "lds", "pf", "pfx4", "pfx2")
+_REUSE_MAX_B = {3: 8, 4: 4}
 
 
 def sweep_reuse(flush, steps: int) -> dict:
@@ -264,6 +268,8 @@ def sweep_reuse(flush, steps: int) -> dict:
                 runs=2)}
             for shape in REUSE_SHAPES:
                 kind, ks, rt, sg, pairs = shape
+                if b > _REUSE_MAX_B.get(kind, b):
+                    continue
                 y.fill_(float("nan"))
                 if benchlib.reuse(kind, ks, rt, sg, pairs, pk[0], sc[0], x, y) == 3:
                     raise RuntimeError(f"reuse {shape} is not instantiated")
