@@ -620,8 +620,9 @@ DKB_API int dkb_reuse_split(int kind, int KS, int RT, int S, const void* packed,
 // of 16): kind 0 gate_up_silu_tiles<KS, 2, pairs> (MFMA operands loaded
 // directly), kind 1 gate_up_silu_tiles_lds<KS, pairs> (both operands staged
 // in LDS), kind 2 gate_up_silu_tiles_pf<KS> (staged and double buffered;
-// pairs only). Returns 3 (nothing launched) for a shape not instantiated
-// here.
+// pairs only), kind 3 gate_up_silu_tiles_pf<KS, 4> (4 x loads per block, up
+// to 8 batch rows). Returns 3 (nothing launched) for a shape not
+// instantiated here.
 DKB_API int dkb_gate_up(int kind, int KS, int pairs, const void* gate, const void* gate_scales,
                         const void* up, const void* up_scales, const void* x, void* h, int I, int H,
                         int B, hipStream_t stream) {
@@ -643,6 +644,10 @@ DKB_API int dkb_gate_up(int kind, int KS, int pairs, const void* gate, const voi
   DKB_GU(1, 4, true, (dk::gate_up_silu_tiles_lds<4, true>))
   DKB_GU(2, 4, true, (dk::gate_up_silu_tiles_pf<4>))
   DKB_GU(2, 6, true, (dk::gate_up_silu_tiles_pf<6>))
+  if (B <= 8) {
+    DKB_GU(3, 4, true, (dk::gate_up_silu_tiles_pf<4, 4>))
+    DKB_GU(3, 6, true, (dk::gate_up_silu_tiles_pf<6, 4>))
+  }
 #undef DKB_GU
   return 3;
 }

@@ -505,6 +505,12 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
     if (pairs && I <= 4096 && B >= 9 && B <= 16)
       return L("gate/up launch", dk::gate_up_silu_tiles_pf<4>, grid, dim3(4 * 64), 0, g, gs, u, us,
                x, I, H, B, h);
+    // Below 9 batch rows (2049-4096 rows), with four x loads per block:
+    // I = 3584, H = 8192, B = 3 9.08 (9.40), B = 8 9.63 (10.34); I = 2752,
+    // H = 4096, B = 8 6.12 (6.48).
+    if (pairs && I <= 4096 && B <= 8)
+      return L("gate/up launch", dk::gate_up_silu_tiles_pf<4, 4>, grid, dim3(4 * 64), 0, g, gs, u,
+               us, x, I, H, B, h);
     if (B >= 8) {
       if (I <= 4096 && B <= 16)
         return pairs ? L("gate/up launch", dk::gate_up_silu_tiles_lds<8, true>, grid, dim3(8 * 64),

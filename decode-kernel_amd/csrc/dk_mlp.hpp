@@ -163,9 +163,11 @@ __global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles_lds(
 }
 
 // The same double buffered (the GEMV's gemv_reuse_pf): tiles 0 and 1 are
-// 16 rows of Wg and Wu, each block's loads issued a block ahead. Needs an
-// even number of groups per row and 4-byte aligned scales.
-template <int KS>
+// 16 rows of Wg and Wu, each block's loads issued a block ahead, kXL x
+// loads per block (batch tiles of up to 2 kXL rows: B <= 2 kXL or
+// kXL = 8). Needs an even number of groups per row and 4-byte aligned
+// scales.
+template <int KS, int kXL = 8>
 __global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles_pf(
     const uint4* __restrict__ gate, const uint16_t* __restrict__ gate_scales,
     const uint4* __restrict__ up, const uint16_t* __restrict__ up_scales,
@@ -194,7 +196,7 @@ __global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles_pf(
   win.Gs = G;
   win.gbeg = 0;
   f4_t acc[2];
-  reuse_pf_loop<KS, 2>(acc, lds, rw, rs, rx, win, lane, wave);
+  reuse_pf_loop<KS, 2, kXL>(acc, lds, rw, rs, rx, win, lane, wave);
   reuse_pf_publish(lds, acc, wave, lane);
   __syncthreads();
   const int b = win.bt0 + (lane & 15);

@@ -191,8 +191,9 @@ def reuse_split(kind: int, ks: int, rt: int, s: int, packed, scales, x, y, works
 def gate_up(kind: int, ks: int, pairs: bool, gp, gs, up, us, x, h) -> int:
     """The fused gate/up tile kernels: kind 0 gate_up_silu_tiles<KS, 2,
     pairs>, kind 1 gate_up_silu_tiles_lds<KS, pairs>, kind 2
-    gate_up_silu_tiles_pf<KS> (pairs). Returns 3 (nothing launched) for a
-    shape not instantiated in the measurement library."""
+    gate_up_silu_tiles_pf<KS> (pairs), kind 3 gate_up_silu_tiles_pf<KS, 4>
+    (up to 8 batch rows). Returns 3 (nothing launched) for a shape not
+    instantiated in the measurement library."""
     i, hd = gp.shape[0], gp.shape[1] * 8
     b = x.shape[0]
     rc = load().dkb_gate_up(kind, ks, int(pairs), gp.data_ptr(), gs.data_ptr(), up.data_ptr(),

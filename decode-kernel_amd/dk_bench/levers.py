@@ -356,7 +356,8 @@ def sweep_rsplit(flush, steps: int) -> dict:
 
 MLP_PROBLEMS = [(11008, 4096), (3584, 8192), (2752, 4096), (14336, 4096), (28672, 8192)]
 MLP_BATCHES = (3, 4, 8, 16, 32)
-MLP_SHAPES = [(0, 8, True), (1, 8, True), (1, 4, True), (2, 4, True), (2, 6, True)]
+MLP_SHAPES = [(0, 8, True), (1, 8, True), (1, 4, True), (2, 4, True), (2, 6, True), (3, 4, True),
+              (3, 6, True)]
 
 
 def sweep_mlp(flush, steps: int) -> dict:
@@ -388,6 +389,8 @@ def sweep_mlp(flush, steps: int) -> dict:
                                                             uss[j % n]), steps, flush, runs=2)}
             for shape in MLP_SHAPES:
                 kind, ks, pairs = shape
+                if b > _REUSE_MAX_B.get(kind, b):
+                    continue
                 hbuf.fill_(float("nan"))
                 if benchlib.gate_up(kind, ks, pairs, gps[0], gss[0], ups[0], uss[0], x, hbuf) == 3:
                     raise RuntimeError(f"gate/up {shape} is not instantiated")
