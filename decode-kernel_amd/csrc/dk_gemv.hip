@@ -633,21 +633,31 @@ struct PfShape {
 //   M = 8192, K = 28672: 26.88 (27.47)  29.74 (31.51)  33.20 (34.60)  66.16 (63.84)
 //   M = 5120, K = 5120:  7.64 (6.98)    8.07 (7.48)    8.16 (7.92)    14.11 (11.76)
 //   M = 28672, K = 8192: 34.93 (33.47)  36.79 (37.13)  39.34 (38.62)  70.05 (66.75)
-// Up to 8 batch rows (one batch tile), 6 waves with 4 x loads per block,
-// rows 8-15 of the x buffers held at zero (M = K = 4096: B = 3 4.33, B = 4
-// 4.35, B = 5 4.33 against 4.54, 4.59, 4.60 for the single-buffered tiles
-// or the streaming kernel; M = 2048, K = 16384, B = 5 9.35 against 9.73);
-// rows of 8192+ weights keep the single-buffered 16 waves at 3 batch rows
-// and rows of 8192+ at up to 5 (M = 4096, K = 11008, B = 4: 7.32 against
-// 7.74). One tile per wave up to 4096 rows; two from 4097 rows on rows of
-// 8192+ weights at 9-16 batch rows, and at 2049-4096 rows above 16. Above
-// 4096 rows up to 8 batch rows and at M <= 1024 above 32 batch rows (three
-// batch tiles) on rows shorter than 16384 weights the single-buffered
-// tiles stay (M = 6144, K = 8192, B = 8: 9.88 against 10.21; M = 512,
-// K = 8192, B = 33: 6.40 against 6.71).
+// Up to 8 batch rows (one batch tile), 4 x loads per block, rows 8-15 of
+// the x buffers held at zero: up to 4096 rows 6 waves of one tile (M = K =
+// 4096: B = 3 4.33, B = 4 4.35, B = 5 4.33 against 4.54, 4.59, 4.60 for the
+// single-buffered tiles or the streaming kernel; M = 2048, K = 16384,
+// B = 5 9.35 against 9.73), where rows of 8192+ weights keep the
+// single-buffered 16 waves at 3 batch rows and rows longer than 8192 at up
+// to 5 (M = 4096, K = 11008, B = 4: 7.32 against 7.74); from 4097 rows 4
+// waves of two tiles on rows of 8192+ weights, or at 8 batch rows (M = 8192,
+// K = 8192: B = 3 9.52, B = 8 10.01 against 9.82, 10.72; M = 8192, K = 3584,
+// B = 8 5.96 against 6.27), above 8192 rows only from 6 batch rows
+// (M = 28672, K = 8192, B = 8: 32.97 against 34.39; the direct tiles keep
+// B <= 5: B = 3 27.59 against 30.74). From 9 batch rows one tile per wave up
+// to 4096 rows; two from 4097 rows on rows of 8192+ weights at 9-16 batch
+// rows, and at 2049-4096 rows above 16. Above 8192 rows from 9 batch rows,
+// at 4097-8192 rows above 16, and at M <= 1024 above 32 batch rows (three
+// batch tiles) on rows shorter than 16384 weights the single-buffered tiles
+// stay (M = 6144, K = 8192, B = 32: 18.67 against 19.33; M = 512, K = 8192,
+// B = 33: 6.40 against 6.71).
 PfShape reuse_pf_shape(int M, int K, int B) {
-  if (M > 8192) return {};
-  if (M > 4096) return B >= 9 && B <= 16 && K >= 8192 ? PfShape{4, 2, 8} : PfShape{};
+  if (M > 8192) return B >= 6 && B <= 8 && K > 4096 ? PfShape{4, 2, 4} : PfShape{};
+  if (M > 4096) {
+    if (B >= 9 && B <= 16 && K >= 8192) return {4, 2, 8};
+    if (B <= 8 && (K >= 8192 || B == 8)) return {4, 2, 4};
+    return {};
+  }
   if (M > 2048) {
     if (B > 16) return K >= 8192 ? PfShape{4, 2, 8} : PfShape{};
     if (B >= 9) return {4, 1, 8};
@@ -688,7 +698,9 @@ int launch_reuse_tiles(const Launch& L, const uint4* p, const uint16_t* s, const
     const PfShape pf = reuse_pf_shape(M, K, B);
     if (pf.ks == 6) return launch_reuse_pf<6, 1, 4>(L, p, s, x, y, M, K, B);
     if (pf.ks == 4 && pf.rt == 1) return launch_reuse_pf<4, 1, 8>(L, p, s, x, y, M, K, B);
-    if (pf.ks == 4 && pf.rt == 2) return launch_reuse_pf<4, 2, 8>(L, p, s, x, y, M, K, B);
+    if (pf.ks == 4 && pf.rt == 2)
+      return pf.xl == 8 ? launch_reuse_pf<4, 2, 8>(L, p, s, x, y, M, K, B)
+                        : launch_reuse_pf<4, 2, 4>(L, p, s, x, y, M, K, B);
   }
   if (M > 2048 && M <= 4096 && K <= 4096 && B <= 5)
     return launch_reuse<8, 1, 2>(L, p, s, x, y, M, K, B);
@@ -773,6 +785,7 @@ enum class ReuseShape { kStream, kTiles };
 //   M = 3072, K = 8192,  B = 3: tiles 6.40 (stream 7.11)
 //   M = 6144, K = 8192,  B = 3: tiles 9.14 (stream 10.45)
 //   M = 11008, K = 4096, B = 3: tiles 7.82 (stream 8.51)
+//   M = 8192, K = 3584,  B = 3: tiles 5.77 (stream 6.43)
 //   M = 2560, K = 8192,  B = 4: tiles 6.27 (stream 9.61)
 //   M = K = 4096,        B = 3: tiles 4.33 (stream 4.54; double buffered)
 //   M = 2048, K = 4096,  B = 8: tiles 4.30 (stream 4.71; double buffered)
@@ -790,7 +803,7 @@ ReuseShape reuse_shape(int M, int K, int B) {
   if (M <= 2048 && (B <= 4 || (B <= 8 && K < 8192 && (K / DK_GROUP_SIZE) % 2 == 1)))
     return ReuseShape::kStream;
   if (B == 3) {
-    const bool tiles = K >= 8192 || M > 8192 || (size_t)M * (size_t)K >= ((size_t)1 << 27) ||
+    const bool tiles = K >= 8192 || M >= 8192 || (size_t)M * (size_t)K >= ((size_t)1 << 27) ||
                        (M >= 3072 && K > 4096 && K < 8192) || (M > 2048 && M <= 4096 && K <= 4096);
     return tiles ? ReuseShape::kTiles : ReuseShape::kStream;
   }

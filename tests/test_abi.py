@@ -196,6 +196,10 @@ ROUTES = [
     ((11008, 4096, 4), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 1, true, 2>", [688, 1, 1]),
     ((11008, 4096, 3), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 1, true, 2>", [688, 1, 1]),
     ((6144, 8192, 12), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 2, 8>", [192, 1, 1]),
+    ((6144, 8192, 8), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 2, 4>", [192, 1, 1]),
+    ((28672, 8192, 8), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 2, 4>", [896, 1, 1]),
+    ((8192, 3584, 3), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 2, true, 2>", [256, 1, 1]),
+    ((5120, 5120, 4), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 2, true, 2>", [160, 1, 1]),
     ((6144, 8192, 32), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 2, true, 2>", [192, 2, 1]),
     ((5120, 5120, 12), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 2, true, 2>", [160, 1, 1]),
     ((2048, 16384, 16), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1, 8>", [128, 1, 1]),
