@@ -563,7 +563,7 @@ DKB_API int dkb_reuse(int kind, int KS, int RT, int SG, int pairs, const void* p
     return launch_error("reuse pf");                                                           \
   }
   DKB_RX(3, 4, 1, 4) DKB_RX(3, 6, 1, 4) DKB_RX(4, 4, 1, 2) DKB_RX(4, 6, 1, 2) DKB_RX(3, 4, 2, 4)
-  DKB_RX(3, 6, 2, 4)
+  DKB_RX(3, 6, 2, 4) DKB_RX(3, 8, 1, 4) DKB_RX(3, 8, 2, 4)
 #undef DKB_RX
   DKB_R0(8, 1, 2, true) DKB_R0(8, 1, 2, false) DKB_R0(8, 1, 4, false) DKB_R0(16, 1, 4, false)
   DKB_R0(16, 1, 2, false) DKB_R0(8, 2, 2, true) DKB_R0(8, 2, 2, false) DKB_R0(8, 2, 4, false)

@@ -505,10 +505,13 @@ int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const ui
     if (pairs && I <= 4096 && B >= 9 && B <= 16)
       return L("gate/up launch", dk::gate_up_silu_tiles_pf<4>, grid, dim3(4 * 64), 0, g, gs, u, us,
                x, I, H, B, h);
-    // Below 9 batch rows (2049-4096 rows), with four x loads per block:
-    // I = 3584, H = 8192, B = 3 9.08 (9.40), B = 8 9.63 (10.34); I = 2752,
-    // H = 4096, B = 8 6.12 (6.48).
-    if (pairs && I <= 4096 && B <= 8)
+    // Below 9 batch rows, with four x loads per block (the x buffers then
+    // hold 8 rows: two workgroups per CU): I = 3584, H = 8192, B = 3 9.08
+    // (9.40), B = 8 9.63 (10.34); I = 28672, H = 8192, B = 3 45.93 (46.95),
+    // B = 8 51.42 (56.29); I = 11008, H = 4096, B = 8 12.93 (13.51). From
+    // 4097 to 16384 rows the direct tiles keep 3-4 batch rows (I = 11008,
+    // B = 3: 11.97 against 12.31).
+    if (pairs && B <= 8 && (I <= 4096 || I > 16384 || B >= 5))
       return L("gate/up launch", dk::gate_up_silu_tiles_pf<4, 4>, grid, dim3(4 * 64), 0, g, gs, u,
                us, x, I, H, B, h);
     if (B >= 8) {
@@ -623,49 +626,54 @@ struct PfShape {
 // only). From the sweep of every tile kernel (dk_bench.levers reuse), us,
 // the double-buffered tiles against the best single-buffered ones in
 // brackets; from 9 batch rows 4 waves with 8 x loads per block:
-//                        B = 8          B = 12         B = 16         B = 32
-//   M = K = 4096:        4.56 (4.87)    4.88 (5.17)    4.97 (5.45)    6.50 (6.37)
-//   M = 4096, K = 11008: 8.55 (8.71)    9.44 (9.59)    10.00 (10.76)  12.94 (13.39)
-//   M = 3072, K = 8192:  6.72 (7.01)    7.36 (7.81)    7.76 (8.52)    10.02 (10.58)
-//   M = 2048, K = 16384: 9.97 (10.73)   11.53 (12.01)  12.33 (13.62)  12.24 (13.44)
-//   M = 2048, K = 4096:  4.30 (4.65)    4.73 (4.87)    4.79 (5.09)    4.79 (5.13)
-//   M = 6144, K = 8192:  10.21 (9.88)   10.44 (10.73)  10.82 (11.46)  19.33 (18.67)
-//   M = 8192, K = 28672: 26.88 (27.47)  29.74 (31.51)  33.20 (34.60)  66.16 (63.84)
-//   M = 5120, K = 5120:  7.64 (6.98)    8.07 (7.48)    8.16 (7.92)    14.11 (11.76)
-//   M = 28672, K = 8192: 34.93 (33.47)  36.79 (37.13)  39.34 (38.62)  70.05 (66.75)
-// Up to 8 batch rows (one batch tile), 4 x loads per block, rows 8-15 of
-// the x buffers held at zero: up to 4096 rows 6 waves of one tile (M = K =
-// 4096: B = 3 4.33, B = 4 4.35, B = 5 4.33 against 4.54, 4.59, 4.60 for the
-// single-buffered tiles or the streaming kernel; M = 2048, K = 16384,
-// B = 5 9.35 against 9.73), where rows of 8192+ weights keep the
-// single-buffered 16 waves at 3 batch rows and rows longer than 8192 at up
-// to 5 (M = 4096, K = 11008, B = 4: 7.32 against 7.74); from 4097 rows 4
-// waves of two tiles on rows of 8192+ weights, or at 8 batch rows (M = 8192,
-// K = 8192: B = 3 9.52, B = 8 10.01 against 9.82, 10.72; M = 8192, K = 3584,
-// B = 8 5.96 against 6.27), above 8192 rows only from 6 batch rows
-// (M = 28672, K = 8192, B = 8: 32.97 against 34.39; the direct tiles keep
-// B <= 5: B = 3 27.59 against 30.74). From 9 batch rows one tile per wave up
-// to 4096 rows; two from 4097 rows on rows of 8192+ weights at 9-16 batch
-// rows, and at 2049-4096 rows above 16. Above 8192 rows from 9 batch rows,
-// at 4097-8192 rows above 16, and at M <= 1024 above 32 batch rows (three
-// batch tiles) on rows shorter than 16384 weights the single-buffered tiles
-// stay (M = 6144, K = 8192, B = 32: 18.67 against 19.33; M = 512, K = 8192,
-// B = 33: 6.40 against 6.71).
+//                        B = 12         B = 16         B = 32
+//   M = K = 4096:        4.88 (5.17)    4.97 (5.45)    6.50 (6.37)
+//   M = 4096, K = 11008: 9.44 (9.59)    10.00 (10.76)  12.94 (13.39)
+//   M = 3072, K = 8192:  7.36 (7.81)    7.76 (8.52)    10.02 (10.58)
+//   M = 2048, K = 16384: 11.53 (12.01)  12.33 (13.62)  12.24 (13.44)
+//   M = 2048, K = 4096:  4.73 (4.87)    4.79 (5.09)    4.79 (5.13)
+//   M = 6144, K = 8192:  10.44 (10.73)  10.82 (11.46)  19.33 (18.67)
+//   M = 8192, K = 28672: 29.74 (31.51)  33.20 (34.60)  66.16 (63.84)
+//   M = 5120, K = 5120:  8.07 (7.48)    8.16 (7.92)    14.11 (11.76)
+//   M = 28672, K = 8192: 36.79 (37.13)  39.34 (38.62)  70.05 (66.75)
+// Up to 8 batch rows (one batch tile) 4 or 2 x loads per block (XL), the x
+// buffers holding only those 8 or 4 rows (the MFMA reads zeros for the
+// rest), which leaves room for two workgroups per CU:
+//                        B = 3               B = 5               B = 8
+//   M = K = 4096:        4.34 (4.41) 6,1,2   4.37 (4.60) 6,1,4   4.56 (4.87) 6,1,4
+//   M = 3072, K = 8192:  6.01 (6.20) 8,1,4   6.22 (6.77) 8,1,4   6.61 (7.01) 8,1,4
+//   M = 2048, K = 16384: (stream 7.86)       9.15 (9.73) 8,1,4   9.83 (10.73) 8,1,4
+//   M = 11008, K = 4096: 7.50 (7.65) 4,1,2   7.82 (7.96) 4,1,4   8.32 (9.13) 4,1,4
+//   M = 28672, K = 8192: 25.42 (27.56) 4,1,2 27.53 (28.85) 4,2,4 29.45 (33.47) 4,2,4
+//   M = 6144, K = 8192:  8.96 (8.92) 4,2,4   9.03 (9.10) 4,2,4   9.24 (9.88) 4,2,4
+// (KS, RT, XL after each). The single-buffered tiles keep 3-5 batch rows on
+// rows longer than 8192 weights at 2049-4096 rows (M = 4096, K = 11008,
+// B = 4: 7.32 against 7.62) and rows shorter than 8192 at 4097-8192 rows up
+// to 5 (M = 5120, K = 5120, B = 3: 6.21 against 6.54), above 16 batch rows
+// at 4097+ rows and from 9 above 8192 rows, and at M <= 1024 above 32
+// batch rows (three batch tiles) on rows shorter than 16384 weights
+// (M = 512, K = 8192, B = 33: 6.40 against 6.71).
 PfShape reuse_pf_shape(int M, int K, int B) {
-  if (M > 8192) return B >= 6 && B <= 8 && K > 4096 ? PfShape{4, 2, 4} : PfShape{};
+  if (M > 8192) {
+    if (B > 8) return {};
+    if (B <= 4) return {4, 1, 2};
+    return K > 4096 ? PfShape{4, 2, 4} : PfShape{4, 1, 4};
+  }
   if (M > 4096) {
     if (B >= 9 && B <= 16 && K >= 8192) return {4, 2, 8};
-    if (B <= 8 && (K >= 8192 || B == 8)) return {4, 2, 4};
+    if (B <= 8 && (K >= 8192 || B >= 6)) return {4, 2, 4};
     return {};
   }
   if (M > 2048) {
     if (B > 16) return K >= 8192 ? PfShape{4, 2, 8} : PfShape{};
     if (B >= 9) return {4, 1, 8};
-    if (B >= 6 || (B >= 4 && K <= 8192) || K <= 4096) return {6, 1, 4};
-    return {};
+    if (K <= 4096) return B <= 4 ? PfShape{6, 1, 2} : PfShape{6, 1, 4};
+    if (K > 8192 && B <= 5) return {};
+    return {8, 1, 4};
   }
   if (B >= 9) return M <= 1024 && B > 32 && K < 16384 ? PfShape{} : PfShape{4, 1, 8};
-  return B >= 5 ? PfShape{6, 1, 4} : PfShape{};
+  if (B < 5) return {};
+  return K >= 8192 ? PfShape{8, 1, 4} : PfShape{6, 1, 4};
 }
 
 // The single-pass tiles. Where the double-buffered tiles do not run
@@ -696,8 +704,15 @@ int launch_reuse_tiles(const Launch& L, const uint4* p, const uint16_t* s, const
                        uint16_t* y, int M, int K, int B) {
   if ((K / DK_GROUP_SIZE) % 2 == 0 && aligned(s, 4)) {
     const PfShape pf = reuse_pf_shape(M, K, B);
-    if (pf.ks == 6) return launch_reuse_pf<6, 1, 4>(L, p, s, x, y, M, K, B);
-    if (pf.ks == 4 && pf.rt == 1) return launch_reuse_pf<4, 1, 8>(L, p, s, x, y, M, K, B);
+    if (pf.ks == 8) return launch_reuse_pf<8, 1, 4>(L, p, s, x, y, M, K, B);
+    if (pf.ks == 6)
+      return pf.xl == 2 ? launch_reuse_pf<6, 1, 2>(L, p, s, x, y, M, K, B)
+                        : launch_reuse_pf<6, 1, 4>(L, p, s, x, y, M, K, B);
+    if (pf.ks == 4 && pf.rt == 1) {
+      if (pf.xl == 2) return launch_reuse_pf<4, 1, 2>(L, p, s, x, y, M, K, B);
+      if (pf.xl == 4) return launch_reuse_pf<4, 1, 4>(L, p, s, x, y, M, K, B);
+      return launch_reuse_pf<4, 1, 8>(L, p, s, x, y, M, K, B);
+    }
     if (pf.ks == 4 && pf.rt == 2)
       return pf.xl == 8 ? launch_reuse_pf<4, 2, 8>(L, p, s, x, y, M, K, B)
                         : launch_reuse_pf<4, 2, 4>(L, p, s, x, y, M, K, B);

@@ -1078,9 +1078,11 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_lds(const uint4* __restric
 // __restrict__ pointers, which lets the compiler wait for the block being
 // computed without waiting for the one being loaded.
 // ---------------------------------------------------------------------------
-template <int KS, int RT>
+// XR: batch rows staged per x buffer (16, or 8 / 4 for batch tiles of at
+// most that many rows; the MFMA then reads zeros for rows XR..15).
+template <int KS, int RT, int XR = 16>
 struct ReusePfLds {
-  uint4 x[2][KS][16 * 32];
+  uint4 x[2][KS][XR * 32];
   uint4 w[2][KS][RT * 16 * 8];
   uint4 s[2][KS][RT * 16];
   int last;  // the split-K form's ticket result
@@ -1112,9 +1114,9 @@ struct ReuseWindow {
 };
 
 // Issues the loads of the block at window group g0 into xb, wb, sb: the
-// kXL x loads of batch rows bt0 .. bt0 + 2 kXL - 1, those of rows >= B out
-// of range, so that each block issues the same number of loads (rows from
-// 2 kXL on are never loaded: the caller keeps them zero).
+// kXL x loads of batch rows bt0 .. bt0 + 2 kXL - 1 (the rows the x buffer
+// holds), those of rows >= B out of range, so that each block issues the
+// same number of loads.
 template <int RT, int kXL>
 __device__ __forceinline__ void reuse_pf_issue(uint4* __restrict__ xb, uint4* __restrict__ wb,
                                                uint4* __restrict__ sb,
@@ -1197,7 +1199,11 @@ __device__ __forceinline__ void reuse_pf_step(f4_t (&acc)[RT], const uint4* __re
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int xc = 16 * u + 4 * kq + j;
-      xp[j] = pair_x8(cx[r_lane * 32 + ((xc & 16) | ((xc ^ stage_swizzle<32>(r_lane)) & 15))]);
+      // Batch rows from 2 kXL on are not staged: zeros.
+      const uint4 xv = 2 * kXL >= 16 || r_lane < 2 * kXL
+                           ? cx[r_lane * 32 + ((xc & 16) | ((xc ^ stage_swizzle<32>(r_lane)) & 15))]
+                           : uint4{0u, 0u, 0u, 0u};
+      xp[j] = pair_x8(xv);
     }
 #pragma unroll
     for (int t = 0; t < RT; ++t) {
@@ -1216,10 +1222,10 @@ __device__ __forceinline__ void reuse_pf_step(f4_t (&acc)[RT], const uint4* __re
 }
 
 // acc[t] over the wave's blocks of the window (window groups 2 wave, 2 wave
-// + 1, then every 2 KS; G even), two buffers in turn. With kXL < 8 (batch
-// tiles of at most 2 kXL rows) the x rows from 2 kXL on are zeroed once.
+// + 1, then every 2 KS; G even), two buffers in turn; with kXL < 8 (batch
+// tiles of at most 2 kXL rows) the x buffers hold 2 kXL rows.
 template <int KS, int RT, int kXL = 8>
-__device__ __forceinline__ void reuse_pf_loop(f4_t (&acc)[RT], ReusePfLds<KS, RT>& lds,
+__device__ __forceinline__ void reuse_pf_loop(f4_t (&acc)[RT], ReusePfLds<KS, RT, 2 * kXL>& lds,
                                               const __amdgpu_buffer_rsrc_t (&rw)[RT],
                                               const __amdgpu_buffer_rsrc_t (&rs)[RT],
                                               __amdgpu_buffer_rsrc_t rx, const ReuseWindow& win,
@@ -1235,14 +1241,6 @@ __device__ __forceinline__ void reuse_pf_loop(f4_t (&acc)[RT], ReusePfLds<KS, RT
   uint4* sa = lds.s[0][wave];
   uint4* sb = lds.s[1][wave];
   static_assert(kXL == 2 || kXL == 4 || kXL == 8, "x loads per block");
-  if constexpr (kXL < 8) {
-    // Rows 2 kXL .. 15 of both x buffers (64 lanes x 16 bytes per store).
-#pragma unroll
-    for (int i = kXL; i < 8; ++i) {
-      xa[i * 64 + lane] = uint4{0u, 0u, 0u, 0u};
-      xb[i * 64 + lane] = uint4{0u, 0u, 0u, 0u};
-    }
-  }
   int g = 2 * wave;
   reuse_pf_issue<RT, kXL>(xa, wa, sa, rw, rs, rx, win, lane, g);
   for (int n = 0;;) {
@@ -1268,8 +1266,8 @@ __device__ __forceinline__ void reuse_pf_loop(f4_t (&acc)[RT], ReusePfLds<KS, RT
 // Tile t's KS wave partials, published in each wave's first x buffer (no
 // other wave touches it; every load of the wave has landed) and, after a
 // barrier, added in wave order.
-template <int KS, int RT>
-__device__ __forceinline__ void reuse_pf_publish(ReusePfLds<KS, RT>& lds, const f4_t (&acc)[RT],
+template <int KS, int RT, int XR>
+__device__ __forceinline__ void reuse_pf_publish(ReusePfLds<KS, RT, XR>& lds, const f4_t (&acc)[RT],
                                                  int wave, int lane) {
   float* part = reinterpret_cast<float*>(lds.x[0][wave]);
 #pragma unroll
@@ -1278,8 +1276,8 @@ __device__ __forceinline__ void reuse_pf_publish(ReusePfLds<KS, RT>& lds, const 
     for (int v = 0; v < 4; ++v) part[(t * 64 + lane) * 4 + v] = acc[t][v];
 }
 
-template <int KS, int RT>
-__device__ __forceinline__ f4_t reuse_pf_sum(const ReusePfLds<KS, RT>& lds, int t, int lane) {
+template <int KS, int RT, int XR>
+__device__ __forceinline__ f4_t reuse_pf_sum(const ReusePfLds<KS, RT, XR>& lds, int t, int lane) {
   f4_t sum = {0.f, 0.f, 0.f, 0.f};
   for (int w2 = 0; w2 < KS; ++w2) {
     const float* pw = reinterpret_cast<const float*>(lds.x[0][w2]);
@@ -1290,8 +1288,8 @@ __device__ __forceinline__ f4_t reuse_pf_sum(const ReusePfLds<KS, RT>& lds, int 
 }
 
 // Wave t < RT: tile t's sums (zeros in the other waves).
-template <int KS, int RT>
-__device__ __forceinline__ f4_t reuse_pf_partials(ReusePfLds<KS, RT>& lds, const f4_t (&acc)[RT],
+template <int KS, int RT, int XR>
+__device__ __forceinline__ f4_t reuse_pf_partials(ReusePfLds<KS, RT, XR>& lds, const f4_t (&acc)[RT],
                                                   int wave, int lane) {
   reuse_pf_publish(lds, acc, wave, lane);
   __syncthreads();
@@ -1310,7 +1308,7 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_pf(const uint4* __restrict
                                                          int B) {
   static_assert(KS >= RT, "wave t sums tile t");
   write_stamp(DK_STAMP_REUSE);
-  __shared__ ReusePfLds<KS, RT> lds;
+  __shared__ ReusePfLds<KS, RT, 2 * kXL> lds;
   const int G = K >> 7;
   const int nck = K >> 5;
   const int lane = threadIdx.x & 63;

@@ -173,7 +173,7 @@ __global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles_pf(
     const uint4* __restrict__ up, const uint16_t* __restrict__ up_scales,
     const uint4* __restrict__ x4, int I, int H, int B, uint16_t* __restrict__ h) {
   write_stamp(kStampGateUp);
-  __shared__ ReusePfLds<KS, 2> lds;
+  __shared__ ReusePfLds<KS, 2, 2 * kXL> lds;
   const int G = H >> 7;
   const int nck = H >> 5;
   const int lane = threadIdx.x & 63;

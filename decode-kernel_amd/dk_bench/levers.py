@@ -237,7 +237,7 @@ REUSE_SHAPES = [(0, 8, 1, 2, True), (0, 8, 1, 4, False), (0, 16, 1, 4, False), (
                 (1, 4, 2, 2, True), (1, 8, 1, 4, True), (1, 4, 1, 4, True), (1, 4, 2, 4, True),
                 (2, 4, 1, 2, True), (2, 6, 1, 2, True), (2, 4, 2, 2, True), (2, 6, 2, 2, True),
                 (3, 4, 1, 2, True), (3, 6, 1, 2, True), (4, 4, 1, 2, True), (4, 6, 1, 2, True),
-                (3, 4, 2, 2, True), (3, 6, 2, 2, True)]
+                (3, 4, 2, 2, True), (3, 6, 2, 2, True), (3, 8, 1, 2, True), (3, 8, 2, 2, True)]
 # kinds 3 and 4: double buffered with 4 and 2 x loads per block (batches of
 # up to 8 and 4 rows; skipped above).
 _REUSE_KINDS = ("tiles", "lds", "pf", "pfx4", "pfx2")

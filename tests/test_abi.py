@@ -151,8 +151,8 @@ def test_describe_names_the_dispatched_kernel(lib):
     assert d["kernel"].startswith("void dk::gemv_v4_split<")
     assert _abi.describe(lib, 4096, 4096, 16, reuse_weights=1)["kernel"].startswith(
         "void dk::gemv_reuse_pf<4, 1, 8>")
-    assert _abi.describe(lib, 28672, 8192, 4, reuse_weights=1)["kernel"].startswith(
-        "void dk::gemv_reuse<8, 2, 2, true>")
+    assert _abi.describe(lib, 28672, 8320, 4, reuse_weights=1)["kernel"].startswith(
+        "void dk::gemv_reuse<8, 2, 2, false>")
     assert _abi.describe(lib, 4096, 4096, 2, reuse_weights=1)["kernel"].startswith(
         "void dk::gemv_v5_lds<") and ", 15, " in _abi.describe(lib, 4096, 4096, 2,
                                                               reuse_weights=1)["kernel"]
@@ -177,24 +177,28 @@ ROUTES = [
     ((8192, 28672, 1), {}, "dk::gemv_v5_lds<2, 1, 16, 1, true,", [256, 1, 1]),
     ((4096, 4096, 2), dict(reuse_weights=1), "dk::gemv_v5_lds<1, 2, 8, 2, true, dk::LayoutLogical, 15,",
      [512, 1, 1]),
-    ((4096, 4096, 4), dict(reuse_weights=1), "dk::gemv_reuse_pf<6, 1, 4>", [256, 1, 1]),
+    ((4096, 4096, 4), dict(reuse_weights=1), "dk::gemv_reuse_pf<6, 1, 2>", [256, 1, 1]),
     ((4096, 4096, 8), dict(reuse_weights=1), "dk::gemv_reuse_pf<6, 1, 4>", [256, 1, 1]),
     ((4096, 4096, 16), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1, 8>", [256, 1, 1]),
     ((4096, 4096, 32), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 2, true, 2>", [128, 2, 1]),
     ((4096, 11008, 32), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 2, 8>", [128, 2, 1]),
-    ((3072, 8192, 8), dict(reuse_weights=1), "dk::gemv_reuse_pf<6, 1, 4>", [192, 1, 1]),
-    ((3072, 8192, 3), dict(reuse_weights=1), "dk::gemv_reuse_lds<16, 1, true, 2>", [192, 1, 1]),
-    ((4096, 4096, 3), dict(reuse_weights=1), "dk::gemv_reuse_pf<6, 1, 4>", [256, 1, 1]),
+    ((3072, 8192, 8), dict(reuse_weights=1), "dk::gemv_reuse_pf<8, 1, 4>", [192, 1, 1]),
+    ((3072, 8192, 3), dict(reuse_weights=1), "dk::gemv_reuse_pf<8, 1, 4>", [192, 1, 1]),
+    ((4096, 4096, 3), dict(reuse_weights=1), "dk::gemv_reuse_pf<6, 1, 2>", [256, 1, 1]),
     ((4096, 11008, 4), dict(reuse_weights=1), "dk::gemv_reuse_lds<16, 1, true, 2>", [256, 1, 1]),
     ((4096, 3968, 4), dict(reuse_weights=1), "dk::gemv_reuse<8, 1, 2, false>", [256, 1, 1]),
     ((2048, 4096, 8), dict(reuse_weights=1), "dk::gemv_reuse_pf<6, 1, 4>", [128, 1, 1]),
     ((2048, 4224, 8), dict(reuse_weights=1), "dk::gemv_v5_lds<1, 1, 16, 4, true, dk::LayoutLogical, 15,",
      [128, 2, 1]),
-    ((2560, 8192, 4), dict(reuse_weights=1), "dk::gemv_reuse_pf<6, 1, 4>", [160, 1, 1]),
-    ((28672, 8192, 4), dict(reuse_weights=1), "dk::gemv_reuse<8, 2, 2, true>", [896, 1, 1]),
+    ((2560, 8192, 4), dict(reuse_weights=1), "dk::gemv_reuse_pf<8, 1, 4>", [160, 1, 1]),
+    ((28672, 8192, 4), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1, 2>", [1792, 1, 1]),
+    ((28672, 8320, 4), dict(reuse_weights=1), "dk::gemv_reuse<8, 2, 2, false>", [896, 1, 1]),
     ((28672, 8192, 16), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 2, true, 2>", [896, 1, 1]),
-    ((11008, 4096, 4), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 1, true, 2>", [688, 1, 1]),
-    ((11008, 4096, 3), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 1, true, 2>", [688, 1, 1]),
+    ((11008, 4096, 4), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1, 2>", [688, 1, 1]),
+    ((11008, 3968, 4), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 1, false, 2>", [688, 1, 1]),
+    ((11008, 4096, 3), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1, 2>", [688, 1, 1]),
+    ((11008, 4096, 8), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1, 4>", [688, 1, 1]),
+    ((4096, 11008, 5), dict(reuse_weights=1), "dk::gemv_reuse_lds<16, 1, true, 2>", [256, 1, 1]),
     ((6144, 8192, 12), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 2, 8>", [192, 1, 1]),
     ((6144, 8192, 8), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 2, 4>", [192, 1, 1]),
     ((28672, 8192, 8), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 2, 4>", [896, 1, 1]),
@@ -203,7 +207,7 @@ ROUTES = [
     ((6144, 8192, 32), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 2, true, 2>", [192, 2, 1]),
     ((5120, 5120, 12), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 2, true, 2>", [160, 1, 1]),
     ((2048, 16384, 16), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1, 8>", [128, 1, 1]),
-    ((2048, 16384, 8), dict(reuse_weights=1), "dk::gemv_reuse_pf<6, 1, 4>", [128, 1, 1]),
+    ((2048, 16384, 8), dict(reuse_weights=1), "dk::gemv_reuse_pf<8, 1, 4>", [128, 1, 1]),
     ((2048, 16512, 16), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 1, false, 4>", [128, 1, 1]),
     ((1024, 16384, 16), dict(reuse_weights=1), "dk::gemv_reuse_split_pf<4, 1>", [64, 1, 2]),
     ((1024, 28672, 16), dict(reuse_weights=1), "dk::gemv_reuse_split_pf<4, 1>", [64, 1, 4]),

@@ -183,7 +183,7 @@ def test_reuse_small_batches_run_the_streaming_kernel():
                                    (4096, 4096, 4), (3000, 4096, 5), (2000, 16512, 13),
                                    (1500, 8320, 9), (4100, 8192, 12), (4096, 11008, 32),
                                    (1000, 16384, 33), (2040, 8192, 20), (1500, 8192, 7),
-                                   (4500, 8192, 8), (9000, 8192, 7)])
+                                   (4500, 8192, 8), (9000, 8192, 7), (11008, 4096, 3)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
     # The single-pass MFMA tile kernels in each of their shapes (operands
     # staged in LDS: one tile per wave with 16 or 8 waves, two tiles per wave
