@@ -611,6 +611,10 @@ int launch_reuse_lds(const Launch& L, const uint4* p, const uint16_t* s, const u
 template <int KS, int RT, int XL>
 int launch_reuse_pf(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
                     int M, int K, int B) {
+  // XL < 8 stages only batch rows 0 .. 2 XL - 1 of one batch tile.
+  if (XL < 8 && B > 2 * XL)
+    return fail(DK_ERR_UNSUPPORTED, "internal: %d x loads per block cannot serve %d batch rows", XL,
+                B);
   const dim3 grid((M + 16 * RT - 1) / (16 * RT), (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
   return L("reuse launch", dk::gemv_reuse_pf<KS, RT, XL>, grid, dim3(KS * 64), 0, p, s, x, y, M, K,
            B);
