@@ -8,7 +8,10 @@ W4A16 GEMV at M=4096, K=4096, B=1, with p50 latency. One "step" is one GEMV
 launch over packed weights resident in HBM. `--warmup` untimed steps run
 first; then exactly `--steps` steps run back-to-back, captured in one HIP
 graph, step i reading weight copy i mod n where the n copies total more than
-640 MB, as in a decode pass over many layers. Before each of 5 timed replays
+640 MB, as in a decode pass over many layers. Each step's output is released
+when the next step's is kept (the caching allocator hands the block back, as
+it does in a decode loop and in the reference's timing loop); only the last
+one is held, to check the replays against an eager launch. Before each of 5 timed replays
 a 1 GiB read is enqueued on the same stream, outside the events: it flushes
 the L2s and the 256 MB Infinity Cache, so every replay starts cold whatever
 --steps is. The timed span is bracketed inside the graph on the GPU's own
@@ -115,6 +118,19 @@ def make_inputs(m, k, batch, seed):
     return (packed.cuda(), scales.cuda(), torch.from_numpy(x).cuda(), packed, scales, x)
 
 
+class LastOutput:
+    """Keeps only the latest step's output. Holding all `steps` outputs of a
+    graph would make every step write fresh pages (at B >= 4 on 4096 x 4096,
+    0.2 us per step); a decode loop, like the reference's timing loop, writes
+    into the block its previous output freed."""
+
+    def __init__(self):
+        self.y = None
+
+    def __call__(self, y):
+        self.y = y
+
+
 def bench_variant(ext, copies, x, variant, steps, flush, warmup=1, y_ref=None,
                   call_level_flush=None):
     """Exactly `steps` launches of one variant back-to-back (HIP graph), step
@@ -139,14 +155,14 @@ def bench_variant(ext, copies, x, variant, steps, flush, warmup=1, y_ref=None,
     if y_ref is not None and not torch_equal(y0, y_ref):
         raise RuntimeError(f"{variant}: output differs from the checked headline output")
     n = len(pk)
-    ys = []
-    st, graph = time_graph_steps(lambda i: ys.append(call(pk[i % n], sc[i % n], x)), steps=steps,
+    last = LastOutput()
+    st, graph = time_graph_steps(lambda i: last(call(pk[i % n], sc[i % n], x)), steps=steps,
                                  warmup=warmup, preroll=flush)
     # Every replayed step recomputes the same product: the last one must equal
     # the eager result bit for bit (graph replays checked against eager work).
-    if not torch_equal(ys[-1], y0):
+    if not torch_equal(last.y, y0):
         raise RuntimeError(f"{variant}: graph replay output differs from the eager launch")
-    del graph, ys
+    del graph, last
     m, k, b = pk[0].shape[0], pk[0].shape[1] * 8, x.shape[0]
     moved = bytes_moved_w4(m, k, b)
     row = {
@@ -352,13 +368,13 @@ def bench_mlp(roof_gbps, steps, flush=None):
         for batch in MLP_BATCHES:
             x = torch.randn(batch, h, device="cuda", generator=gen).half()
             y0 = mlp_decode(x, *copies[0])
-            ys = []
-            st, graph = time_graph_steps(lambda k: ys.append(mlp_decode(x, *copies[k % n])),
+            last = LastOutput()
+            st, graph = time_graph_steps(lambda k: last(mlp_decode(x, *copies[k % n])),
                                          steps=steps, preroll=flush)
-            if not torch.equal(ys[-1], y0):
+            if not torch.equal(last.y, y0):
                 raise RuntimeError(f"mlp {name} B={batch}: graph replay output differs from the "
                                    f"eager step")
-            del graph, ys
+            del graph, last
             reuse = batch > 1
 
             def unfused(k):
