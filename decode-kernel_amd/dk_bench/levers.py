@@ -1,6 +1,6 @@
 """Launch-shape and kernel-variant sweeps behind the routing choices.
 
-    python -m dk_bench.levers floor|c0|v4|split|reuse|rsplit|mlp|all [--steps 300] [--out PATH]
+    python -m dk_bench.levers floor|c0|v4|split|reuse|rsplit|mlp|cache|all [--steps 300] [--out PATH]
     (from decode-kernel_amd/, after build_ext.py)
 
   floor  read-probe launch shapes at the algorithmic bytes of c0, c1 and c2
@@ -24,7 +24,10 @@
          single-pass tiles at M <= 2048 on long rows, 5-33 batch rows,
          against the product's reuse path;
   mlp    the fused gate/up tile kernels (all three forms) at 3-32 batch rows on
-         Llama MLP shapes, against the product's fused gate/up.
+         Llama MLP shapes, against the product's fused gate/up;
+  cache  the product at one batch row with its weight copies cycled over
+         > 640 MB (cold, as bench.py), 128 or 64 MB (inside the Infinity
+         Cache) or two copies (largely in the L2s).
 Every variant that computes y is checked against the product's v5 output
 (bit-exact where the summation order is the same, else within 1e-3 plus one
 fp16 ulp) before it is timed. Timing as in bench.py: HIP graphs of `steps`
@@ -411,9 +414,42 @@ def sweep_mlp(flush, steps: int) -> dict:
     return out
 
 
+CACHE_PROBLEMS = [(4096, 4096), (8192, 3584), (4096, 11008)]
+# Working sets the weight copies are cycled over: past the Infinity Cache
+# (cold, as bench.py), inside it but past the L2s, and two copies.
+CACHE_SETS = {"cold": 640 << 20, "mall_128MB": 128 << 20, "mall_64MB": 64 << 20, "two_copies": 0}
+
+
+def sweep_cache(flush, steps: int) -> dict:
+    """The product at one batch row with its weights cold in HBM against
+    the same copies cycled within the Infinity Cache or the L2s."""
+    from decode_kernel import _cuda
+
+    from .ablation import gpu_case
+    from .common import weight_copies
+
+    out = {}
+    for m, k in CACHE_PROBLEMS:
+        packed, scales, x = gpu_case(m, k, seed=7000 + m + k)
+        rows = {}
+        for name, nbytes in CACHE_SETS.items():
+            pk, sc = weight_copies(packed, scales, min_bytes=nbytes)
+            n = len(pk)
+            rows[name] = _time(lambda i: _cuda.w4a16_gemv(pk[i % n], sc[i % n], x), steps, flush,
+                               runs=2)
+            del pk, sc
+        print(f"cache m{m}_k{k}: " + "  ".join(f"{kk} {v:.3f}" for kk, v in rows.items()),
+              flush=True)
+        out[f"m{m}_k{k}"] = rows
+        del packed, scales, x
+        torch.cuda.empty_cache()
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("what", choices=["floor", "c0", "v4", "split", "reuse", "rsplit", "mlp", "all"])
+    ap.add_argument("what", choices=["floor", "c0", "v4", "split", "reuse", "rsplit", "mlp", "cache",
+                                     "all"])
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--out", type=Path, default=None)
     args = ap.parse_args()
@@ -437,6 +473,8 @@ def main() -> None:
         res["rsplit"] = sweep_rsplit(flush, args.steps)
     if args.what in ("mlp", "all"):
         res["mlp"] = sweep_mlp(flush, args.steps)
+    if args.what in ("cache", "all"):
+        res["cache"] = sweep_cache(flush, args.steps)
     if args.out:
         args.out.parent.mkdir(parents=True, exist_ok=True)
         args.out.write_text(json.dumps(res, indent=2) + "\n")
