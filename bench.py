@@ -57,14 +57,20 @@ METRIC = "HBM read GB/s & % of measured read roof, W4A16 GEMV 4096x4096 B=1; p50
 # name -> (M, K, batches, variants timed). The headline is c0 B=1 with the
 # default op (v5). Seeds follow the config index.
 CONFIGS = {
-    "c0": (4096, 4096, [1], ["v0", "v1", "v1_wpr2", "v1_wpr4", "v2", "v3", "v4", "v5", "reuse",
+    "c0": (4096, 4096, [1], ["v5", "v0", "v1", "v1_wpr2", "v1_wpr4", "v2", "v3", "v4", "reuse",
                              "v5_paired"]),
     "c1": (11008, 4096, [1], ["v5", "v4", "reuse", "v5_paired"]),
     "c2": (4096, 11008, [1], ["v5", "v4", "reuse", "v5_paired"]),
-    "c3": (4096, 4096, [1, 2, 4, 8, 16], ["reuse", "v5", "v4"]),
+    "c3": (4096, 4096, [1, 2, 4, 8, 16, 32, 48, 64, 128, 256], ["reuse", "v5", "v4"]),
     "c4a": (28672, 8192, [1], ["v5", "v4", "reuse", "v5_paired"]),
     "c4b": (8192, 28672, [1], ["v5", "v4", "reuse", "v5_paired"]),
 }
+# c3 beyond the BASELINE batches: the reference's own sweep continues to
+# B = 256 (bench/bench.py:36, 261-264); there only the reuse path (the
+# batch op, w4a16_linear's choice) and the fp16 baseline are timed.
+C3_BASELINE_BATCHES = (1, 2, 4, 8, 16)
+# The margin over the B = 1 time that names c3's crossover batch.
+C3_CROSSOVER_MARGIN = 0.25
 VARIANTS = {
     "v0": dict(version=0), "v1": dict(version=1), "v1_wpr2": dict(version=1, warps_per_row=2),
     "v1_wpr4": dict(version=1, warps_per_row=4), "v2": dict(version=2), "v3": dict(version=3),
@@ -353,7 +359,7 @@ def bench_mlp(roof_gbps, steps, flush=None):
     them. Keys: the shape name at B = 1, name_bB for a batch."""
     import torch
 
-    from decode_kernel import gemv, mlp_decode, quantize_and_pack
+    from decode_kernel import gate_up_silu, gemv, mlp_decode, quantize_and_pack
     from dk_bench.common import mlp_bytes, time_graph_steps
 
     out = {}
@@ -386,17 +392,72 @@ def bench_mlp(roof_gbps, steps, flush=None):
 
             st_u, graph = time_graph_steps(unfused, steps=steps, preroll=flush)
             del graph
+            # Each launch of the fused step alone: gate/up (with SiLU*mul) on
+            # its own, and the down projection on the h it produces (the GEMV
+            # w4a16_linear picks, as mlp_decode runs it).
+            hs = [gate_up_silu(x, *copies[kk][:4]) for kk in range(2)]
+            st_gu, graph = time_graph_steps(lambda kk: gate_up_silu(x, *copies[kk % n][:4]),
+                                            steps=steps, preroll=flush)
+            del graph
+            st_dn, graph = time_graph_steps(
+                lambda kk: gemv(copies[kk % n][4], copies[kk % n][5], hs[kk % 2],
+                                reuse_weights=batch > 1), steps=steps, preroll=flush)
+            del graph, hs
             moved = mlp_bytes(i, h, batch)
+            w_gu = 2 * (i * h // 2 + i * h // 128 * 2)
+            w_dn = i * h // 2 + i * h // 128 * 2
             out[name if batch == 1 else f"{name}_b{batch}"] = {
                 "I": i, "H": h, "batch": batch, "bytes_moved": moved, "weight_copies": n,
                 "fused_p50_us": st["median_us"], "fused_gbps": moved / (st["median_us"] * 1e3),
                 "fused_pct_of_read_roof": 100.0 * moved / (st["median_us"] * 1e3) / roof_gbps,
                 "unfused_p50_us": st_u["median_us"], "speedup": st_u["median_us"] / st["median_us"],
                 "launches": {"fused": 2, "unfused": 6},
+                "gate_up_p50_us": st_gu["median_us"],
+                "gate_up_pct_of_read_roof": 100.0 * (w_gu + 2 * batch * (h + i)) /
+                (st_gu["median_us"] * 1e3) / roof_gbps,
+                "down_p50_us": st_dn["median_us"],
+                "down_pct_of_read_roof": 100.0 * (w_dn + 2 * batch * (h + i)) /
+                (st_dn["median_us"] * 1e3) / roof_gbps,
+                "gate_up_share": st_gu["median_us"] / (st_gu["median_us"] + st_dn["median_us"]),
             }
         del copies
         torch.cuda.empty_cache()
     return out
+
+
+def c3_crossover(results: dict, margin: float):
+    """c3's crossover (where the decode's cost stops
+    hiding under the HBM time): per batch the reuse path's per-step time
+    against its B = 1 time and against torch fp16 F.linear; the smallest
+    batch whose time exceeds the B = 1 time by more than `margin`, and the
+    smallest batch at which the fp16 baseline is at least as fast."""
+    rows = []
+    for r in results.values():
+        if r["M"] != 4096 or r["K"] != 4096 or not r.get("c3"):
+            continue
+        reuse = next((k for k in r["kernels"] if k["impl"] == "reuse"), None)
+        if reuse is None:
+            continue
+        f16 = r.get("torch_fp16")
+        rows.append((r["batch"], reuse["median_us"], f16["p50_us"] if f16 else None))
+    rows.sort()
+    if not rows or rows[0][0] != 1:
+        return None
+    t1 = rows[0][1]
+    return {
+        "margin": margin,
+        "b1_us": t1,
+        "first_batch_over_margin": next((b for b, t, _ in rows if t > (1.0 + margin) * t1), None),
+        "fp16_overtakes_at": next((b for b, t, f in rows if f is not None and f <= t), None),
+        "per_batch": [{"batch": b, "reuse_us": round(t, 3), "over_b1": round(t / t1, 3),
+                       "torch_fp16_us": None if f is None else round(f, 3),
+                       "fp16_over_w4a16": None if f is None else round(f / t, 3)}
+                      for b, t, f in rows],
+        "note": ("reuse path (the batch op w4a16_linear picks) per step at M = K = 4096; "
+                 "first_batch_over_margin: smallest B whose time exceeds (1 + margin) x the "
+                 "B = 1 time; fp16_overtakes_at: smallest B where torch fp16 F.linear on the "
+                 "dequantized weights (4x the weight bytes) is at least as fast"),
+    }
 
 
 def kernel_of(m, k, b, **cfg):
@@ -440,7 +501,7 @@ def main():
                                    measure_read, measure_read_floor, measure_read_same_size)
     from decode_kernel.quantize import dequantize
     from dk_bench.common import (MI355X_HBM_PEAK_GBPS, Flush, bytes_moved_w4, meta_dict,
-                                 weight_copies)
+                                 time_direct_steps, weight_copies)
 
     wanted = list(CONFIGS) if args.configs == "all" else ["c0"] + [
         c for c in args.configs.split(",") if c and c != "c0"]
@@ -454,9 +515,12 @@ def main():
     flush = Flush(args.flush_bytes, args.flush)
     preroll = flush if args.flush != "none" else None
     floor = measure_event_floor(preroll=preroll)
+    lead = flush if flush.kind == "read" else Flush(args.flush_bytes, "read")
+    floor_direct = time_direct_steps(lambda i: _cuda.empty_kernel(), 200, lead)
     log(f"[bench] read roof {roof['gbps']:.1f} GB/s (blocks {roof['block_sweep_gbps']}); copy "
         f"{copy_roof['gbps']:.1f} GB/s; empty kernel {floor['back_to_back']['median_us']:.2f} "
-        f"us/launch back-to-back, {floor['call']['median_us']:.2f} us with events around one call")
+        f"us/launch back-to-back in a graph, {floor_direct['median_us']:.2f} direct, "
+        f"{floor['call']['median_us']:.2f} us with events around one call")
     read_floor = measure_read_floor(bytes_moved_w4(4096, 4096, 1), preroll=preroll)
     rf = read_floor["best"]
     log(f"[bench] read floor at the headline's bytes: {rf['median_us']:.3f} us/launch "
@@ -465,6 +529,7 @@ def main():
     results = {}
     headline = None
     headline_long = None
+    headline_direct = None
     cpu = None
     for ci, name in enumerate(CONFIGS):
         if name not in wanted:
@@ -485,7 +550,7 @@ def main():
                     raise RuntimeError(f"headline kernel fails the 1e-2 gate: {err}")
             copies = weight_copies(pd, sd)
             del pd, sd
-            entry = {"M": m, "K": k, "batch": b, "kernels": []}
+            entry = {"M": m, "K": k, "batch": b, "kernels": [], "c3": name == "c3"}
             if b == 1:
                 same = measure_read_same_size(copies[0], preroll=preroll)
                 entry["same_size_read"] = same
@@ -494,21 +559,21 @@ def main():
             for v in variants:
                 if v == "v0" and name != "c0":
                     continue
+                if name == "c3" and b not in C3_BASELINE_BATCHES and v != "reuse":
+                    continue
                 headline_row = name == "c0" and v == "v5"
                 steps = args.steps if headline_row else other_steps
-                # The first variant timed on a new set of weight copies is
-                # timed twice and the lower median kept: the first timings
-                # after new copies run up to 8% slow on MI355X, whichever
-                # kernel comes first.
-                for run in range(2 if first else 1):
-                    r_run = bench_variant(_cuda, copies, xd, v, steps, preroll,
-                                          warmup=args.warmup if headline_row else 1,
-                                          y_ref=y_ref if v == "v5" else None,
-                                          call_level_flush=flush if headline_row else None)
-                    if first:
-                        r_run["runs"] = 2
-                    r = r_run if run == 0 or r_run["median_us"] < r["median_us"] else r
-                first = False
+                if first:
+                    # The first timings after a new set of weight copies run
+                    # up to 8% slow on MI355X, whichever kernel comes first:
+                    # one untimed run of the first variant precedes the
+                    # timed runs, and every variant is then timed once.
+                    bench_variant(_cuda, copies, xd, v, steps, preroll, warmup=1)
+                    first = False
+                r = bench_variant(_cuda, copies, xd, v, steps, preroll,
+                                  warmup=args.warmup if headline_row else 1,
+                                  y_ref=y_ref if v == "v5" else None,
+                                  call_level_flush=flush if headline_row else None)
                 r["kernel"] = (None if v == "v5_paired" else
                                kernel_of(m, k, b, **VARIANTS[v])["kernel"])
                 r["pct_of_read_roof"] = 100.0 * r["gbps"] / roof["gbps"]
@@ -517,18 +582,31 @@ def main():
                 entry["kernels"].append(r)
                 log(f"   {v:8s} {r['median_us']:8.2f} us/step  {r['gbps']:8.1f} GB/s  "
                     f"{r['pct_of_read_roof']:5.1f}% of read roof")
+                if headline_row:
+                    # The same kernel launched directly (no graph), back to
+                    # back behind queued work, on the same GPU-clock bracket.
+                    pk_, sc_ = copies
+                    nc = len(pk_)
+                    headline_direct = time_direct_steps(
+                        lambda i: _cuda.w4a16_gemv(pk_[i % nc], sc_[i % nc], xd), 200, lead)
+                    log(f"   v5 direct launches {headline_direct['median_us']:8.2f} us/step")
                 if headline_row and args.steps != 1000:
                     # The same kernel over 1000 steps in the same run: the
                     # per-step figure must not depend on the step count.
                     headline_long = bench_variant(_cuda, copies, xd, v, 1000, preroll,
                                                   warmup=args.warmup)
                     log(f"   v5 at 1000 steps {headline_long['median_us']:8.2f} us/step")
-            if b == 1 and not args.no_fp16_baseline:
+            if (b == 1 or name == "c3") and not args.no_fp16_baseline:
+                # Beside every c3 batch, as the reference's sweep has a
+                # cuBLAS column at every B (bench/bench.py:128-139), compared
+                # with the batch op there (the reuse path) and with v5 at B = 1.
                 r16 = bench_torch_fp16(copies[0][0], copies[1][0], xd, other_steps, preroll)
-                v5row = next(r for r in entry["kernels"] if r["impl"] == "v5")
+                cmp_impl = "reuse" if name == "c3" else "v5"
+                v5row = next(r for r in entry["kernels"] if r["impl"] == cmp_impl)
                 pct16 = 100.0 * r16["gbps"] / roof["gbps"]
                 entry["torch_fp16"] = {"precision": "fp16", "p50_us": r16["median_us"],
                                        "gbps": r16["gbps"], "pct_of_read_roof": pct16,
+                                       "compared_with": cmp_impl,
                                        "w4a16_v5_speedup": r16["median_us"] / v5row["median_us"]}
                 if pct16 > 90.0:
                     # bench/common.py:145-171 of the reference: an fp16 row above 90% of the
@@ -538,7 +616,7 @@ def main():
                         f"{pct16:.1f}% of read-only STREAM exceeds 90%; do not report as a hit "
                         f"of the roof")
                 log(f"   torch fp16 F.linear {r16['median_us']:8.2f} us/step (cross-precision; "
-                    f"{pct16:.1f}% of read roof; v5 is "
+                    f"{pct16:.1f}% of read roof; {cmp_impl} is "
                     f"{entry['torch_fp16']['w4a16_v5_speedup']:.2f}x faster)")
             results[f"{name}_B{b}"] = entry
             if name == "c0":
@@ -557,7 +635,8 @@ def main():
         mlp = bench_mlp(roof["gbps"], steps=other_steps, flush=preroll)
         for name, r in mlp.items():
             log(f"   {name:13s} fused {r['fused_p50_us']:8.2f} us  {r['fused_gbps']:8.1f} GB/s  "
-                f"{r['fused_pct_of_read_roof']:5.1f}% of read roof; unfused {r['unfused_p50_us']:8.2f} us")
+                f"{r['fused_pct_of_read_roof']:5.1f}% of read roof; unfused {r['unfused_p50_us']:8.2f} us; "
+                f"gate/up alone {r['gate_up_p50_us']:.2f} us, down alone {r['down_p50_us']:.2f} us")
 
     quant = None
     if not args.no_quantizer:
@@ -609,11 +688,13 @@ def main():
         "same_size_read_gbps": results["c0_B1"]["same_size_read"]["gbps"],
         "pct_of_same_size_read": headline["pct_of_same_size_read"],
         "floor_read_us": rf["median_us"],
-        "floor_read_shape": {kk: rf[kk] for kk in ("blocks", "threads", "loads", "nt")},
+        "floor_read_shape": {kk: rf[kk] for kk in ("kind", "blocks", "threads", "loads", "nt")},
         "pct_of_floor_read": 100.0 * rf["median_us"] / headline["median_us"],
         "p50_us_reference_protocol": headline["call_events"]["median_us"],
         "empty_kernel_us_back_to_back": floor["back_to_back"]["median_us"],
         "empty_kernel_us_call_events": floor["call"]["median_us"],
+        "empty_kernel_us_direct": floor_direct["median_us"],
+        "p50_us_direct": headline_direct["median_us"] if headline_direct else None,
         "reference_protocol_flush": flush.describe(),
         "gemm_fp16_tflops": gemm["tflops"],
         "ridge_flop_per_byte": ridge,
@@ -626,6 +707,7 @@ def main():
             "algorithmic_bytes": headline["bytes_moved"],
         },
         "cpu_baseline": cpu,
+        "crossover": c3_crossover(results, C3_CROSSOVER_MARGIN),
         "quantizer": quant,
         "mlp": mlp,
         "configs": {

@@ -491,7 +491,27 @@ __global__ __launch_bounds__(W * kWave) void gemv_v5_lds(const uint4* __restrict
 // miscounted.
 // ---------------------------------------------------------------------------
 // Takes the ticket of a split reduction for generation `gen` (low 6 bits
-// zero); true for the last of `S` arrivals. One thread per workgroup.
+// zero); true for the last of `S` arrivals. One thread per workgroup, after
+// a workgroup barrier that follows every wave's partial stores.
+//
+// Ordering. Every access here and to the partials is a relaxed atomic at
+// agent scope, so the HIP memory model alone does not order the partial
+// stores before the ticket. The order rests on how gfx950 executes them
+// (checked in this library's assembly):
+//  1. each partial is stored by `global_store_dword ... sc1` (agent scope:
+//     written through the issuing XCD's L2), and every wave executes
+//     `s_waitcnt vmcnt(0)` (reuse_split_finish) before the workgroup's
+//     `s_barrier`, so the stores are acknowledged before the ticket is taken;
+//  2. the ticket is a `global_atomic_cmpswap_x2` at agent scope, performed at
+//     the device-coherent level, which serializes the S arrivals;
+//  3. the last arrival's partial loads are `global_load_dword ... sc1` (agent
+//     scope: they miss the XCD's L2 and read the coherent copy), issued only
+//     after the compare-and-swap has returned and a barrier has passed.
+// The formal alternative, an acquire-release compare-and-swap, makes the
+// compiler write back the XCD's L2 before it and invalidate the L2 after it
+// in every workgroup; measured on MI355X it cost 10-46% at the split shapes
+// (M = 1024, K = 28672, B = 16: 21.7 against 14.8 us) with identical bits,
+// so the relaxed form stays.
 __device__ __forceinline__ bool take_ticket(unsigned long long* ticket, unsigned long long gen, int S) {
   unsigned long long t = __hip_atomic_load(ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   unsigned long long arrived;

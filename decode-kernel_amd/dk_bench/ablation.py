@@ -90,7 +90,8 @@ def run(configs, steps: int) -> dict:
         row["same_size_read_us"] = measure_read_same_size(pk, preroll=flush)["median_us"]
         floor = measure_read_floor(row["bytes_moved"], preroll=flush)
         row["read_floor_us"] = floor["best"]["median_us"]
-        row["read_floor_shape"] = {kk: floor["best"][kk] for kk in ("blocks", "threads", "loads", "nt")}
+        row["read_floor_shape"] = {kk: floor["best"][kk]
+                                   for kk in ("kind", "blocks", "threads", "loads", "nt")}
         out[name] = row
         print(f"{name:4s} product {row['product_us']:7.2f}  no decode {row['no_decode_us']:7.2f}  "
               f"loads only {row['loads_only_us']:7.2f}  same-size read {row['same_size_read_us']:7.2f}  "

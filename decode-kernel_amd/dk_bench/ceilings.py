@@ -102,15 +102,21 @@ def measure_read_same_size(packed_copies: list, preroll=None) -> dict:
 
 def measure_read_floor(nbytes: int, preroll=None, grids=(256, 512, 1024, 2048, 4096),
                        threads=(256, 512, 1024), loads=(1, 2, 4, 8), max_passes: int = 2,
-                       steps: int = 200) -> dict:
+                       steps: int = 200, stride_blocks=(512, 1024, 2048, 4096, 8192)) -> dict:
     """The read floor at `nbytes`: the fastest per-launch time of a kernel that
     only reads that many bytes, over launch shapes of the read probe
     (dk_bench/libdk_bench.so): `grids` workgroups of `threads` lanes, `loads`
     16-byte loads per lane all issued before the first wait, with and without
     the non-temporal hint; shapes needing more than `max_passes` passes over
-    the buffer are skipped. Each shape is timed back-to-back over buffer
-    copies totalling > 640 MB (cold), `steps` launches per graph, p50 of 5
-    replays after a 1 GiB pre-roll. Returns the best shape and the sweep."""
+    the buffer are skipped. The grid-stride STREAM read (one load per lane
+    per step, `stride_blocks` workgroups of 256 lanes: the kernel of the read
+    roof and the same-size read) is swept beside them (`threads` 256,
+    `loads` 0 in the rows), so the floor is never above the same-size read.
+    Each shape is timed back-to-back over buffer copies totalling > 640 MB
+    (cold), `steps` launches per graph, p50 of 5 replays after a 1 GiB
+    pre-roll. Returns the best shape and the sweep."""
+    from decode_kernel import _cuda
+
     from . import benchlib
     from .common import COLD_WORKING_SET
 
@@ -119,6 +125,15 @@ def measure_read_floor(nbytes: int, preroll=None, grids=(256, 512, 1024, 2048, 4
     bufs = [torch.ones(nbytes // 4, dtype=torch.float32, device="cuda") for _ in range(n)]
     pieces = nbytes // 16
     sweep, best = [], None
+    for g in stride_blocks:
+        partials = torch.empty(g, dtype=torch.float32, device="cuda")
+        st, _ = time_graph_steps(lambda i: _cuda.stream_read(bufs[i % n], partials), steps=steps,
+                                 preroll=preroll)
+        row = {"blocks": g, "threads": 256, "loads": 0, "nt": False, "kind": "grid_stride",
+               "median_us": st["median_us"], "gbps": nbytes / (st["median_us"] * 1e3)}
+        sweep.append(row)
+        if best is None or row["median_us"] < best["median_us"]:
+            best = row
     for t in threads:
         partials = torch.empty(max(grids) * t // 64, dtype=torch.float32, device="cuda")
         for g in grids:
@@ -129,7 +144,7 @@ def measure_read_floor(nbytes: int, preroll=None, grids=(256, 512, 1024, 2048, 4
                     st, _ = time_graph_steps(
                         lambda i: benchlib.read_probe(bufs[i % n], partials, g, t, ld, nt),
                         steps=steps, preroll=preroll)
-                    row = {"blocks": g, "threads": t, "loads": ld, "nt": nt,
+                    row = {"blocks": g, "threads": t, "loads": ld, "nt": nt, "kind": "probe",
                            "median_us": st["median_us"], "gbps": nbytes / (st["median_us"] * 1e3)}
                     sweep.append(row)
                     if best is None or row["median_us"] < best["median_us"]:

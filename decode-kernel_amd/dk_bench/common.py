@@ -259,6 +259,49 @@ def time_graph_steps(step: Callable[[int], object], steps: int, trials: int = 5,
     return out, graph
 
 
+def time_direct_steps(step: Callable[[int], object], steps: int, flush: Flush,
+                      trials: int = 5, lead_reads: int = 24) -> dict:
+    """Per-step time of exactly `steps` direct launches (`step(i)`, no graph)
+    back-to-back on the current stream, bracketed by the same GPU-clock
+    timestamp kernels as time_graph_steps. The launches are queued behind
+    `lead_reads` 1 GiB reads (~4 ms of GPU work), so the host has enqueued
+    all of them before the GPU reaches the first: the span measures the
+    GPU's cadence, not the host's launch rate (which is checked: the host's
+    enqueue time must fit inside the lead reads). The bracket's own cost is
+    measured the same way and subtracted. p50 over `trials`."""
+    import time
+
+    from . import benchlib
+
+    khz = benchlib.wall_clock_khz()
+    ts = torch.zeros(2, dtype=torch.int64, device="cuda")
+    step(0)
+    torch.cuda.synchronize()
+    per, host = [], []
+    for _ in range(trials):
+        for _ in range(lead_reads):
+            flush()
+        benchlib.timestamp(ts, 0)
+        benchlib.timestamp(ts, 1)
+        torch.cuda.synchronize()
+        bracket = int(ts[1]) - int(ts[0])
+        for _ in range(lead_reads):
+            flush()
+        t0 = time.perf_counter()
+        benchlib.timestamp(ts, 0)
+        for i in range(steps):
+            step(i)
+        benchlib.timestamp(ts, 1)
+        host.append((time.perf_counter() - t0) * 1e6)
+        torch.cuda.synchronize()
+        per.append((int(ts[1]) - int(ts[0]) - bracket) * 1e3 / khz / steps)
+    out = _stats(per)
+    out.update({"steps": steps, "trials": trials, "timer": "gpu_clock_bracket_direct_launches",
+                "host_enqueue_us_per_step": statistics.median(host) / steps,
+                "host_kept_ahead": max(host) < lead_reads * 150.0})
+    return out
+
+
 def time_repeated(fn: Callable[[], object], reps: int, trials: int = 5) -> dict:
     """Per-launch time of `reps` back-to-back launches between two events (the
     STREAM method: the event overhead is shared by `reps` launches)."""

@@ -35,7 +35,10 @@ SHAPES = {"c0": (4096, 4096, 1), "c1": (11008, 4096, 1), "c2": (4096, 11008, 1),
           "m6144k8192b16": (6144, 8192, 16), "m1024k16384b16": (1024, 16384, 16),
           "m1024k28672b16": (1024, 28672, 16)}
 VARIANTS = {"v5": dict(version=5), "v2": dict(version=2), "v4": dict(version=4, split_k=4),
-            "reuse": dict(version=5, reuse_weights=True), "v1": dict(version=1)}
+            "reuse": dict(version=5, reuse_weights=True), "v1": dict(version=1),
+            # w4a16_linear's choice: the reuse path for a batch, v5 at one row
+            # (python/decode_kernel/__init__.py:71-74)
+            "linear": None}
 ABLATIONS = {"no_decode": 1, "loads_only": 2}
 COPY_BYTES = 64 << 20
 
@@ -99,6 +102,9 @@ def main() -> None:
                     help="comma-separated: " + ", ".join(sorted(VARIANTS) + sorted(ABLATIONS)))
     ap.add_argument("--reps", type=int, default=50)
     ap.add_argument("--copies", type=int, default=5)
+    ap.add_argument("--sclk", action="store_true",
+                    help="print the shader clock (clock probe kernel) before and after the "
+                         "workload, so SCLK-cycle counters convert to time in the same run")
     args = ap.parse_args()
     configs = args.config.split(",")
     variants = args.variant.split(",")
@@ -116,6 +122,15 @@ def main() -> None:
     from dk_bench.common import Flush, bytes_moved_w4
     from dk_bench.common import synthetic_case
 
+    def sclk(when):
+        if args.sclk:
+            from dk_bench import benchlib
+
+            print(json.dumps({"sclk_mhz": {"when": when, "one_wave": benchlib.sclk_mhz(),
+                                           "all_cus": benchlib.sclk_mhz(blocks=1024)}}),
+                  flush=True)
+
+    sclk("start")
     flush = Flush()
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
@@ -145,13 +160,17 @@ def main() -> None:
                     flush()
                     benchlib.run_kernel(kern, ABLATIONS[variant], pd, sd, xd, y)
             else:
+                kw = VARIANTS[variant]
+                if kw is None:
+                    kw = dict(version=5, reuse_weights=b > 1)
                 for _ in range(args.reps):
                     flush()
-                    gemv(pd, sd, xd, **VARIANTS[variant])
+                    gemv(pd, sd, xd, **kw)
             torch.cuda.synchronize()
             print(json.dumps({"config": config, "variant": variant, "M": m, "K": k, "B": b,
                               "reps": args.reps, "copy_bytes": COPY_BYTES,
                               "algorithmic_bytes": bytes_moved_w4(m, k, b)}), flush=True)
+    sclk("end")
 
 
 if __name__ == "__main__":

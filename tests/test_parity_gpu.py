@@ -38,6 +38,9 @@ CONFIGS = {
     "c2_4096x11008": (4096, 11008),
     "c4a_28672x8192": (28672, 8192),
     "c4b_8192x28672": (8192, 28672),
+    # The reference's DK_FULL_SHAPES shape (tests/test_correctness.py:24-26),
+    # run here by default.
+    "full_4096x14336": (4096, 14336),
 }
 
 # Every product path: (label, gemv kwargs)
@@ -120,7 +123,9 @@ def test_configs_full_size(name):
         _check_against_oracle(y, y_ref, f"{name}/{label}")
 
 
-@pytest.mark.parametrize("batch", [1, 2, 4, 8, 16])
+# c3's batches and the reference's sweep beyond them (bench/bench.py:36);
+# 64 and 257 run on every path in test_large_batches_all_paths below.
+@pytest.mark.parametrize("batch", [1, 2, 4, 8, 16, 32, 48, 128])
 def test_batch_sweep_c3(batch):
     m, k = 4096, 4096
     w, x = oracle.make_case(m, k, batch, seed=3000 + batch)
