@@ -620,6 +620,80 @@ int launch_reuse_pf(const Launch& L, const uint4* p, const uint16_t* s, const ui
            B);
 }
 
+// The many-batch tiles (gemv_reuse_pfb): RT row tiles and NBT batch tiles
+// per workgroup of KS waves; KS = 0: not these tiles.
+struct PfbShape {
+  int ks = 0, rt = 0, nbt = 0;
+};
+
+template <int KS, int RT, int NBT>
+int launch_reuse_pfb(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x,
+                     uint16_t* y, int M, int K, int B) {
+  const dim3 grid((M + 16 * RT - 1) / (16 * RT), (B + 16 * NBT - 1) / (16 * NBT));
+  return L("reuse launch", dk::gemv_reuse_pfb<KS, RT, NBT>, grid, dim3(KS * 64), 0, p, s, x, y,
+           M, K, B);
+}
+
+// Above 16 batch rows (where the groups pair), the many-batch tiles. Of the
+// shapes RT x NBT = 1 x 2, 2 x 2, 4 x 2, 4 x 4 (NBT = 4 only from three batch
+// tiles), in order of reuse, the first whose grid is one round of 144-256
+// workgroups (one per CU: four waves, 82-139 KiB of LDS); below 144 the one
+// before it; where none reaches one round, 4 x 4 (or 4 x 2 up to 32 batch
+// rows) with two waves when its grid is at most 512, so that two
+// workgroups per CU make one round. Up to 32 batch rows only with RT >= 2:
+// there the two batch columns of the single-tile kernels beat RT = 1.
+// From sweeps of 14 shapes (KS, RT, NBT) at 12 (M, K) and B = 24-256, us,
+// the chosen shape against the earlier dispatch (gemv_reuse_lds or
+// gemv_reuse_pf, one workgroup per batch tile of 16):
+//                        B = 48           B = 128          B = 256
+//   M = K = 4096:        8.36 (11.36)     13.03 (21.06)    20.47 (39.94)
+//   M = 4096, K = 11008: 17.89 (24.46)    29.38 (46.57)    46.98 (93.26)
+//   M = 11008, K = 4096: 20.82 (21.57)    38.11 (45.44)    61.24 (87.96)
+//   M = 2048, K = 8192:  10.75 (13.27)    13.85 (24.54)    22.11 (48.48)
+//   M = 8192, K = 8192:  23.61 (28.43)    37.58 (68.98)    66.34 (140.76)
+//   M = 3584, K = 8192:  14.12 (18.33)    22.32 (34.93)    36.16 (62.53)
+//   M = 1024, K = 4096:  (4.97: earlier)  6.33 (8.67)      8.01 (15.66)
+//   M = 28672, K = 8192: 69.32 (97.50)    129.53 (248.57)  250.81 (489.97)
+// At 24-32 batch rows: M = 8192, K = 8192 16.07 (20.65); M = 6144, K =
+// 8192 15.34 (18.66); M = 11008, K = 4096 13.96 (14.81); M = 28672, K =
+// 8192 46.94 (66.60); M = K = 4096 keeps the earlier tiles (6.42 against
+// 7.02 for RT = 1). Slower than the earlier dispatch at one shape of those
+// swept: M = K = 5120, B = 48 (16.46 against 12.92; B = 64: 16.56 against
+// 17.66).
+PfbShape reuse_pfb_shape(int M, int B) {
+  if (B <= 16) return {};
+  const long long bt = (B + 15) / 16;  // batch tiles of 16 rows
+  struct Cand {
+    int rt, nbt;
+  };
+  constexpr Cand kCands[] = {{1, 2}, {2, 2}, {4, 2}, {4, 4}};
+  Cand pick{0, 0}, prev{0, 0};
+  long long w_pick = 0, w_prev = 0;
+  for (const Cand& c : kCands) {
+    if (c.nbt == 4 && bt < 3) continue;
+    const long long w = (long long)((M + 16 * c.rt - 1) / (16 * c.rt)) * ((bt + c.nbt - 1) / c.nbt);
+    if (w <= 256) {
+      if (w >= 144) {
+        pick = c;
+        w_pick = w;
+      } else if (prev.rt) {
+        pick = prev;
+        w_pick = w_prev;
+      }
+      break;
+    }
+    prev = c;
+    w_prev = w;
+  }
+  if (!pick.rt && w_prev > 256) {  // no shape fits one round: the most reuse
+    pick = prev;
+    w_pick = w_prev;
+  }
+  if (!pick.rt || (pick.rt == 1 && B <= 32)) return {};
+  const bool two_per_cu = pick.rt == 4 && pick.nbt == 4 && w_pick > 256 && w_pick <= 512;
+  return {two_per_cu ? 2 : 4, pick.rt, pick.nbt};
+}
+
 // A shape of the double-buffered tiles (gemv_reuse_pf): KS waves, RT tiles
 // per wave, XL x loads per block; KS = 0: not these tiles.
 struct PfShape {
@@ -707,6 +781,13 @@ PfShape reuse_pf_shape(int M, int K, int B) {
 int launch_reuse_tiles(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x,
                        uint16_t* y, int M, int K, int B) {
   if ((K / DK_GROUP_SIZE) % 2 == 0 && aligned(s, 4)) {
+    const PfbShape pfb = reuse_pfb_shape(M, B);
+    if (pfb.rt == 4 && pfb.nbt == 4)
+      return pfb.ks == 2 ? launch_reuse_pfb<2, 4, 4>(L, p, s, x, y, M, K, B)
+                         : launch_reuse_pfb<4, 4, 4>(L, p, s, x, y, M, K, B);
+    if (pfb.rt == 4) return launch_reuse_pfb<4, 4, 2>(L, p, s, x, y, M, K, B);
+    if (pfb.rt == 2) return launch_reuse_pfb<4, 2, 2>(L, p, s, x, y, M, K, B);
+    if (pfb.rt == 1) return launch_reuse_pfb<4, 1, 2>(L, p, s, x, y, M, K, B);
     const PfShape pf = reuse_pf_shape(M, K, B);
     if (pf.ks == 8) return launch_reuse_pf<8, 1, 4>(L, p, s, x, y, M, K, B);
     if (pf.ks == 6)

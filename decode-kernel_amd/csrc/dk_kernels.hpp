@@ -1122,6 +1122,15 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
+// Orders memory accesses for the compiler only (no instruction): the LDS
+// reads after an explicit s_waitcnt must not be hoisted above it, and reads
+// before an LDS-DMA issue must not sink below it. s_waitcnt and
+// sched_barrier do not order memory operations before instruction
+// selection; without this the compiler moved a block's weight and scale
+// reads of gemv_reuse_pfb to the loop head, above the wait for their
+// LDS-DMA.
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
 // A window of each row: groups [gbeg, gbeg + G) of a K-long row, tile t's
 // weights and scales through descriptors rw[t], rs[t] (starting at group
 // gbeg of the tile's first row; rows K / 2 bytes and Gs scales apart), x of
@@ -1196,6 +1205,7 @@ __device__ __forceinline__ void reuse_pf_step(f4_t (&acc)[RT], const uint4* __re
   if constexpr (kNext) {
     // The previous step's reads of the buffers about to be refilled have
     // returned (its MFMAs consumed them; this orders the loads after them).
+    compiler_fence();
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_sched_barrier(0);
     reuse_pf_issue<RT, kXL>(nx, nw, ns, rw, rs, rx, win, lane, gn);
@@ -1204,6 +1214,7 @@ __device__ __forceinline__ void reuse_pf_step(f4_t (&acc)[RT], const uint4* __re
     wait_vmcnt<0>();
   }
   __builtin_amdgcn_sched_barrier(0);
+  compiler_fence();
   uint32_t sc[RT][4];
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
@@ -1359,6 +1370,263 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_pf(const uint4* __restrict
     for (int v = 0; v < 4; ++v) {
       const int orow = row0 + 16 * wave + 4 * (lane >> 4) + v;
       if (orow < M) y[(size_t)b * M + orow] = f2h(sum[v]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// The double-buffered tiles for many batch rows: a workgroup's RT 16-row
+// tiles serve NBT batch tiles of 16 rows (grid.y over groups of 16 NBT batch
+// rows), so each weight is loaded and decoded once per 16 NBT batch rows
+// instead of once per 16, and each x load serves the RT tiles. Each wave
+// decodes a block's weights once into registers (the MFMA A operands of the
+// block's two halves for each tile: 8 x h8 per tile) and runs the NBT batch
+// tiles' MFMAs on them, streaming x one batch tile (16 rows x 2 groups,
+// 8 KiB) per step through two LDS buffers; the weights and scales of the
+// next block arrive, into the other pair of buffers, during the last batch
+// tile of this one. Every step issues the next step's loads before it waits
+// for its own (exact vmcnt: 8 x loads, 8 + 3 RT with the next block's
+// weights and scales). One grid column of NBT batch tiles replaces NBT
+// columns of the single-batch-tile kernels, which repeat every weight load
+// and decode per column and, with one workgroup per CU fitting in LDS, run
+// the columns in rounds. NBT even; groups per row even and scales 4-byte
+// aligned, as for gemv_reuse_pf.
+// ---------------------------------------------------------------------------
+// x of batch rows bt .. bt + 15 (those below B) for the block at group g0,
+// into xb (the layout of reuse_pf_issue with kXL = 8).
+__device__ __forceinline__ void reuse_pfb_issue_x(uint4* __restrict__ xb, __amdgpu_buffer_rsrc_t rx,
+                                                  int bt, int B, int K, int g0, int lane) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int bb = 2 * i + lane / 32;
+    const int p = lane % 32;
+    const int c = (p & 16) | ((p ^ stage_swizzle<32>(bb)) & 15);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rx, (lds_void_ptr)(xb + i * 64), 16,
+        bt + bb < B ? (bt + bb) * K * 2 + g0 * 256 + c * 16 : kOutOfRange, 0, 0, 0);
+  }
+}
+
+// Weights and scale pairs of the block at group g0 of the RT tiles (rw[t],
+// rs[t]) into wb, sb (the layout of reuse_pf_issue).
+template <int RT>
+__device__ __forceinline__ void reuse_pfb_issue_ws(uint4* __restrict__ wb, uint4* __restrict__ sb,
+                                                   const __amdgpu_buffer_rsrc_t (&rw)[RT],
+                                                   const __amdgpu_buffer_rsrc_t (&rs)[RT], int K,
+                                                   int G, int g0, int lane) {
+#pragma unroll
+  for (int i = 0; i < 2 * RT; ++i) {
+    const int r = 8 * (i % 2) + lane / 8;
+    const int c = (lane % 8) ^ stage_swizzle<8>(r);
+    const __amdgpu_buffer_rsrc_t rwt = rw[i / 2];
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rwt, (lds_void_ptr)(wb + i * 64), 16,
+                                             r * (K / 2) + (g0 * 4 + c) * 16, 0, 0,
+                                             kLoadNonTemporal);
+  }
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const __amdgpu_buffer_rsrc_t rst = rs[t];
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rst, (lds_void_ptr)(sb + 16 * t), 4,
+                                             lane < 16 ? (lane * G + g0) * 2 : kOutOfRange, 0, 0,
+                                             0);
+  }
+}
+
+// The block's MFMA A operands (weights of tile t's row lane % 16, both halves
+// of the block) and this lane's four rows' scale pairs per tile, from LDS.
+template <int RT>
+__device__ __forceinline__ void reuse_pfb_decode(h8_t (&a)[RT][2][4], uint32_t (&sc)[RT][4],
+                                                 const uint4* __restrict__ cw,
+                                                 const uint4* __restrict__ cs, int lane) {
+  const int kq = lane >> 4;
+  const int r_lane = lane & 15;
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const uint4 s4 = cs[16 * t + kq];
+    sc[t][0] = s4.x;
+    sc[t][1] = s4.y;
+    sc[t][2] = s4.z;
+    sc[t][3] = s4.w;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint4 wv = cw[(16 * t + r_lane) * 8 + ((4 * u + kq) ^ stage_swizzle<8>(r_lane))];
+      a[t][u][0] = unpack_word_h8(wv.x);
+      a[t][u][1] = unpack_word_h8(wv.y);
+      a[t][u][2] = unpack_word_h8(wv.z);
+      a[t][u][3] = unpack_word_h8(wv.w);
+    }
+  }
+}
+
+// One batch tile of one block: acc[t] += tile t's products with x in cx.
+template <int RT>
+__device__ __forceinline__ void reuse_pfb_mma(f4_t (&acc)[RT], const h8_t (&a)[RT][2][4],
+                                              const uint32_t (&sc)[RT][4],
+                                              const uint4* __restrict__ cx, int lane) {
+  const int kq = lane >> 4;
+  const int r_lane = lane & 15;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    h8_t xp[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int xc = 16 * u + 4 * kq + j;
+      xp[j] = pair_x8(cx[r_lane * 32 + ((xc & 16) | ((xc ^ stage_swizzle<32>(r_lane)) & 15))]);
+    }
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      f4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[t][u][j], xp[j], c, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        acc[t][v] = __builtin_fmaf(c[v], h2f((uint16_t)(sc[t][v] >> (16 * u))), acc[t][v]);
+    }
+  }
+}
+
+// One block of NBT steps: weights and scales in cw, cs; batch tile 0's x in
+// xa, then alternately xb, xa, ... With kNext the last step issues the next
+// block (group gn) into nw, ns and its tile 0 into xa.
+template <int RT, int NBT, bool kNext>
+__device__ __forceinline__ void reuse_pfb_block(f4_t (&acc)[NBT][RT], const uint4* __restrict__ cw,
+                                                const uint4* __restrict__ cs,
+                                                uint4* __restrict__ nw, uint4* __restrict__ ns,
+                                                uint4* __restrict__ xa, uint4* __restrict__ xb,
+                                                const __amdgpu_buffer_rsrc_t (&rw)[RT],
+                                                const __amdgpu_buffer_rsrc_t (&rs)[RT],
+                                                __amdgpu_buffer_rsrc_t rx, int bt0, int B, int K,
+                                                int G, int g, int gn, int lane) {
+  static_assert(NBT % 2 == 0, "steps alternate between two x buffers within a block");
+  h8_t a[RT][2][4];
+  uint32_t sc[RT][4];
+#pragma unroll
+  for (int t = 0; t < NBT; t += 2) {
+    // Step t: x in xa; issue batch tile t + 1 into xb.
+    compiler_fence();
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): earlier reads of xb have returned
+    __builtin_amdgcn_sched_barrier(0);
+    reuse_pfb_issue_x(xb, rx, bt0 + 16 * (t + 1), B, K, g, lane);
+    wait_vmcnt<8>();
+    __builtin_amdgcn_sched_barrier(0);
+    compiler_fence();
+    if (t == 0) reuse_pfb_decode<RT>(a, sc, cw, cs, lane);
+    reuse_pfb_mma<RT>(acc[t], a, sc, xa, lane);
+    // Step t + 1: x in xb; issue tile t + 2 into xa, or the next block.
+    compiler_fence();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_sched_barrier(0);
+    if (t + 2 < NBT) {
+      reuse_pfb_issue_x(xa, rx, bt0 + 16 * (t + 2), B, K, g, lane);
+      wait_vmcnt<8>();
+    } else if constexpr (kNext) {
+      reuse_pfb_issue_ws<RT>(nw, ns, rw, rs, K, G, gn, lane);
+      reuse_pfb_issue_x(xa, rx, bt0, B, K, gn, lane);
+      wait_vmcnt<8 + 3 * RT>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    compiler_fence();
+    reuse_pfb_mma<RT>(acc[t + 1], a, sc, xb, lane);
+  }
+}
+
+template <int KS, int RT, int NBT>
+__global__ __launch_bounds__(KS * 64) void gemv_reuse_pfb(const uint4* __restrict__ packed,
+                                                          const uint16_t* __restrict__ scales,
+                                                          const uint4* __restrict__ x4,
+                                                          uint16_t* __restrict__ y, int M, int K,
+                                                          int B) {
+  static_assert(NBT * RT <= 16, "the partials fit a wave's two x buffers");
+  write_stamp(DK_STAMP_REUSE);
+  __shared__ ReusePfLds<KS, RT, 16> lds;
+  const int G = K >> 7;
+  const int nck = K >> 5;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = blockIdx.x * 16 * RT;
+  const int bt0 = blockIdx.y * 16 * NBT;
+  __amdgpu_buffer_rsrc_t rw[RT], rs[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const int rows = __builtin_amdgcn_readfirstlane(max(0, min(16, M - row0 - 16 * t)));
+    const int rbase = rows > 0 ? row0 + 16 * t : 0;
+    rw[t] = buffer_rsrc(packed + (size_t)rbase * nck, (uint32_t)(rows * (K / 2)));
+    rs[t] = buffer_rsrc(scales + (size_t)rbase * G, (uint32_t)(rows * G * 2));
+  }
+  const auto rx = buffer_rsrc(x4, (uint32_t)((size_t)B * K * 2));
+  f4_t acc[NBT][RT];
+#pragma unroll
+  for (int b = 0; b < NBT; ++b)
+#pragma unroll
+    for (int t = 0; t < RT; ++t) acc[b][t] = f4_t{0.f, 0.f, 0.f, 0.f};
+  // This wave's blocks: window groups 2 wave, then every 2 KS.
+  const int nb = max(0, (G / 2 - wave + KS - 1) / KS);
+  if (nb > 0) {
+    uint4* xa = lds.x[0][wave];
+    uint4* xb = lds.x[1][wave];
+    uint4* wa = lds.w[0][wave];
+    uint4* wb = lds.w[1][wave];
+    uint4* sa = lds.s[0][wave];
+    uint4* sb = lds.s[1][wave];
+    int g = 2 * wave;
+    reuse_pfb_issue_ws<RT>(wa, sa, rw, rs, K, G, g, lane);
+    reuse_pfb_issue_x(xa, rx, bt0, B, K, g, lane);
+    for (int n = 0;;) {
+      if (n + 1 < nb) {
+        reuse_pfb_block<RT, NBT, true>(acc, wa, sa, wb, sb, xa, xb, rw, rs, rx, bt0, B, K, G, g,
+                                       g + 2 * KS, lane);
+      } else {
+        reuse_pfb_block<RT, NBT, false>(acc, wa, sa, wb, sb, xa, xb, rw, rs, rx, bt0, B, K, G, g,
+                                        0, lane);
+        break;
+      }
+      ++n;
+      g += 2 * KS;
+      if (n + 1 < nb) {
+        reuse_pfb_block<RT, NBT, true>(acc, wb, sb, wa, sa, xa, xb, rw, rs, rx, bt0, B, K, G, g,
+                                       g + 2 * KS, lane);
+      } else {
+        reuse_pfb_block<RT, NBT, false>(acc, wb, sb, wa, sa, xa, xb, rw, rs, rx, bt0, B, K, G, g,
+                                        0, lane);
+        break;
+      }
+      ++n;
+      g += 2 * KS;
+    }
+  }
+  // Every load of this wave has landed (the last step waited for all). Each
+  // wave's partials of (batch tile b, row tile t), i = b RT + t, go to its x
+  // buffer i / 8, slot i % 8; after the barrier wave w adds items w, w + KS,
+  // ... over the KS waves in wave order.
+  compiler_fence();
+#pragma unroll
+  for (int b = 0; b < NBT; ++b)
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      const int i = b * RT + t;
+      float* part = reinterpret_cast<float*>(lds.x[i / 8][wave]) + (i % 8) * 256;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) part[lane * 4 + v] = acc[b][t][v];
+    }
+  __syncthreads();
+  const int kq = lane >> 4;
+  for (int i = wave; i < NBT * RT; i += KS) {
+    f4_t sum = {0.f, 0.f, 0.f, 0.f};
+    for (int w2 = 0; w2 < KS; ++w2) {
+      const float* part = reinterpret_cast<const float*>(lds.x[i / 8][w2]) + (i % 8) * 256;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sum[v] += part[lane * 4 + v];
+    }
+    const int bcol = bt0 + 16 * (i / RT) + (lane & 15);
+    if (bcol < B) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int orow = row0 + 16 * (i % RT) + 4 * kq + v;
+        if (orow < M) y[(size_t)bcol * M + orow] = f2h(sum[v]);
+      }
     }
   }
 }

@@ -204,7 +204,21 @@ ROUTES = [
     ((28672, 8192, 8), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 2, 4>", [896, 1, 1]),
     ((8192, 3584, 3), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 2, true, 2>", [256, 1, 1]),
     ((5120, 5120, 4), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 2, true, 2>", [160, 1, 1]),
-    ((6144, 8192, 32), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 2, true, 2>", [192, 2, 1]),
+    ((6144, 8192, 32), dict(reuse_weights=1), "dk::gemv_reuse_pfb<4, 2, 2>", [192, 1, 1]),
+    # Above 16 batch rows, the many-batch tiles: the least reuse whose grid
+    # is one round of 144-256 workgroups, else the most reuse (two waves up
+    # to 512 workgroups); RT = 1 only above 32 batch rows.
+    ((4096, 4096, 48), dict(reuse_weights=1), "dk::gemv_reuse_pfb<4, 2, 2>", [128, 2, 1]),
+    ((4096, 4096, 128), dict(reuse_weights=1), "dk::gemv_reuse_pfb<4, 4, 2>", [64, 4, 1]),
+    ((4096, 4096, 256), dict(reuse_weights=1), "dk::gemv_reuse_pfb<4, 4, 4>", [64, 4, 1]),
+    ((4096, 4096, 257), dict(reuse_weights=1), "dk::gemv_reuse_pfb<2, 4, 4>", [64, 5, 1]),
+    ((2048, 8192, 48), dict(reuse_weights=1), "dk::gemv_reuse_pfb<4, 1, 2>", [128, 2, 1]),
+    ((2048, 8192, 32), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1, 8>", [128, 2, 1]),
+    ((8192, 8192, 256), dict(reuse_weights=1), "dk::gemv_reuse_pfb<2, 4, 4>", [128, 4, 1]),
+    ((11008, 4096, 32), dict(reuse_weights=1), "dk::gemv_reuse_pfb<4, 4, 2>", [172, 1, 1]),
+    ((1000, 1024, 300), dict(reuse_weights=1), "dk::gemv_reuse_pfb<4, 4, 2>", [16, 10, 1]),
+    ((1024, 4096, 64), dict(reuse_weights=1), "dk::gemv_reuse_lds<16, 1, true, 2>", [64, 4, 1]),
+    ((4096, 3968, 48), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 2, false, 2>", [128, 3, 1]),
     ((5120, 5120, 12), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 2, true, 2>", [160, 1, 1]),
     ((2048, 16384, 16), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1, 8>", [128, 1, 1]),
     ((2048, 16384, 8), dict(reuse_weights=1), "dk::gemv_reuse_pf<8, 1, 4>", [128, 1, 1]),

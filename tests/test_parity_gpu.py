@@ -234,6 +234,61 @@ def test_reuse_tile_kernel_exact_properties(m, k, b):
         _check_against_oracle(y, oracle.linear_f64(x, packed, scales), f"reuse {m}x{k} B={b}")
 
 
+# The many-batch tiles (gemv_reuse_pfb<KS, RT, NBT>) in each launch shape the
+# dispatch takes, with ragged M and B, a one-block row (K = 256: three of four
+# waves have no block), long rows, and 17-32 batch rows with RT >= 2.
+PFB_CASES = [
+    ((2048, 2048, 40), "gemv_reuse_pfb<4, 1, 2>"),
+    ((2000, 2048, 45), "gemv_reuse_pfb<4, 1, 2>"),
+    ((2048, 16384, 48), "gemv_reuse_pfb<4, 1, 2>"),
+    ((4096, 1024, 48), "gemv_reuse_pfb<4, 2, 2>"),
+    ((4000, 1280, 40), "gemv_reuse_pfb<4, 2, 2>"),
+    ((4096, 256, 48), "gemv_reuse_pfb<4, 2, 2>"),
+    ((5000, 1024, 20), "gemv_reuse_pfb<4, 2, 2>"),
+    ((4096, 1024, 128), "gemv_reuse_pfb<4, 4, 2>"),
+    ((4090, 768, 100), "gemv_reuse_pfb<4, 4, 2>"),
+    ((11008, 512, 24), "gemv_reuse_pfb<4, 4, 2>"),
+    ((4096, 1024, 256), "gemv_reuse_pfb<4, 4, 4>"),
+    ((4000, 1024, 250), "gemv_reuse_pfb<4, 4, 4>"),
+    ((4096, 512, 257), "gemv_reuse_pfb<2, 4, 4>"),
+    ((5000, 1024, 200), "gemv_reuse_pfb<2, 4, 4>"),
+]
+
+
+@pytest.mark.parametrize("shape,kernel", PFB_CASES)
+def test_reuse_many_batch_tiles(shape, kernel):
+    """Against the float64 oracle within half an fp16 ulp + 1e-3, plus the
+    exactness properties of the tile kernels: y(2x) = 2 y(x), y(-x) = -y(x),
+    a one-hot batch row selects single scaled weights bit for bit, and a
+    batch row alone at row 0 gives the outputs it has inside the batch."""
+    from decode_kernel import _abi
+
+    m, k, b = shape
+    print(f"[pfb] M={m} K={k} B={b} {kernel}", flush=True)
+    assert kernel in _abi.describe(_abi.load(), m, k, b, reuse_weights=1)["kernel"]
+    w, x = oracle.make_case(m, k, b, seed=11 + b, w_std=0.05)
+    packed, scales, pd, sd, xd = _upload(w, x)
+    y = _gemv(pd, sd, xd, reuse_weights=True)
+    _check_against_oracle(y, oracle.linear_f64(x, packed, scales), f"pfb {m}x{k} B={b}")
+    _assert_doubles(_gemv(pd, sd, xd * 2, reuse_weights=True), y, f"pfb {m}x{k} B={b}")
+    assert torch.equal(_gemv(pd, sd, -xd, reuse_weights=True), -y)
+    for j in (1, b - 1):
+        xs = torch.zeros(b, k, dtype=torch.float16, device="cuda")
+        xs[0] = xd[j]
+        assert torch.equal(_gemv(pd, sd, xs, reuse_weights=True)[0], y[j]), j
+    e = torch.zeros(b, k, dtype=torch.float16, device="cuda")
+    cols = [(i * 37 + 5) % k for i in range(b)]
+    for i, kk in enumerate(cols):
+        e[i, kk] = 1.0
+    ye = _gemv(pd, sd, e, reuse_weights=True).cpu().numpy()
+    for i, kk in enumerate(cols):
+        q = oracle.unpack_to_int(np.ascontiguousarray(packed[:, kk // 8: kk // 8 + 1]))[:, kk % 8]
+        expect = (scales[:, kk // 128].astype(np.float32) * q).astype(np.float16)
+        assert np.array_equal(ye[i].view(np.uint16), expect.view(np.uint16)), (i, kk)
+    # Repeated launches are bit-identical.
+    assert torch.equal(_gemv(pd, sd, xd, reuse_weights=True), y)
+
+
 @pytest.mark.parametrize("m,k,b", [(4096, 4096, 8), (8192, 8192, 4), (6144, 8192, 16),
                                    (28672, 1024, 5), (28672, 8192, 4), (2048, 8192, 16),
                                    (9000, 4096, 20), (1500, 8192, 12)])
