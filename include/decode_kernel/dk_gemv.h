@@ -52,14 +52,23 @@ typedef enum dk_kernel_version {
  * (GemvLaunchConfig); defaults are the same (v5, split_k 4, no reuse, 1). */
 typedef struct dk_gemv_config {
   int version;       /* dk_kernel_version, 0..5 */
-  int split_k;       /* v4 only, 1..32 (slices: min(split_k, K/128, 16));
-                        ignored otherwise */
-  int reuse_weights; /* nonzero: weight-reuse path, ignores version: MFMA tiles
-                        from 5 batch rows (3 at M * K >= 2^27 or with
-                        4096 < K < 8192 and M >= 3072, 4 at M >= 3072; 9 at
-                        M <= 2048, 17 at M <= 1024, 33 at M <= 512, none at
-                        M <= 128), the v5 kernel with batch tiles below that
-                        (stamp 15) */
+  int split_k;       /* v4 only, 1..32: caps the waves that share a row
+                        at min(split_k, K/128, 8). With a cap of 1 one
+                        wave per row, else two; four (cap >= 4) at
+                        M <= 512 on rows of more than 4096 weights and at
+                        M <= 1024 on rows of 16384+; two at most for a
+                        batch. Ignored otherwise */
+  int reuse_weights; /* nonzero: weight-reuse path, ignores version (stamp
+                        15). The v5 kernel with batch tiles for up to two
+                        batch rows and at M <= 128, up to 32 at M <= 512,
+                        up to 11 at M <= 1024, up to 4 at M <= 2048 (8 on
+                        rows of fewer than 8192 weights with an odd group
+                        count), and at three batch rows unless K >= 8192,
+                        M >= 8192, M * K >= 2^27, M >= 3072 with
+                        4096 < K < 8192, or 2048 < M <= 4096 with
+                        K <= 4096; MFMA tiles otherwise, one workgroup per
+                        16 batch rows up to 16 and, above, workgroups of
+                        2-8 tiles of 16 batch rows where the groups pair */
   int warps_per_row; /* v1 only, 1..8: wave64s sharing one row's K */
 } dk_gemv_config;
 

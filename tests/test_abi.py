@@ -233,6 +233,34 @@ ROUTES = [
     ((1024, 4096, 8), dict(reuse_weights=1), "dk::gemv_v5_lds<1, 2, 8, 2, true, dk::LayoutLogical, 15,",
      [128, 4, 1]),
     ((1024, 4096, 12), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1, 8>", [64, 1, 1]),
+    # The boundaries the header documents for reuse_weights: the streaming
+    # kernel's batch tiles on one side, MFMA tiles on the other.
+    ((128, 4096, 64), dict(reuse_weights=1), "dk::gemv_v5_lds<1, 2, 8, 2, true, dk::LayoutLogical, 15,",
+     [16, 32, 1]),
+    ((144, 4096, 64), dict(reuse_weights=1), "dk::gemv_reuse_lds<16, 1, true, 2>", [9, 4, 1]),
+    ((512, 8192, 32), dict(reuse_weights=1), "dk::gemv_v5_lds<1, 2, 8, 2, true, dk::LayoutLogical, 15,",
+     [64, 16, 1]),
+    ((1024, 4096, 11), dict(reuse_weights=1), "dk::gemv_v5_lds<1, 2, 8, 2, true, dk::LayoutLogical, 15,",
+     [128, 6, 1]),
+    ((2048, 4096, 4), dict(reuse_weights=1), "dk::gemv_v5_lds<2, 2, 8, 2, true, dk::LayoutLogical, 15,",
+     [128, 2, 1]),
+    ((2048, 4096, 5), dict(reuse_weights=1), "dk::gemv_reuse_pf<6, 1, 4>", [128, 1, 1]),
+    ((2048, 4224, 8), dict(reuse_weights=1), "dk::gemv_v5_lds<1, 1, 16, 4, true, dk::LayoutLogical, 15,",
+     [128, 2, 1]),
+    ((2048, 4224, 9), dict(reuse_weights=1), "dk::gemv_reuse_lds<16, 1, false, 2>", [128, 1, 1]),
+    ((4096, 4096, 2), dict(reuse_weights=1), "dk::gemv_v5_lds<1, 2, 8, 2, true, dk::LayoutLogical, 15,",
+     [512, 1, 1]),
+    # The waves per row of v4 that the header documents for split_k.
+    ((4096, 4096, 1), dict(version=4, split_k=1), "dk::gemv_v4_split<1, 2, 8, 1, 1, true,", [512, 1, 1]),
+    ((4096, 4096, 1), dict(version=4, split_k=32), "dk::gemv_v4_split<1, 1, 8, 2, 1, true,",
+     [1024, 1, 1]),
+    ((1024, 28672, 1), dict(version=4, split_k=4), "dk::gemv_v4_split<2, 2, 8, 4, 1, false,",
+     [256, 1, 1]),
+    ((1024, 28672, 1), dict(version=4, split_k=2), "dk::gemv_v4_split<1, 4, 8, 2, 1, false,",
+     [256, 1, 1]),
+    ((512, 8192, 1), dict(version=4, split_k=8), "dk::gemv_v4_split<1, 2, 8, 4, 1, true,", [256, 1, 1]),
+    ((1024, 28672, 3), dict(version=4, split_k=32), "dk::gemv_v4_split<1, 1, 8, 2, 4, true,",
+     [256, 1, 1]),
 ]
 
 
