@@ -29,7 +29,8 @@ sys.path.insert(0, str(HERE.parents[2]))
 
 SHAPES = {"c0": (4096, 4096, 1), "c1": (11008, 4096, 1), "c2": (4096, 11008, 1),
           "c3b4": (4096, 4096, 4), "c3b8": (4096, 4096, 8), "c3b12": (4096, 4096, 12),
-          "c3b16": (4096, 4096, 16), "c4ab4": (28672, 8192, 4),
+          "c3b16": (4096, 4096, 16), "c3b48": (4096, 4096, 48), "c3b128": (4096, 4096, 128),
+          "c3b256": (4096, 4096, 256), "c4ab4": (28672, 8192, 4),
           "c4a": (28672, 8192, 1), "c4ab8": (28672, 8192, 8), "c4b": (8192, 28672, 1),
           # shapes of the reuse path's two-tile and split-K routes
           "m6144k8192b16": (6144, 8192, 16), "m1024k16384b16": (1024, 16384, 16),
