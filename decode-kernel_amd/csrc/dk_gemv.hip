@@ -157,8 +157,8 @@ int launch_split(const Launch& L, const uint4* p, const uint16_t* s, const uint4
 
 // v4 launch plan. split_k caps the waves per row (S, a power of two, also at
 // most K / 128 and 8). Set from a sweep of 62 shapes (R 1-2, U 1-4, W 4-16,
-// S 2-8, prefetch on and off) at 24 shapes of M and K (dk_bench.levers v4 and
-// split), us per launch, the choice against the best:
+// S 2-8, prefetch on and off) at 24 shapes of M and K, timed back to back
+// over cold weights, us per launch, the choice against the best:
 //   M = K = 4096:         R1 U1 W8  S2 pf    3.62 (3.60)
 //   M = 4096, K = 11008:  R1 U1 W16 S2 pf    6.10 (6.10)
 //   M = 4096, K = 28672:  R2 U1 W16 S2 pf   11.53 (11.53)
@@ -701,7 +701,8 @@ struct PfShape {
 };
 
 // Where the double-buffered tiles take the single pass (paired scales
-// only). From the sweep of every tile kernel (dk_bench.levers reuse), us,
+// only). From a sweep of every tile kernel, timed back to back over cold
+// weights, us,
 // the double-buffered tiles against the best single-buffered ones in
 // brackets; from 9 batch rows 4 waves with 8 x loads per block:
 //                        B = 12         B = 16         B = 32
@@ -877,7 +878,8 @@ enum class ReuseShape { kStream, kTiles };
 
 // Which kernel the reuse path takes, from a sweep of the tile kernels (both
 // forms, 4-16 waves, one or two tiles per wave) against the streaming
-// kernel at 3-32 batch rows on 11 shapes (dk_bench.levers reuse), us:
+// kernel at 3-32 batch rows on 11 shapes, timed back to back over cold
+// weights, us:
 //   M = 2048, K = 16384: B = 4 stream 9.02 (tiles 9.37), B = 5 tiles 9.97 (stream 10.80)
 //   M = 2048, K = 8192:  B = 4 stream 5.74 (6.19), B = 8 tiles 7.12 (7.66)
 //   M = 1024, K = 4096:  B = 8 stream 3.73 (4.64), B = 12 tiles 4.87 (4.99)
