@@ -288,7 +288,7 @@ DKB_API int dkb_v4s(int math, int R, int U, int W, int S, int pf, const void* pa
     const int rows = w / k * r;                                                                 \
     hipLaunchKernelGGL((dk::gemv_v4_split<r, u, w, k, 1, f, Mt>), dim3((M + rows - 1) / rows),   \
                        dim3(w * 64), 0, stream, p, s, xx, yy, static_cast<float*>(nullptr), M, K, \
-                       1, 4);                                                                   \
+                       1);                                                                      \
     return launch_error("v4 split");                                                            \
   }
 #define DKB_V4S_ABL(r, u, w, k, f)                                                         \

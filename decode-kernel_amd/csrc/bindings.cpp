@@ -351,7 +351,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("stream_recommended_blocks", &stream_recommended_blocks,
         "Block count used by STREAM probes");
   m.def("last_kernel_stamp", &last_kernel_stamp,
-        "Stage stamp written by the GEMV that actually launched");
+        "Dispatch stamp of the GEMV last launched on this device (read and cleared)");
   m.def("empty_kernel", &empty_kernel, "Empty kernel on the current stream (launch floor)");
   m.def("workspace_bytes", &workspace_bytes, "Device workspace bytes a GEMV call needs",
         py::arg("M"), py::arg("K"), py::arg("B"), py::arg("version") = 5, py::arg("split_k") = 4,

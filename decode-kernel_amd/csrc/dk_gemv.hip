@@ -1,6 +1,6 @@
 // W4A16 decode GEMV for MI355X (gfx950, CDNA4, wave64).
 //
-// One translation unit holds every GEMV variant, the dispatch stamp and the
+// One translation unit holds every GEMV variant, the dispatch stamps and the
 // C ABI declared in include/decode_kernel/dk_gemv.h. The variants keep the
 // reference's numbering and stamps (csrc/gemv_w4a16.cu:67-413) but each is
 // written for CDNA4: wave64 lanes, 16-byte coalesced loads, whole-word nibble
@@ -8,7 +8,7 @@
 // accumulation, DPP wave reductions and a single-launch split-K.
 //
 // The kernels themselves are in dk_kernels.hpp; the fused gate/up kernel of
-// the MLP decode step (dk_mlp.h) is in dk_mlp.hpp and shares the stamp.
+// the MLP decode step (dk_mlp.h) is in dk_mlp.hpp and shares the stamps.
 #include <hip/hip_runtime.h>
 
 #include <cxxabi.h>
@@ -91,6 +91,11 @@ void kernel_name(const void* handle, char* out, size_t len) {
   std::free(dem);
 }
 
+// Dispatch stamps, one per device (dk_last_kernel_stamp): stamp + 1 of the
+// last successful launch on that device, 0 for none since the last read.
+constexpr int kStampDevices = 64;
+std::atomic<int> g_stamps[kStampDevices];
+
 // Launches one kernel on `stream` and reports a launch error as DK_ERR_HIP.
 // With `info` set it launches nothing and records the kernel and its launch
 // shape instead (dk_gemv_describe); the first launch of a call is recorded
@@ -98,6 +103,16 @@ void kernel_name(const void* handle, char* out, size_t len) {
 struct Launch {
   hipStream_t stream;
   dk_launch_info* info = nullptr;
+
+  // After a successful launch: records `stamp` as the current device's
+  // dispatch stamp (not in describe mode). Returns rc.
+  int stamp(int rc, int stamp) const {
+    if (rc != DK_OK || info) return rc;
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kStampDevices)
+      g_stamps[dev].store(stamp + 1, std::memory_order_relaxed);
+    return rc;
+  }
 
   template <typename... KArgs, typename... Args>
   int operator()(const char* what, void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds,
@@ -129,19 +144,19 @@ struct SplitShape {
 
 template <int R, int U, int W, int S, int NB, bool PF>
 int launch_split_t(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
-                   float* acc, int M, int K, int B, int stamp) {
+                   float* acc, int M, int K, int B) {
   constexpr int kRows = W / S * R;
   const dim3 grid((M + kRows - 1) / kRows, (B + NB - 1) / NB);
   return L("split-K launch", dk::gemv_v4_split<R, U, W, S, NB, PF>, grid, dim3(W * 64), 0, p, s, x,
-           y, acc, M, K, B, stamp);
+           y, acc, M, K, B);
 }
 
 // acc: the reference's [B, M] fp32 buffer to receive the sums, or NULL.
 int launch_split(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
-                 float* acc, int M, int K, int B, const SplitShape& sh, int stamp) {
+                 float* acc, int M, int K, int B, const SplitShape& sh) {
 #define DK_SPLIT(r, u, w, k, nb, f)                                                          \
   if (sh.R == r && sh.U == u && sh.W == w && sh.S == k && sh.NB == nb && sh.pf == f)        \
-    return launch_split_t<r, u, w, k, nb, f>(L, p, s, x, y, acc, M, K, B, stamp);
+    return launch_split_t<r, u, w, k, nb, f>(L, p, s, x, y, acc, M, K, B);
   DK_SPLIT(1, 2, 8, 1, 1, true) DK_SPLIT(1, 2, 8, 4, 1, false) DK_SPLIT(1, 4, 4, 2, 1, false)
   DK_SPLIT(1, 1, 4, 2, 1, true) DK_SPLIT(1, 2, 8, 4, 1, true) DK_SPLIT(1, 4, 4, 2, 1, true)
   DK_SPLIT(2, 2, 8, 4, 1, false) DK_SPLIT(1, 4, 8, 2, 1, false) DK_SPLIT(1, 2, 4, 2, 1, true)
@@ -200,7 +215,7 @@ SplitShape v4_plan(int M, int K, int B, int split_k) {
 
 int launch_v4(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x, uint16_t* y,
               float* acc, int M, int K, int B, int split_k) {
-  return launch_split(L, p, s, x, y, acc, M, K, B, v4_plan(M, K, B, split_k), 4);
+  return launch_split(L, p, s, x, y, acc, M, K, B, v4_plan(M, K, B, split_k));
 }
 
 // One batch row at the shapes where the split-K kernel beats gemv_v5_lds by
@@ -297,7 +312,7 @@ int launch_lds(const Launch& L, const uint4* p, const uint16_t* s, const uint4* 
                int M, int K) {
   SplitShape sh;
   if (std::is_same<Layout, dk::LayoutLogical>::value && v5_takes_split(M, K, &sh))
-    return launch_split(L, p, s, x, y, nullptr, M, K, 1, sh, kStamp);
+    return launch_split(L, p, s, x, y, nullptr, M, K, 1, sh);
   if (K <= 2048) return launch_lds_t<1, 1, 16, true, Layout, kStamp>(L, p, s, x, y, M, K);
   if (M <= 3072) {
     if (K <= 4096) return launch_lds_t<1, 2, 4, true, Layout, kStamp>(L, p, s, x, y, M, K);
@@ -975,32 +990,39 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
 
   if (cfg->reuse_weights) {
     if (reuse_shape(M, K, B) == ReuseShape::kStream)
-      return launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B);
-    if (split) return launch_reuse_split(L, p4, scales, x4, y, M, K, B, workspace);
-    return launch_reuse_tiles(L, p4, scales, x4, y, M, K, B);
+      return L.stamp(launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B),
+                     DK_STAMP_REUSE);
+    if (split)
+      return L.stamp(launch_reuse_split(L, p4, scales, x4, y, M, K, B, workspace), DK_STAMP_REUSE);
+    return L.stamp(launch_reuse_tiles(L, p4, scales, x4, y, M, K, B), DK_STAMP_REUSE);
   }
   const dim3 block4(kWavesPerBlock * 64);
   const dim3 rows4((M + kWavesPerBlock - 1) / kWavesPerBlock);
   switch (cfg->version) {
     case DK_V0:
-      return L("v0 launch", dk::gemv_v0, dim3((M + 255) / 256), dim3(256), 0, packed, scales, x, y,
-               M, K, B);
+      return L.stamp(L("v0 launch", dk::gemv_v0, dim3((M + 255) / 256), dim3(256), 0, packed,
+                       scales, x, y, M, K, B),
+                     DK_V0);
     case DK_V1:
       if (cfg->warps_per_row > 1) {
         const int wpr = clamp_wpr(cfg->warps_per_row);
-        return L("v1 multiwave launch", dk::gemv_v1_multiwave, dim3(M), dim3(wpr * 64), 0, packed,
-                 scales, x4, y, M, K, B);
+        return L.stamp(L("v1 multiwave launch", dk::gemv_v1_multiwave, dim3(M), dim3(wpr * 64), 0,
+                         packed, scales, x4, y, M, K, B),
+                       DK_STAMP_MULTIWAVE_BASE + wpr);
       }
-      return L("v1 launch", dk::gemv_v1, rows4, block4, 0, packed, scales, x4, y, M, K, B);
+      return L.stamp(L("v1 launch", dk::gemv_v1, rows4, block4, 0, packed, scales, x4, y, M, K, B),
+                     DK_V1);
     case DK_V2:
-      return L("v2 launch", dk::gemv_v23<false>, rows4, block4, 0, p4, scales, x4, y, M, K, B);
+      return L.stamp(
+          L("v2 launch", dk::gemv_v23<false>, rows4, block4, 0, p4, scales, x4, y, M, K, B), DK_V2);
     case DK_V3:
-      return L("v3 launch", dk::gemv_v23<true>, rows4, block4, v3_lds_bytes(K), p4, scales, x4, y,
-               M, K, B);
+      return L.stamp(L("v3 launch", dk::gemv_v23<true>, rows4, block4, v3_lds_bytes(K), p4, scales,
+                       x4, y, M, K, B),
+                     DK_V3);
     case DK_V4:
-      return launch_v4(L, p4, scales, x4, y, nullptr, M, K, B, cfg->split_k);
+      return L.stamp(launch_v4(L, p4, scales, x4, y, nullptr, M, K, B, cfg->split_k), DK_V4);
     case DK_V5:
-      return launch_v5(L, p4, scales, x4, y, M, K, B);
+      return L.stamp(launch_v5(L, p4, scales, x4, y, M, K, B), DK_V5);
     default:
       return fail(DK_ERR_INVALID_ARGUMENT, "unknown version %d", cfg->version);
   }
@@ -1023,8 +1045,9 @@ int gemv_ref_workspace_impl(const uint32_t* packed, const uint16_t* scales, cons
   if (!acc)
     return fail(DK_ERR_INVALID_ARGUMENT, "v4 needs the caller-zeroed fp32 [B, M] workspace");
   if (!aligned(acc, 4)) return fail(DK_ERR_INVALID_ARGUMENT, "workspace must be 4-byte aligned");
-  return launch_v4(L, reinterpret_cast<const uint4*>(packed), scales,
-                   reinterpret_cast<const uint4*>(x), y, acc, M, K, B, cfg->split_k);
+  return L.stamp(launch_v4(L, reinterpret_cast<const uint4*>(packed), scales,
+                           reinterpret_cast<const uint4*>(x), y, acc, M, K, B, cfg->split_k),
+                 DK_V4);
 }
 
 }  // namespace
@@ -1168,19 +1191,14 @@ int dk_last_kernel_stamp(void) {
     dk::hip_error(e, "hipDeviceSynchronize");
     return -1;
   }
-  int h = -1;
-  e = hipMemcpyFromSymbol(&h, HIP_SYMBOL(dk::g_stamp), sizeof(int), 0, hipMemcpyDeviceToHost);
+  int dev = 0;
+  e = hipGetDevice(&dev);
   if (e != hipSuccess) {
-    dk::hip_error(e, "read stamp");
+    dk::hip_error(e, "hipGetDevice");
     return -1;
   }
-  const int neg = -1;
-  e = hipMemcpyToSymbol(HIP_SYMBOL(dk::g_stamp), &neg, sizeof(int), 0, hipMemcpyHostToDevice);
-  if (e != hipSuccess) {
-    dk::hip_error(e, "clear stamp");
-    return -1;
-  }
-  return h;
+  if (dev < 0 || dev >= kStampDevices) return -1;
+  return g_stamps[dev].exchange(0, std::memory_order_relaxed) - 1;
 }
 
 int dk_w4a16_gemv_paired(const uint32_t* paired, const uint16_t* scales, const uint16_t* x,
@@ -1196,8 +1214,10 @@ int dk_w4a16_gemv_paired(const uint32_t* paired, const uint16_t* scales, const u
     return fail(DK_ERR_INVALID_ARGUMENT, "paired and x must be 16-byte aligned");
   if (!aligned(scales, 2) || !aligned(y, 2))
     return fail(DK_ERR_INVALID_ARGUMENT, "scales and y must be 2-byte aligned");
-  return launch_v5<dk::LayoutPaired>(Launch{stream}, reinterpret_cast<const uint4*>(paired), scales,
-                                     reinterpret_cast<const uint4*>(x), y, M, K, B);
+  const Launch L{stream};
+  return L.stamp(launch_v5<dk::LayoutPaired>(L, reinterpret_cast<const uint4*>(paired), scales,
+                                             reinterpret_cast<const uint4*>(x), y, M, K, B),
+                 DK_STAMP_PAIRED);
 }
 
 int dk_gate_up_silu(const uint32_t* gate_packed, const uint16_t* gate_scales,
@@ -1215,9 +1235,11 @@ int dk_gate_up_silu(const uint32_t* gate_packed, const uint16_t* gate_scales,
     return fail(DK_ERR_INVALID_ARGUMENT, "gate, up and x must be 16-byte aligned");
   if (!aligned(gate_scales, 2) || !aligned(up_scales, 2) || !aligned(h, 2))
     return fail(DK_ERR_INVALID_ARGUMENT, "scales and h must be 2-byte aligned");
-  return launch_gate_up(Launch{stream}, reinterpret_cast<const uint4*>(gate_packed), gate_scales,
-                        reinterpret_cast<const uint4*>(up_packed), up_scales,
-                        reinterpret_cast<const uint4*>(x), h, I, H, B);
+  const Launch L{stream};
+  return L.stamp(launch_gate_up(L, reinterpret_cast<const uint4*>(gate_packed), gate_scales,
+                                reinterpret_cast<const uint4*>(up_packed), up_scales,
+                                reinterpret_cast<const uint4*>(x), h, I, H, B),
+                 DK_STAMP_GATE_UP);
 }
 
 size_t dk_mlp_workspace_bytes(int I, int H, int B) {

@@ -1,6 +1,6 @@
 // Every W4A16 GEMV kernel for gfx950, as templates and __global__ functions.
-// Included by exactly one translation unit of the library (dk_gemv.hip),
-// which owns the one __device__ global defined here (the dispatch stamp).
+// Included by exactly one translation unit of the library (dk_gemv.hip) and
+// by the measurement library.
 //
 // Layout in HBM (the reference format, no repacking):
 //   packed uint32 [M, K/8]: row m is K/2 bytes; 16-byte chunk c of a row holds
@@ -17,15 +17,12 @@
 namespace dk {
 
 // ---------------------------------------------------------------------------
-// Dispatch stamp: written by block (0,0) thread 0 of whichever GEMV kernel
-// ran. Host reads and clears it in dk_last_kernel_stamp().
-// Reference: csrc/gemv_w4a16.cu:18-25.
+// Dispatch stamps (the reference's numbering, csrc/gemv_w4a16.cu:18-25,74-368)
+// are recorded by the host when a launch succeeds (dk_last_kernel_stamp);
+// no kernel writes one. A template's kStamp names the stamp its launches
+// record. (A stamp store from one thread of one workgroup, as the reference
+// writes it, measured 0.04-0.05 us per launch on MI355X: 1.3% at M = K = 4096.)
 // ---------------------------------------------------------------------------
-__device__ int g_stamp = -1;
-
-__device__ __forceinline__ void write_stamp(int s) {
-  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) g_stamp = s;
-}
 
 // ---------------------------------------------------------------------------
 // v0: one thread per row, scalar decode (the uncoalesced baseline stage).
@@ -35,7 +32,6 @@ __global__ __launch_bounds__(256) void gemv_v0(const uint32_t* __restrict__ pack
                                                const uint16_t* __restrict__ scales,
                                                const uint16_t* __restrict__ x,
                                                uint16_t* __restrict__ y, int M, int K, int B) {
-  write_stamp(0);
   const int row = blockIdx.x * blockDim.x + threadIdx.x;
   if (row >= M) return;
   const int words = K >> 3;
@@ -67,7 +63,6 @@ __global__ __launch_bounds__(256) void gemv_v1(const uint32_t* __restrict__ pack
                                                const uint16_t* __restrict__ scales,
                                                const uint4* __restrict__ x4,
                                                uint16_t* __restrict__ y, int M, int K, int B) {
-  write_stamp(1);
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= M) return;
@@ -98,7 +93,6 @@ __global__ __launch_bounds__(512) void gemv_v1_multiwave(const uint32_t* __restr
                                                          uint16_t* __restrict__ y, int M, int K,
                                                          int B) {
   const int wpr = blockDim.x >> 6;
-  write_stamp(10 + wpr);
   __shared__ float red[8];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -137,7 +131,6 @@ __global__ __launch_bounds__(256) void gemv_v23(const uint4* __restrict__ packed
                                                 const uint16_t* __restrict__ scales,
                                                 const uint4* __restrict__ x4,
                                                 uint16_t* __restrict__ y, int M, int K, int B) {
-  write_stamp(kScalesInLds ? 3 : 2);
   extern __shared__ uint16_t lds_scales[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -448,7 +441,6 @@ __global__ __launch_bounds__(W * kWave) void gemv_v5_lds(const uint4* __restrict
                                                          const uint4* __restrict__ x4,
                                                          uint16_t* __restrict__ y, int M, int K,
                                                          int B) {
-  write_stamp(kStamp);
   __shared__ LdsActs<U, NB> xs;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -542,7 +534,7 @@ __device__ __forceinline__ void release_ticket(unsigned long long* ticket, unsig
 // kS of them in slice order (deterministic; fixed for a launch shape) and
 // writes y, and the fp32 sums to `acc` when one is given (the reference's
 // workspace contract). One launch, no workspace: the slices meet inside one
-// CU. kS = 1 is the GEMV. The stamp is an argument: 4 for v4, 5 where the
+// CU. kS = 1 is the GEMV. Its launches record stamp 4 for v4, 5 where the
 // v5 dispatch takes this kernel (it is faster than gemv_v5_lds at some
 // shapes).
 // ---------------------------------------------------------------------------
@@ -552,11 +544,10 @@ __global__ __launch_bounds__(W * kWave) void gemv_v4_split(const uint4* __restri
                                                            const uint4* __restrict__ x4,
                                                            uint16_t* __restrict__ y,
                                                            float* __restrict__ acc_out, int M,
-                                                           int K, int B, int stamp) {
+                                                           int K, int B) {
   static_assert(W % kS == 0, "a workgroup holds whole rows");
   constexpr int kRowWaves = W / kS;
   constexpr int kRows = kRowWaves * R;  // rows per workgroup
-  write_stamp(stamp);
   __shared__ LdsActs<kS * U, NB> xs;
   __shared__ float red[kS > 1 ? kS * NB * kRows : 1];
   const int tid = threadIdx.x;
@@ -804,7 +795,6 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse(const uint4* __restrict__ 
                                                       uint16_t* __restrict__ y, int M, int K,
                                                       int B) {
   static_assert(KS >= RT, "wave t sums tile t");
-  write_stamp(DK_STAMP_REUSE);
   __shared__ ReuseLds<KS, RT, SG> lds;
   const int G = K >> 7;
   const int nck = K >> 5;
@@ -1051,7 +1041,6 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_lds(const uint4* __restric
                                                           uint16_t* __restrict__ y, int M, int K,
                                                           int B) {
   static_assert(KS >= RT, "wave t sums tile t");
-  write_stamp(DK_STAMP_REUSE);
   __shared__ ReuseDmaLds<KS, RT, SG> lds;
   const int G = K >> 7;
   const int nck = K >> 5;
@@ -1338,7 +1327,6 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_pf(const uint4* __restrict
                                                          uint16_t* __restrict__ y, int M, int K,
                                                          int B) {
   static_assert(KS >= RT, "wave t sums tile t");
-  write_stamp(DK_STAMP_REUSE);
   __shared__ ReusePfLds<KS, RT, 2 * kXL> lds;
   const int G = K >> 7;
   const int nck = K >> 5;
@@ -1540,7 +1528,6 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_pfb(const uint4* __restric
                                                           uint16_t* __restrict__ y, int M, int K,
                                                           int B) {
   static_assert(NBT * RT <= 16, "the partials fit a wave's two x buffers");
-  write_stamp(DK_STAMP_REUSE);
   __shared__ ReusePfLds<KS, RT, 16> lds;
   const int G = K >> 7;
   const int nck = K >> 5;
@@ -1692,7 +1679,6 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_split(
     const uint4* __restrict__ x4, uint16_t* __restrict__ y, float* __restrict__ partials,
     unsigned long long* __restrict__ tickets, unsigned long long gen, int M, int K, int B) {
   static_assert(KS >= RT, "wave t sums tile t");
-  write_stamp(DK_STAMP_REUSE);
   __shared__ ReuseLds<KS, RT, SG> lds;
   __shared__ int last;
   const int S = gridDim.z;
@@ -1742,7 +1728,6 @@ __global__ __launch_bounds__(KS * 64) void gemv_reuse_split_pf(
     const uint4* __restrict__ x4, uint16_t* __restrict__ y, float* __restrict__ partials,
     unsigned long long* __restrict__ tickets, unsigned long long gen, int M, int K, int B) {
   static_assert(KS >= RT, "wave t sums tile t");
-  write_stamp(DK_STAMP_REUSE);
   __shared__ ReusePfLds<KS, RT> lds;
   const int S = gridDim.z;
   const int Gall = K >> 7;

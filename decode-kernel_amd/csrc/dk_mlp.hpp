@@ -27,8 +27,6 @@
 
 namespace dk {
 
-constexpr int kStampGateUp = 20;
-
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + expf(-v)); }
 
 // The stage loop of gemv_v5_lds with NB batch rows per stage (grid.y covers
@@ -38,7 +36,6 @@ __global__ __launch_bounds__(W * kWave) void gate_up_silu_lds(
     const uint4* __restrict__ gate, const uint16_t* __restrict__ gate_scales,
     const uint4* __restrict__ up, const uint16_t* __restrict__ up_scales,
     const uint4* __restrict__ x4, int I, int H, int B, uint16_t* __restrict__ h) {
-  write_stamp(kStampGateUp);
   __shared__ LdsActs<U, NB> xs;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -82,7 +79,6 @@ __global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles(
     const uint4* __restrict__ gate, const uint16_t* __restrict__ gate_scales,
     const uint4* __restrict__ up, const uint16_t* __restrict__ up_scales,
     const uint4* __restrict__ x4, int I, int H, int B, uint16_t* __restrict__ h) {
-  write_stamp(kStampGateUp);
   __shared__ ReuseLds<KS, 2, SG> lds;
   const int G = H >> 7;
   const int nck = H >> 5;
@@ -126,7 +122,6 @@ __global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles_lds(
     const uint4* __restrict__ gate, const uint16_t* __restrict__ gate_scales,
     const uint4* __restrict__ up, const uint16_t* __restrict__ up_scales,
     const uint4* __restrict__ x4, int I, int H, int B, uint16_t* __restrict__ h) {
-  write_stamp(kStampGateUp);
   __shared__ ReuseDmaLds<KS, 2> lds;
   const int G = H >> 7;
   const int nck = H >> 5;
@@ -172,7 +167,6 @@ __global__ __launch_bounds__(KS * 64) void gate_up_silu_tiles_pf(
     const uint4* __restrict__ gate, const uint16_t* __restrict__ gate_scales,
     const uint4* __restrict__ up, const uint16_t* __restrict__ up_scales,
     const uint4* __restrict__ x4, int I, int H, int B, uint16_t* __restrict__ h) {
-  write_stamp(kStampGateUp);
   __shared__ ReusePfLds<KS, 2, 2 * kXL> lds;
   const int G = H >> 7;
   const int nck = H >> 5;

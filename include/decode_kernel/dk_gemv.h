@@ -31,8 +31,9 @@ extern "C" {
 #define DK_WEIGHTS_PER_CHUNK 32 /* one 16-byte load of packed weights */
 
 /* Kernel variants. Reference: include/decode_kernel/gemv_w4a16.h:13-20.
- * Each variant is a distinct gfx950 kernel and writes its own dispatch stamp:
- * v0..v5 -> 0..5, waves-per-row w (2..8) -> 10+w, weight-reuse -> 15. */
+ * Each variant is a distinct gfx950 kernel with its own dispatch stamp
+ * (dk_last_kernel_stamp): v0..v5 -> 0..5, waves-per-row w (2..8) -> 10+w,
+ * weight-reuse -> 15. */
 typedef enum dk_kernel_version {
   DK_V0 = 0, /* one thread per row (naive baseline) */
   DK_V1 = 1, /* one wave64 per row, 4-byte coalesced word loads */
@@ -210,11 +211,13 @@ int dk_stream_write(void* dst, size_t bytes, int blocks, hipStream_t stream);
  * Returns a negative dk_status on error. */
 int dk_stream_recommended_blocks(void);
 
-/* Stamp written by the last GEMV kernel that ran on the current device, or -1
- * if none ran since the previous read. Synchronises the device, reads the
- * stamp and clears it to -1 (the reference cleared it with an extra host-to-
- * device copy before every launch, csrc/gemv_w4a16.cu:553-564,573).
- * Returns -1 on error as well; see dk_last_error(). */
+/* Stamp of the last GEMV kernel launched on the current device, or -1 if
+ * none was launched since the previous read. The host records it when a
+ * launch succeeds (the reference's kernels wrote it to a device global,
+ * cleared with an extra host-to-device copy before every launch,
+ * csrc/gemv_w4a16.cu:18-25,553-564,573; that store costs 0.04-0.05 us per
+ * launch here). Synchronises the device, then reads the stamp and clears it
+ * to -1. Returns -1 on error as well; see dk_last_error(). */
 int dk_last_kernel_stamp(void);
 
 /* An empty kernel on `stream`: the per-launch floor for the benchmark.

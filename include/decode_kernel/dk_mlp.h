@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-/* Dispatch stamp written by the fused gate/up kernel. */
+/* Dispatch stamp of the fused gate/up kernel (dk_last_kernel_stamp). */
 #define DK_STAMP_GATE_UP 20
 
 /* h[b, i] = fp16(silu(g) * u) for g = Wg x, u = Wu x. I, H, B <= 0 is a no-op.
