@@ -912,20 +912,6 @@ __device__ __forceinline__ void reuse_lds_block(f4_t (&acc)[RT], uint4* xbuf, ui
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rwt, (lds_void_ptr)(wbuf + i * 64), 16, off, 0, 0,
                                              kLoadNonTemporal);
   }
-  // x: load i covers batch rows bt0 + kXR i .. + kXR - 1, lane l chunk
-  // l % kXC of row kXR i + l / kXC (chunk c = group c / 16, bytes 16 (c % 16)).
-#pragma unroll
-  for (int i = 0; i < 16 / kXR; ++i) {
-    if (i < nxl) {
-      const int bb = kXR * i + lane / kXC;
-      const int p = lane % kXC;
-      const int c = (p & ~15) | ((p ^ stage_swizzle<kXC>(bb)) & 15);
-      const bool ok = bt0 + bb < B && (!kTail || g0 * 16 + c < G * 16);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rx, (lds_void_ptr)(xbuf + i * 64), 16,
-          ok ? (bt0 + bb) * K * 2 + (g0 * 16 + c) * 16 : kOutOfRange, 0, 0, 0);
-    }
-  }
   // Scales of this lane's four D rows: two groups in one 4-byte load where
   // the scales allow (an even number of groups, so g0 + 2v + 1 < G when
   // g0 + 2v < G).
@@ -951,6 +937,20 @@ __device__ __forceinline__ void reuse_lds_block(f4_t (&acc)[RT], uint4* xbuf, ui
         }
       }
     }
+  // x: load i covers batch rows bt0 + kXR i .. + kXR - 1, lane l chunk
+  // l % kXC of row kXR i + l / kXC (chunk c = group c / 16, bytes 16 (c % 16)).
+#pragma unroll
+  for (int i = 0; i < 16 / kXR; ++i) {
+    if (i < nxl) {
+      const int bb = kXR * i + lane / kXC;
+      const int p = lane % kXC;
+      const int c = (p & ~15) | ((p ^ stage_swizzle<kXC>(bb)) & 15);
+      const bool ok = bt0 + bb < B && (!kTail || g0 * 16 + c < G * 16);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rx, (lds_void_ptr)(xbuf + i * 64), 16,
+          ok ? (bt0 + bb) * K * 2 + (g0 * 16 + c) * 16 : kOutOfRange, 0, 0, 0);
+    }
+  }
   // Every load of the block, LDS writes included, has landed.
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1131,10 +1131,16 @@ struct ReuseWindow {
   int bt0, B, K, G, Gs, gbeg;
 };
 
-// Issues the loads of the block at window group g0 into xb, wb, sb: the
-// kXL x loads of batch rows bt0 .. bt0 + 2 kXL - 1 (the rows the x buffer
-// holds), those of rows >= B out of range, so that each block issues the
-// same number of loads.
+// Issues the loads of the block at window group g0 into wb, sb, xb: the
+// weights and scale pairs first (from HBM), then the kXL x loads of batch
+// rows bt0 .. bt0 + 2 kXL - 1 (the rows the x buffer holds; from L2), those
+// of rows >= B out of range, so that each block issues the same number of
+// loads. Scales before x: the block's last HBM load then starts before the
+// x loads rather than after them. Against x before the scales, us (same
+// inputs, the two libraries alternating): M = K = 4096, B = 8 4.47 (4.57),
+// B = 16 4.92 (5.08); M = 4096, K = 11008, B = 16 9.66 (9.94); the split
+// form at M = 1024, K = 28672, B = 16 14.43 (14.84); gate/up at I = 2752,
+// H = 4096, B = 16 6.36 (6.74); within 1.3% at the other shapes timed.
 template <int RT, int kXL>
 __device__ __forceinline__ void reuse_pf_issue(uint4* __restrict__ xb, uint4* __restrict__ wb,
                                                uint4* __restrict__ sb,
@@ -1154,6 +1160,14 @@ __device__ __forceinline__ void reuse_pf_issue(uint4* __restrict__ xb, uint4* __
                                              r * (win.K / 2) + (g0 * 4 + c) * 16, 0, 0,
                                              kLoadNonTemporal);
   }
+  // Scale pairs: lane r < 16 row r of tile t.
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const __amdgpu_buffer_rsrc_t rst = rs[t];
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rst, (lds_void_ptr)(sb + 16 * t), 4,
+                                             lane < 16 ? (lane * win.Gs + g0) * 2 : kOutOfRange,
+                                             0, 0, 0);
+  }
   // x: load i covers batch rows bt0 + 2 i, bt0 + 2 i + 1, lane l chunk
   // l % 32 of row 2 i + l / 32 (chunk c = group c / 16, bytes 16 (c % 16)).
 #pragma unroll
@@ -1166,14 +1180,6 @@ __device__ __forceinline__ void reuse_pf_issue(uint4* __restrict__ xb, uint4* __
         win.bt0 + bb < win.B ? (win.bt0 + bb) * win.K * 2 + (win.gbeg + g0) * 256 + c * 16
                              : kOutOfRange,
         0, 0, 0);
-  }
-  // Scale pairs: lane r < 16 row r of tile t.
-#pragma unroll
-  for (int t = 0; t < RT; ++t) {
-    const __amdgpu_buffer_rsrc_t rst = rs[t];
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rst, (lds_void_ptr)(sb + 16 * t), 4,
-                                             lane < 16 ? (lane * win.Gs + g0) * 2 : kOutOfRange,
-                                             0, 0, 0);
   }
 }
 
