@@ -142,6 +142,43 @@ def test_kernel_stamps_are_distinct():
     assert int(ext.last_kernel_stamp()) == -1  # read-and-clear
 
 
+def test_stamp_recorded_only_for_launches():
+    """The host records the stamp when a launch succeeds: a describe call, a
+    rejected call and a call with nothing to do leave it unset, and the
+    stamp is per device (read on the current one)."""
+    import ctypes
+
+    from decode_kernel import _abi
+    from decode_kernel.quantize import quantize_and_pack
+
+    ext = _ext()
+    lib = _abi.load()
+    m, k = 512, 1024
+    packed, scales = quantize_and_pack(torch.randn(m, k, device="cuda") * 0.05)
+    x = torch.randn(1, k, device="cuda", dtype=torch.float16)
+    y = torch.empty(1, m, device="cuda", dtype=torch.float16)
+    cfg = _abi.default_config(lib)
+    stream = torch.cuda.current_stream().cuda_stream
+    ext.last_kernel_stamp()
+    assert _abi.describe(lib, m, k, 1)["launches"] == 1
+    assert int(ext.last_kernel_stamp()) == -1
+    # K not a multiple of the group size: rejected before any launch.
+    rc = lib.dk_w4a16_gemv(packed.data_ptr(), scales.data_ptr(), x.data_ptr(), y.data_ptr(), m,
+                           k - 64, 1, ctypes.byref(cfg), None, 0, stream)
+    assert rc != _abi.DK_OK
+    assert int(ext.last_kernel_stamp()) == -1
+    # B = 0: nothing to launch.
+    rc = lib.dk_w4a16_gemv(packed.data_ptr(), scales.data_ptr(), x.data_ptr(), y.data_ptr(), m, k,
+                           0, ctypes.byref(cfg), None, 0, stream)
+    assert rc == _abi.DK_OK
+    assert int(ext.last_kernel_stamp()) == -1
+    rc = lib.dk_w4a16_gemv(packed.data_ptr(), scales.data_ptr(), x.data_ptr(), y.data_ptr(), m, k,
+                           1, ctypes.byref(cfg), None, 0, stream)
+    assert rc == _abi.DK_OK
+    assert int(ext.last_kernel_stamp()) == 5
+    assert int(ext.last_kernel_stamp()) == -1
+
+
 def test_v1_multiwarp_matches_v1():
     # tests/test_correctness.py:124-142, plus every waves-per-row value.
     from decode_kernel import gemv
