@@ -104,12 +104,17 @@ struct Launch {
   hipStream_t stream;
   dk_launch_info* info = nullptr;
 
-  // After a successful launch: records `stamp` as the current device's
-  // dispatch stamp (not in describe mode). Returns rc.
+  // After a successful launch: records `stamp` as the dispatch stamp of the
+  // device the launch went to (the stream's; the current device for the
+  // null stream), not in describe mode. Returns rc.
   int stamp(int rc, int stamp) const {
     if (rc != DK_OK || info) return rc;
     int dev = 0;
-    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kStampDevices)
+    hipDevice_t sdev = 0;
+    const bool ok = stream ? hipStreamGetDevice(stream, &sdev) == hipSuccess
+                           : hipGetDevice(&dev) == hipSuccess;
+    if (stream) dev = static_cast<int>(sdev);
+    if (ok && dev >= 0 && dev < kStampDevices)
       g_stamps[dev].store(stamp + 1, std::memory_order_relaxed);
     return rc;
   }
