@@ -452,9 +452,23 @@ int launch_v5(const Launch& L, const uint4* p, const uint16_t* s, const uint4* x
 // Two batch rows stream everywhere (I = 11008: 13.38 against 12.56); three
 // take the tiles at I = 3584, H = 8192 as well (9.48 against 11.19 for the
 // streaming kernel in a later sweep).
-bool gate_up_tiles(int I, int H, int B) {
+// Up to 2048 rows, where the scales pair, the double-buffered tiles
+// (gate_up_silu_tiles_pf, I / 16 workgroups: their time barely depends on I
+// or B) take over from the streaming kernel once B I exceeds 8192; at most
+// 512 rows the streaming kernel stays to 16 batch rows. Against the
+// streaming kernel (us, H = 4096 / 8192):
+//   I = 1024, B = 8: 5.71 (5.33) / 8.77 (8.25); B = 12: 5.90 (7.48) / 9.26 (12.42)
+//   I = 1376, B = 5: 5.77 (5.56) / 8.89 (9.37); B = 8: 5.77 (7.33) / 8.90 (12.05)
+//   I = 1792, B = 5: 5.80 (6.75) / 8.92 (11.96); B = 8: 5.84 (9.01) / 9.02 (15.50)
+//   I = 2048, B = 5: 5.88 (7.00) / 8.94 (12.42); B = 8: 5.87 (9.33) / 9.03 (15.71)
+//   I = 512, B = 16: 6.03 (5.40) / 9.89 (8.31)
+// (3-4 batch rows stream at every I up to 2048: I = 2048, B = 4 5.73 against
+// 5.37 at H = 4096.) Where the scales do not pair the earlier rule holds.
+bool gate_up_tiles(int I, int H, int B, bool pairs) {
   (void)H;
-  return !(B <= 2 || (B <= 8 && I <= 2048) || (B <= 16 && I <= 1024));
+  if (B <= 2) return false;
+  if (pairs && I > 512 && I <= 2048 && B <= 16) return (long long)B * I > 8192;
+  return !((B <= 8 && I <= 2048) || (B <= 16 && I <= 1024));
 }
 
 // Fused gate/up, R rows of each matrix per wave, on the LDS stage loop (U
@@ -502,9 +516,9 @@ int launch_gate_up_lds_t(const Launch& L, const uint4* g, const uint16_t* gs, co
   launch_gate_up_lds_t<R, U, W, PF, NB>(L, g, gs, u, us, x, h, I, H, B)
 int launch_gate_up(const Launch& L, const uint4* g, const uint16_t* gs, const uint4* u,
                    const uint16_t* us, const uint4* x, uint16_t* h, int I, int H, int B) {
-  if (gate_up_tiles(I, H, B)) {
+  const bool pairs = (H / DK_GROUP_SIZE) % 2 == 0 && aligned(gs, 4) && aligned(us, 4);
+  if (gate_up_tiles(I, H, B, pairs)) {
     const dim3 grid((I + 15) / 16, (B + dk::kReuseBatch - 1) / dk::kReuseBatch);
-    const bool pairs = (H / DK_GROUP_SIZE) % 2 == 0 && aligned(gs, 4) && aligned(us, 4);
     // From 8 batch rows, both tiles' operands staged in LDS (as the GEMV's
     // gemv_reuse_lds), 8 waves up to I = 4096 and 16 batch rows, else 4
     // (us, against the tiles that load the operands directly):

@@ -96,7 +96,7 @@ def test_mlp_step_matches_oracle(i, h, b):
 # 8192, above) the gate/up dispatch tells apart.
 GATE_UP_SHAPES = [(1000, 4224), (2000, 8320), (3000, 4224), (3000, 8320), (5000, 4224),
                   (4500, 8320), (1800, 6144), (700, 3968), (5000, 5120), (2752, 4096),
-                  (3000, 6144)]
+                  (3000, 6144), (1000, 4096), (600, 8192), (1376, 8192)]
 
 
 @pytest.mark.parametrize("i,h", GATE_UP_SHAPES)
@@ -106,9 +106,11 @@ def test_gate_up_every_dispatch_class(i, h):
     # I > 2048, and from 9 rows at I > 1024, the MFMA tiles run instead (with
     # both operands staged in LDS from 8 rows, double buffered at 9-16 rows
     # up to I = 4096 where the scales pair: I = 1800, 2752 and 3000, and
-    # below 9 rows with four x loads per block at I = 2752 and 3000). Each
-    # output row depends on its own activation row only, so the first b rows
-    # of one 16-row case give the reference for every b.
+    # below 9 rows with four x loads per block at I = 2752 and 3000). Where
+    # the scales pair at 513-2048 rows the double-buffered tiles run once
+    # B I > 8192: I = 1800 from 5 rows, I = 1376 from 6, I = 1000 from 9,
+    # I = 600 at 16. Each output row depends on its own activation row only,
+    # so the first b rows of one 16-row case give the reference for every b.
     from decode_kernel import _cuda, gate_up_silu
 
     (gp, gs, up, us, _, _), (ngp, ngs, nup, nus, _, _) = _weights(i, h, seed=i + h)
