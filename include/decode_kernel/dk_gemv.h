@@ -183,7 +183,9 @@ int dk_unpack_paired(const uint32_t* paired, uint32_t* packed, int M, int K,
                      hipStream_t stream);
 
 /* The v5 GEMV on paired weights (stamp DK_STAMP_PAIRED); arguments, checks
- * and results as dk_w4a16_gemv with the default configuration. */
+ * and results as dk_w4a16_gemv with the default configuration (a batch runs
+ * the v5 kernel's batch tiles; the weight-reuse MFMA tiles read the API
+ * layout only). */
 int dk_w4a16_gemv_paired(const uint32_t* paired, const uint16_t* scales,
                          const uint16_t* x, uint16_t* y, int M, int K, int B,
                          hipStream_t stream);
