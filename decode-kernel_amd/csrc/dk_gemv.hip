@@ -766,11 +766,19 @@ struct PfShape {
 // at 4097+ rows and from 9 above 8192 rows, and at M <= 1024 above 32
 // batch rows (three batch tiles) on rows shorter than 16384 weights
 // (M = 512, K = 8192, B = 33: 6.40 against 6.71).
+// Above 8192 rows, two tiles per wave from 12289 rows, one below (an
+// earlier rule took two tiles on rows longer than 4096 weights and one
+// otherwise; us, against it in brackets):
+//   M = 9216, K = 8192, B = 5: 13.54 (14.84)   M = 11008, K = 8192, B = 5: 13.87 (15.01)
+//   M = 12288, K = 8192, B = 8: 15.53 (16.23)  M = 14336, K = 4096, B = 8: 9.45 (10.29)
+//   M = 16384, K = 4096, B = 8: 9.60 (10.65)   M = 28672, K = 4096, B = 8: 15.59 (16.78)
+//   M = 14336, K = 8192, B = 4: 14.74 (16.04)  M = 28672, K = 8192, B = 4: 25.90 (26.69)
+// (M = 28672 and 14336 at K = 8192, B = 5-8 keep two tiles.)
 PfShape reuse_pf_shape(int M, int K, int B) {
   if (M > 8192) {
     if (B > 8) return {};
-    if (B <= 4) return {4, 1, 2};
-    return K > 4096 ? PfShape{4, 2, 4} : PfShape{4, 1, 4};
+    const int rt = M > 12288 ? 2 : 1;
+    return {4, rt, B <= 4 ? 2 : 4};
   }
   if (M > 4096) {
     if (B >= 9 && B <= 16 && K >= 8192) return {4, 2, 8};
@@ -833,9 +841,11 @@ int launch_reuse_tiles(const Launch& L, const uint4* p, const uint16_t* s, const
       if (pf.xl == 4) return launch_reuse_pf<4, 1, 4>(L, p, s, x, y, M, K, B);
       return launch_reuse_pf<4, 1, 8>(L, p, s, x, y, M, K, B);
     }
-    if (pf.ks == 4 && pf.rt == 2)
+    if (pf.ks == 4 && pf.rt == 2) {
+      if (pf.xl == 2) return launch_reuse_pf<4, 2, 2>(L, p, s, x, y, M, K, B);
       return pf.xl == 8 ? launch_reuse_pf<4, 2, 8>(L, p, s, x, y, M, K, B)
                         : launch_reuse_pf<4, 2, 4>(L, p, s, x, y, M, K, B);
+    }
   }
   if (M > 2048 && M <= 4096 && K <= 4096 && B <= 5)
     return launch_reuse<8, 1, 2>(L, p, s, x, y, M, K, B);
@@ -932,7 +942,16 @@ enum class ReuseShape { kStream, kTiles };
 // double-buffered tiles need pairs of groups; the single-buffered ones
 // were level with the streaming kernel: M = 2048, K = 4096, B = 8 4.65
 // against 4.68).
-ReuseShape reuse_shape(int M, int K, int B) {
+// Where the groups pair (`pairs`: an even group count and 4-byte aligned
+// scales), the double-buffered tiles also take two batch rows above 12288
+// rows and three at 4097-8191 rows on rows of up to 4096 weights, found by
+// timing them at shapes the streaming kernel kept (us, streaming in
+// brackets): B = 2, M = 14336, K = 8192 14.30 (15.63); M = 16384, K = 4096
+// 8.45 (9.75); M = 13824, K = 5120 9.94 (11.83); M = 28672, K = 8192 25.00
+// (25.80); B = 3 at K = 2048 / 3072 / 4096, M = 6144: 4.14 / 4.90 / 5.62
+// (5.95 / 6.12 / 6.21), M = 4608 and 7168 alike.
+ReuseShape reuse_shape(int M, int K, int B, bool pairs) {
+  if (B == 2 && pairs && M > 12288) return ReuseShape::kTiles;
   if (B <= 2 || M <= 128) return ReuseShape::kStream;
   if (M <= 512) return B <= 32 ? ReuseShape::kStream : ReuseShape::kTiles;
   if (M <= 1024) return B < 12 ? ReuseShape::kStream : ReuseShape::kTiles;
@@ -940,7 +959,8 @@ ReuseShape reuse_shape(int M, int K, int B) {
     return ReuseShape::kStream;
   if (B == 3) {
     const bool tiles = K >= 8192 || M >= 8192 || (size_t)M * (size_t)K >= ((size_t)1 << 27) ||
-                       (M >= 3072 && K > 4096 && K < 8192) || (M > 2048 && M <= 4096 && K <= 4096);
+                       (M >= 3072 && K > 4096 && K < 8192) || (M > 2048 && M <= 4096 && K <= 4096) ||
+                       (pairs && M > 4096 && K <= 4096);
     return tiles ? ReuseShape::kTiles : ReuseShape::kStream;
   }
   return ReuseShape::kTiles;
@@ -961,7 +981,7 @@ ReuseShape reuse_shape(int M, int K, int B) {
 // and single-pass where it lost: M = 1024, K = 28672, B = 33: 18.27 (S = 2
 // 24.18); M = 1024, K = 14336, B = 16: 11.44 (S = 2 11.32, S = 4 12.13).
 int reuse_split_slices(int M, int K, int B) {
-  if (reuse_shape(M, K, B) != ReuseShape::kTiles || M > 1024) return 0;
+  if (reuse_shape(M, K, B, false) != ReuseShape::kTiles || M > 1024) return 0;
   const long long tiles = (long long)((M + 15) / 16) * ((B + dk::kReuseBatch - 1) / dk::kReuseBatch);
   if (tiles <= 64 && K >= 28672) return 4;
   if (tiles <= 64 && K >= 16384) return 2;
@@ -1008,7 +1028,8 @@ int gemv_impl(const uint32_t* packed, const uint16_t* scales, const uint16_t* x,
   const uint4* x4 = reinterpret_cast<const uint4*>(x);
 
   if (cfg->reuse_weights) {
-    if (reuse_shape(M, K, B) == ReuseShape::kStream)
+    const bool pairs = (K / DK_GROUP_SIZE) % 2 == 0 && aligned(scales, 4);
+    if (reuse_shape(M, K, B, pairs) == ReuseShape::kStream)
       return L.stamp(launch_v5<dk::LayoutLogical, DK_STAMP_REUSE>(L, p4, scales, x4, y, M, K, B),
                      DK_STAMP_REUSE);
     if (split)

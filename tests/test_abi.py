@@ -191,7 +191,15 @@ ROUTES = [
     ((2048, 4224, 8), dict(reuse_weights=1), "dk::gemv_v5_lds<1, 1, 16, 4, true, dk::LayoutLogical, 15,",
      [128, 2, 1]),
     ((2560, 8192, 4), dict(reuse_weights=1), "dk::gemv_reuse_pf<8, 1, 4>", [160, 1, 1]),
-    ((28672, 8192, 4), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1, 2>", [1792, 1, 1]),
+    ((28672, 8192, 4), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 2, 2>", [896, 1, 1]),
+    ((28672, 8192, 2), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 2, 2>", [896, 1, 1]),
+    ((12288, 8192, 2), dict(reuse_weights=1), "dk::gemv_v5_lds<2, 2, 8, 2, false, dk::LayoutLogical, 15,",
+     [768, 1, 1]),
+    ((12288, 8192, 5), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1, 4>", [768, 1, 1]),
+    ((12416, 8192, 5), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 2, 4>", [388, 1, 1]),
+    ((6144, 4096, 3), dict(reuse_weights=1), "dk::gemv_reuse_lds<8, 2, true, 2>", [192, 1, 1]),
+    ((6144, 3968, 3), dict(reuse_weights=1), "dk::gemv_v5_lds<2, 2, 8, 3, false, dk::LayoutLogical, 15,",
+     [384, 1, 1]),
     ((28672, 8320, 4), dict(reuse_weights=1), "dk::gemv_reuse<8, 2, 2, false>", [896, 1, 1]),
     ((28672, 8192, 16), dict(reuse_weights=1), "dk::gemv_reuse_lds<4, 2, true, 2>", [896, 1, 1]),
     ((11008, 4096, 4), dict(reuse_weights=1), "dk::gemv_reuse_pf<4, 1, 2>", [688, 1, 1]),

@@ -139,9 +139,11 @@ def test_batch_sweep_c3(batch):
 
 
 def test_reuse_small_batches_run_the_streaming_kernel():
-    # Up to two batch rows; three below 2^27 weights with rows shorter than
-    # 8192 weights below 8192 rows (but not rows of 4097-8191 weights at
-    # M >= 3072, nor rows of up to 4096 at 2049-4096 rows); four at
+    # Up to two batch rows (but not above 12288 rows where the groups pair);
+    # three below 2^27 weights with rows shorter than 8192 weights below 8192
+    # rows (but not rows of 4097-8191 weights at M >= 3072, nor rows of up to
+    # 4096 above 2048 rows, where the groups pair: M = 6000, K = 3968 has an
+    # odd group count); four at
     # M <= 2048; up to 8 at M <= 2048 on rows shorter than 8192 weights with
     # an odd number of groups; 11 at M <= 1024, 32 at M <= 512 and any at
     # M <= 128: the
@@ -151,7 +153,8 @@ def test_reuse_small_batches_run_the_streaming_kernel():
     from decode_kernel import _abi, _cuda
 
     for (m, k, b) in [(4096, 4096, 1), (4096, 4096, 2), (11008, 4096, 2), (300, 8192, 1),
-                      (512, 8192, 2), (6000, 4096, 3), (28672, 8192, 2), (1500, 4096, 3),
+                      (512, 8192, 2), (6000, 3968, 3), (28672, 8320, 2), (12288, 8192, 2),
+                      (1500, 4096, 3),
                       (2000, 8192, 4), (512, 8320, 3), (1024, 11008, 6), (1024, 4224, 11),
                       (2048, 4224, 8), (40, 197632, 3), (500, 4224, 32),
                       (100, 8192, 64)]:
@@ -168,12 +171,15 @@ def test_reuse_small_batches_run_the_streaming_kernel():
     _check_against_oracle(y, oracle.linear_f64(x, packed, scales), "reuse 3000x8320 B=5")
     # Where the LDS-staged tiles beat the streaming kernel at small batches:
     # three rows of 8192 weights or more (or from 8192 rows, or up to 4096
-    # at 2049-4096 rows), four above 2048 rows, 12 rows at M <= 1024, five
-    # rows at M <= 2048 (any length where the groups pair).
+    # at 2049-4096 rows, or up to 4096 above 4096 rows where the groups
+    # pair), four above 2048 rows, 12 rows at M <= 1024, five rows at
+    # M <= 2048 (any length where the groups pair), two above 12288 rows
+    # where the groups pair.
     lib = _abi.load()
     for (m, k, b) in [(8192, 8192, 3), (4096, 11008, 3), (1000, 4224, 12), (2048, 8192, 5),
                       (3000, 8192, 4), (11008, 4096, 3), (4096, 4096, 3), (2048, 4096, 6),
-                      (8192, 3584, 3)]:
+                      (8192, 3584, 3), (6000, 4096, 3), (4608, 2048, 3), (28672, 8192, 2),
+                      (14336, 4096, 2)]:
         name = _abi.describe(lib, m, k, b, reuse_weights=1)["kernel"]
         assert "gemv_reuse_lds<" in name or "gemv_reuse_pf<" in name, (m, k, b)
 
@@ -188,7 +194,9 @@ def test_reuse_small_batches_run_the_streaming_kernel():
                                    (4096, 4096, 4), (3000, 4096, 5), (2000, 16512, 13),
                                    (1500, 8320, 9), (4100, 8192, 12), (4096, 11008, 32),
                                    (1000, 16384, 33), (2040, 8192, 20), (1500, 8192, 7),
-                                   (4500, 8192, 8), (9000, 8192, 7), (11008, 4096, 3)])
+                                   (4500, 8192, 8), (9000, 8192, 7), (11008, 4096, 3),
+                                   (14336, 8192, 2), (13900, 5120, 4), (6144, 4096, 3),
+                                   (11008, 8192, 5), (16384, 4096, 8)])
 def test_reuse_tile_kernel_exact_properties(m, k, b):
     # The single-pass MFMA tile kernels in each of their shapes (operands
     # staged in LDS: one tile per wave with 16 or 8 waves, two tiles per wave
@@ -198,7 +206,10 @@ def test_reuse_tile_kernel_exact_properties(m, k, b):
     # M = 1000 and two, the second partial, at M = 2040, and with four x
     # loads per block up to 8 batch rows, one tile per wave of 6 up to 4096
     # rows (M = 3000 partial) and two per wave of 4 above (M = 4500 and 9000
-    # ending in partial pairs of tiles); operands
+    # ending in partial pairs of tiles); above 8192 rows one tile per wave up
+    # to 12288 rows (M = 11008, B = 5) and two above, with two x loads per
+    # block up to 4 batch rows (M = 14336 at B = 2, M = 13900 ending in a
+    # partial pair of tiles); three rows at M = 6144 on rows of 4096; operands
     # loaded directly: M > 8192 with rows longer than 4096 weights up to 8
     # batch rows; the split form is test_reuse_split_tiles), three and four
     # batch rows on the shapes that take the tiles there, long rows of 512
