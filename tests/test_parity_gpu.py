@@ -10,6 +10,8 @@
   repeated launches are bit-identical (including split-K).
 * Edge shapes: M = 1 and M not a multiple of any tile, one group (K = 128),
   K not a power of two, batch sizes around the tile widths, K = 0, M = 0.
+* 40 seeded random shapes across the dispatch's whole range (27 distinct
+  kernels), with arbitrary weight words, against the oracle's tight bound.
 * The committed golden fixtures through the GPU.
 * Direct calls through the C ABI (ctypes) agree bit-for-bit with the
   extension, and the STREAM probes compute what they claim.
@@ -93,6 +95,18 @@ def _assert_doubles(y2: torch.Tensor, y1: torch.Tensor, label: str):
     assert diff.numel() == 0 or float(diff.max()) <= 2.0 ** -23, f"{label}: subnormal y(2x)"
 
 
+def _device_random(m: int, k: int, b: int, seed: int):
+    """Arbitrary weight words (every nibble value), scales in [0.0005, 0.004]
+    and N(0, 1) activations, drawn on the GPU: for comparisons between two
+    kernels, which need no oracle and no quantizer."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    packed = torch.randint(-(1 << 31), (1 << 31) - 1, (m, k // 8), dtype=torch.int32,
+                           device="cuda", generator=gen)
+    scales = (torch.rand(m, k // 128, device="cuda", generator=gen) * 0.0035 + 0.0005).half()
+    x = torch.randn(b, k, device="cuda", generator=gen).half()
+    return packed, scales, x
+
+
 _CASES = {}
 
 
@@ -158,8 +172,7 @@ def test_reuse_small_batches_run_the_streaming_kernel():
                       (2000, 8192, 4), (512, 8320, 3), (1024, 11008, 6), (1024, 4224, 11),
                       (2048, 4224, 8), (40, 197632, 3), (500, 4224, 32),
                       (100, 8192, 64)]:
-        w, x = oracle.make_case(m, k, b, seed=m + k + b)
-        _, _, pd, sd, xd = _upload(w, x)
+        pd, sd, xd = _device_random(m, k, b, seed=m + k + b)
         y_reuse = _gemv(pd, sd, xd, version=5, reuse_weights=True)
         assert int(_cuda.last_kernel_stamp()) == 15
         y_v5 = _gemv(pd, sd, xd, version=5)
@@ -563,6 +576,53 @@ def test_every_dispatch_class(m, k):
         # Batch rows are independent of their position in the batch: the
         # reversed batch gives the reversed outputs bit for bit.
         assert torch.equal(_gemv(pd, sd, xd.flip(0).contiguous(), version=5), y.flip(0))
+
+
+def _random_shapes(n: int, seed: int) -> list:
+    """n shapes (M, K, B) drawn across the dispatch's whole range: M
+    log-uniform in 16..24576, K = 128 g with g log-uniform in 1..256, B from
+    batch widths either side of every tile boundary, M K <= 2**24 so the
+    oracle stays quick. The seed below gives 27 distinct kernels."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    batches = [1, 2, 3, 4, 5, 6, 8, 9, 12, 16, 17, 24, 32, 33, 48, 64]
+    out = []
+    while len(out) < n:
+        m = int(np.exp(rng.uniform(np.log(16.0), np.log(24576.0))))
+        k = 128 * int(np.exp(rng.uniform(0.0, np.log(256.0))))
+        if m * k > (1 << 24):
+            continue
+        out.append((m, k, int(rng.choice(batches))))
+    return out
+
+
+@pytest.mark.parametrize("m,k,b", _random_shapes(40, seed=20261202))
+def test_random_shapes_against_oracle(m, k, b):
+    """Shapes off every sweep and route boundary, with arbitrary weight words
+    (every nibble value, -8 included) and scales, through the streaming
+    kernel, the weight-reuse path and (one batch row) the split kernel: the
+    oracle's tight bound and bit-identical repeats. Each failure names the
+    kernel that ran."""
+    from decode_kernel import _abi
+
+    lib = _abi.load()
+    rng = np.random.Generator(np.random.PCG64(m * 131071 + k * 17 + b))
+    packed = rng.integers(0, 1 << 32, size=(m, k // 8), dtype=np.uint64).astype(np.uint32)
+    packed = packed.view(np.int32)
+    scales = rng.uniform(0.0005, 0.004, size=(m, k // 128)).astype(np.float16)
+    x = rng.standard_normal((b, k), dtype=np.float32).astype(np.float16)
+    pd, sd, xd = (torch.from_numpy(a).cuda() for a in (packed, scales, x))
+    y_ref = oracle.linear_f64(x, packed, scales)
+    paths = [("v5", dict(version=5)), ("reuse", dict(reuse_weights=True))]
+    if b == 1:
+        paths.append(("v4", dict(version=4, split_k=4)))
+    for label, kw in paths:
+        kern = _abi.describe(lib, m, k, b, reuse_weights=int(kw.get("reuse_weights", False)),
+                             version=kw.get("version", 5), split_k=kw.get("split_k", 4))["kernel"]
+        tag = f"{label} {m}x{k} B={b} ({kern.split('(')[0]})"
+        print(f"[random] {tag}", flush=True)
+        y = _gemv(pd, sd, xd, **kw)
+        _check_against_oracle(y, y_ref, tag)
+        assert torch.equal(_gemv(pd, sd, xd, **kw), y), f"{tag}: repeat differs"
 
 
 def test_empty_dimensions():
