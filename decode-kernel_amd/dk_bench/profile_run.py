@@ -8,7 +8,7 @@ Runs, each after a 1 GiB read-only flush so every launch starts cold:
   * `--reps` launches of each GEMV variant at each benchmark configuration
     (comma-separated lists), or of another operation on the path (the MLP
     step, the paired-layout GEMV, the device quantizer:
-    `--config mlp7b|mlp70b|paired_c0|paired_c4b|quant_c4a`). Variants
+    `--config mlp7b|mlp70b|mlp70b_tp8|mlp70b_tp8_b8|paired_c0|paired_c4b|quant_c4a`). Variants
     `no_decode` and `loads_only` run the kernel the product dispatches at one
     batch row with the ablation maths of dk_bench/libdk_bench.so (the same
     loads; the decode replaced, or the decode and the activation reads from
@@ -44,7 +44,7 @@ ABLATIONS = {"no_decode": 1, "loads_only": 2}
 COPY_BYTES = 64 << 20
 
 
-def _mlp(i: int, h: int):
+def _mlp(i: int, h: int, b: int = 1):
     def run(reps, flush):
         import torch
 
@@ -54,7 +54,7 @@ def _mlp(i: int, h: int):
         ws = []
         for shape in ((i, h), (i, h), (h, i)):
             ws += list(quantize_and_pack(torch.randn(*shape, device="cuda", generator=gen) * 0.02))
-        x = torch.randn(1, h, device="cuda", generator=gen).half()
+        x = torch.randn(b, h, device="cuda", generator=gen).half()
         for _ in range(reps):
             flush()
             mlp_decode(x, *ws)
@@ -89,8 +89,10 @@ def _quant(reps, flush):
 
 
 # Other operations on the path, by name: the MLP step at the Llama-7B and
-# 70B shapes, the paired-layout GEMV at c0 and c4b, the device quantizer.
+# 70B shapes and at the 70B TP = 8 shard (one and eight batch rows), the
+# paired-layout GEMV at c0 and c4b, the device quantizer.
 OTHER_OPS = {"mlp7b": _mlp(11008, 4096), "mlp70b": _mlp(28672, 8192),
+             "mlp70b_tp8": _mlp(3584, 8192), "mlp70b_tp8_b8": _mlp(3584, 8192, 8),
              "paired_c0": _paired(4096, 4096), "paired_c4b": _paired(8192, 28672),
              "quant_c4a": _quant}
 
