@@ -767,8 +767,9 @@ struct PfShape {
 // batch rows (three batch tiles) on rows shorter than 16384 weights
 // (M = 512, K = 8192, B = 33: 6.40 against 6.71).
 // Above 8192 rows, two tiles per wave from 12289 rows, one below (an
-// earlier rule took two tiles on rows longer than 4096 weights and one
-// otherwise; us, against it in brackets):
+// earlier rule, the one the table above was timed with, took two tiles on
+// rows longer than 4096 weights and one otherwise; us, against it in
+// brackets):
 //   M = 9216, K = 8192, B = 5: 13.54 (14.84)   M = 11008, K = 8192, B = 5: 13.87 (15.01)
 //   M = 12288, K = 8192, B = 8: 15.53 (16.23)  M = 14336, K = 4096, B = 8: 9.45 (10.29)
 //   M = 16384, K = 4096, B = 8: 9.60 (10.65)   M = 28672, K = 4096, B = 8: 15.59 (16.78)
