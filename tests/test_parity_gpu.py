@@ -500,10 +500,11 @@ def test_edge_shapes_all_paths(m, k, batch):
         assert err < MAX_ABS, (label, m, k, batch, err)
 
 
-@pytest.mark.parametrize("batch", [64, 257])
+@pytest.mark.parametrize("batch", [64, 257, 1000])
 def test_large_batches_all_paths(batch):
-    # Many batch tiles on every path: 17 tiles of 16 rows on the MFMA path,
-    # 65-129 tiles of 2-4 rows on the streaming path.
+    # Many batch tiles on every path: up to 63 tiles of 16 rows on the MFMA
+    # path (the single-buffered tiles: 9 groups per row do not pair), up to
+    # 500 tiles of 2-4 rows on the streaming path.
     m, k = 300, 1152
     w, x = oracle.make_case(m, k, batch, seed=batch, w_std=0.05)
     packed, scales, pd, sd, xd = _upload(w, x)
